@@ -1,0 +1,332 @@
+"""daiza_amd — MI355X (gfx950) Q1_0 batch-1 decode behind a C ABI.
+
+Python mirror of the reference interface for this path (guang384/Daiza, Daiza-engine):
+  Q1_0Matrix      -> Daiza-engine/src/model/weights.rs:83-1208
+  Config          -> Daiza-engine/src/model/config.rs:12-76
+  Model / Context -> LoadedWeights + ForwardContext (weights.rs:1308, forward.rs:32-131)
+Everything calls libdaiza_hip.so (include/daiza_hip.h) through ctypes; there is no CPU
+fallback: if the library or a gfx950 device is missing, calls raise DaizaError.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "libdaiza_hip.so")
+
+DZ_OK = 0
+DZ_ERR_TENSOR = -1
+DZ_ERR_MODEL = -2
+DZ_ERR_UNSUPPORTED = -3
+DZ_ERR_DEVICE = -4
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_vp = ctypes.c_void_p
+
+
+class DaizaError(RuntimeError):
+    """BonsaiError counterpart (Daiza-engine/src/lib.rs:42-78): code is the DZ_ERR_* status."""
+
+    def __init__(self, code, msg):
+        super().__init__("%s (%d): %s" % ({-1: "Tensor", -2: "Model", -3: "Unsupported", -4: "Device"}.get(code, "Error"),
+                                          code, msg))
+        self.code = code
+
+
+class Config(ctypes.Structure):
+    """dz_config; field meaning follows Config (config.rs:12-76)."""
+
+    _fields_ = [
+        ("n_layers", ctypes.c_int32), ("hidden", ctypes.c_int32), ("ffn", ctypes.c_int32),
+        ("vocab", ctypes.c_int32), ("n_head", ctypes.c_int32), ("n_head_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("rope_dim", ctypes.c_int32), ("rope_base", ctypes.c_float),
+        ("rms_eps", ctypes.c_float), ("full_attn_interval", ctypes.c_int32), ("ssm_conv_kernel", ctypes.c_int32),
+        ("ssm_state", ctypes.c_int32), ("ssm_k_heads", ctypes.c_int32), ("ssm_v_heads", ctypes.c_int32),
+        ("embd_f16", ctypes.c_int32), ("max_ctx", ctypes.c_int32),
+    ]
+
+    @classmethod
+    def bonsai27b(cls, max_ctx=4096):
+        """Config::default (config.rs:47-76) with an f16 embedding."""
+        return cls(n_layers=64, hidden=5120, ffn=17408, vocab=248320, n_head=24, n_head_kv=4, head_dim=256,
+                   rope_dim=64, rope_base=1.0e7, rms_eps=1e-6, full_attn_interval=4, ssm_conv_kernel=4,
+                   ssm_state=128, ssm_k_heads=16, ssm_v_heads=48, embd_f16=1, max_ctx=max_ctx)
+
+    @classmethod
+    def small(cls, n_layers=4, max_ctx=256, **kw):
+        """A reduced hybrid stack with the same per-head shapes, for fast parity tests."""
+        c = cls(n_layers=n_layers, hidden=512, ffn=1024, vocab=2048, n_head=4, n_head_kv=2, head_dim=256,
+                rope_dim=64, rope_base=1.0e7, rms_eps=1e-6, full_attn_interval=4, ssm_conv_kernel=4,
+                ssm_state=128, ssm_k_heads=2, ssm_v_heads=6, embd_f16=1, max_ctx=max_ctx)
+        for k, v in kw.items():
+            setattr(c, k, v)
+        return c
+
+    def is_full_attention(self, i):
+        """Config::is_full_attention_block (config.rs:161-167)."""
+        if self.full_attn_interval == 0:
+            return True
+        return i % self.full_attn_interval == self.full_attn_interval - 1
+
+    @property
+    def qkv_dim(self):
+        return (2 * self.ssm_k_heads + self.ssm_v_heads) * self.ssm_state
+
+
+_lib = None
+
+
+def lib():
+    """Load libdaiza_hip.so (built by daiza_amd.build); raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise DaizaError(DZ_ERR_DEVICE, "libdaiza_hip.so not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    L.dz_last_error.restype = ctypes.c_char_p
+    L.dz_device_init.argtypes = [ctypes.c_int]
+    L.dz_q1_0_upload.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(_vp)]
+    L.dz_q1_0_free.argtypes = [_vp]
+    L.dz_q1_0_shape.argtypes = [_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+    L.dz_q1_0_matvec.argtypes = [_vp, _f32p, _f32p, ctypes.c_int]
+    L.dz_q1_0_matvec_multi.argtypes = [ctypes.POINTER(_vp), ctypes.c_int, _f32p, ctypes.POINTER(_f32p)]
+    L.dz_q1_0_matvec_dev.argtypes = [_vp, _vp, _vp, ctypes.c_int, _vp]
+    L.dz_q1_0_dequant_rows.argtypes = [_vp, ctypes.c_size_t, ctypes.c_size_t, _f32p]
+    for name, args in _MODEL_PROTOS.items():
+        fn = getattr(L, name, None)
+        if fn is not None:
+            fn.argtypes = args[0]
+            fn.restype = args[1]
+    _lib = L
+    return L
+
+
+_MODEL_PROTOS = {
+    "dz_config_bonsai27b": ([_vp, ctypes.c_int32], None),
+    "dz_model_create_synth": ([_vp, ctypes.c_uint64, ctypes.POINTER(_vp)], ctypes.c_int),
+    "dz_model_free": ([_vp], ctypes.c_int),
+    "dz_model_weight_bytes": ([_vp, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "dz_ctx_create": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
+    "dz_ctx_free": ([_vp], ctypes.c_int),
+    "dz_ctx_reset": ([_vp], ctypes.c_int),
+    "dz_ctx_pos": ([_vp], ctypes.c_int),
+    "dz_forward_token": ([_vp, ctypes.c_uint32, _f32p, _u32p], ctypes.c_int),
+    "dz_forward_batch": ([_vp, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p], ctypes.c_int),
+    "dz_decode_greedy": ([_vp, ctypes.c_uint32, ctypes.c_int, _u32p], ctypes.c_int),
+    "dz_ctx_logits": ([_vp, _f32p], ctypes.c_int),
+    "dz_ctx_set_ssm_state": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.c_int], ctypes.c_int),
+    "dz_ctx_get_ssm_state": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "dz_ctx_set_kv": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.c_int], ctypes.c_int),
+    "dz_ctx_get_kv": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.c_int], ctypes.c_int),
+    "dz_ctx_kv_len": ([_vp, ctypes.c_int], ctypes.c_int),
+    "dz_kv_truncate": ([_vp, ctypes.c_int], ctypes.c_int),
+    "dz_ctx_set_pos": ([_vp, ctypes.c_int], ctypes.c_int),
+    "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
+    "dz_ctx_stream": ([_vp], _vp),
+}
+
+EXPORTED_SYMBOLS = [
+    "dz_config_bonsai27b", "dz_last_error", "dz_device_init",
+    "dz_q1_0_upload", "dz_q1_0_free", "dz_q1_0_shape", "dz_q1_0_matvec", "dz_q1_0_matvec_multi",
+    "dz_q1_0_matvec_dev", "dz_q1_0_dequant_rows",
+] + list(k for k in _MODEL_PROTOS if k != "dz_config_bonsai27b")
+
+
+def _check(rc):
+    if rc != DZ_OK:
+        raise DaizaError(rc, lib().dz_last_error().decode(errors="replace"))
+
+
+def _f(a):
+    return a.ctypes.data_as(_f32p)
+
+
+class Q1_0Matrix:
+    """Device-resident Q1_0 matrix (Q1_0Matrix, weights.rs:83-1208).
+
+    `aos` is the reference byte layout: per row, cols/128 blocks of [f16 scale LE | 16 sign bytes].
+    """
+
+    def __init__(self, aos, rows, cols):
+        aos = np.ascontiguousarray(aos, dtype=np.uint8)
+        if aos.size != rows * (cols // 128) * 18:
+            raise DaizaError(DZ_ERR_TENSOR, "byte count %d does not match %dx%d Q1_0" % (aos.size, rows, cols))
+        self.rows, self.cols = int(rows), int(cols)
+        h = _vp()
+        _check(lib().dz_q1_0_upload(aos.ctypes.data_as(_u8p), rows, cols, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().dz_q1_0_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def matvec_into_slice(self, x, y):
+        """y = W x (weights.rs:123-325)."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.size == self.cols and y.size == self.rows and y.dtype == np.float32 and y.flags.c_contiguous
+        _check(lib().dz_q1_0_matvec(self._h, _f(x), _f(y), 0))
+
+    def matvec_add_into_slice(self, x, y):
+        """y += W x (weights.rs:334-465)."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.size == self.cols and y.size == self.rows and y.dtype == np.float32 and y.flags.c_contiguous
+        _check(lib().dz_q1_0_matvec(self._h, _f(x), _f(y), 1))
+
+    def matvec(self, x):
+        y = np.empty(self.rows, np.float32)
+        self.matvec_into_slice(x, y)
+        return y
+
+    @staticmethod
+    def matvec_multi_into_slice(x, matrices, outputs):
+        """Several matrices sharing x in one pass (weights.rs:831-972)."""
+        n = len(matrices)
+        x = np.ascontiguousarray(x, np.float32)
+        hs = (_vp * n)(*[m._h for m in matrices])
+        ys = (_f32p * n)(*[_f(o) for o in outputs])
+        _check(lib().dz_q1_0_matvec_multi(hs, n, _f(x), ys))
+
+    def row_into_slice(self, row, y):
+        """Dequantised row (weights.rs:106 -> quant.rs:161-194)."""
+        _check(lib().dz_q1_0_dequant_rows(self._h, row, 1, _f(y)))
+
+    def dequant_rows(self, r0, n):
+        out = np.empty((n, self.cols), np.float32)
+        _check(lib().dz_q1_0_dequant_rows(self._h, r0, n, _f(out)))
+        return out
+
+
+class Model:
+    """Device-resident weights (LoadedWeights, weights.rs:1308-1379)."""
+
+    def __init__(self, cfg, seed=None, tensors=None):
+        self.cfg = cfg
+        h = _vp()
+        if tensors is None:
+            _check(lib().dz_model_create_synth(ctypes.byref(cfg), int(seed), ctypes.byref(h)))
+        else:
+            raise DaizaError(DZ_ERR_UNSUPPORTED, "named-tensor loading is exposed through the C ABI only")
+        self._h = h
+
+    @classmethod
+    def synthetic(cls, cfg, seed):
+        """Random Q1_0 model from the daiza_synth.h generator (BASELINE config 4 at Bonsai shape)."""
+        return cls(cfg, seed=seed)
+
+    def q1_bytes(self):
+        v = ctypes.c_uint64()
+        _check(lib().dz_model_weight_bytes(self._h, ctypes.byref(v)))
+        return v.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().dz_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Context:
+    """ModelState + ForwardContext (forward.rs:32-131) on the device."""
+
+    def __init__(self, model):
+        self.model = model
+        self.cfg = model.cfg
+        h = _vp()
+        _check(lib().dz_ctx_create(model._h, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().dz_ctx_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def pos(self):
+        return lib().dz_ctx_pos(self._h)
+
+    def reset(self):
+        _check(lib().dz_ctx_reset(self._h))
+
+    def set_pos(self, pos):
+        _check(lib().dz_ctx_set_pos(self._h, int(pos)))
+
+    def forward_single_token(self, token, want_logits=True):
+        """forward.rs:204; returns (argmax, logits or None)."""
+        am = ctypes.c_uint32()
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        _check(lib().dz_forward_token(self._h, int(token), _f(logits) if want_logits else None, ctypes.byref(am)))
+        return am.value, logits
+
+    def forward_batch(self, ids, per_pos_logits=False):
+        """forward.rs:394; returns last logits, or all positions' logits [n][vocab]."""
+        ids = np.ascontiguousarray(ids, np.uint32)
+        n = ids.size
+        last = np.empty(self.cfg.vocab, np.float32)
+        per = np.empty((n, self.cfg.vocab), np.float32) if per_pos_logits else None
+        _check(lib().dz_forward_batch(self._h, ids.ctypes.data_as(_u32p), n, self.pos, _f(last),
+                                      _f(per) if per_pos_logits else None))
+        return per if per_pos_logits else last
+
+    def decode_greedy(self, first_token, n):
+        out = np.empty(n, np.uint32)
+        _check(lib().dz_decode_greedy(self._h, int(first_token), int(n), out.ctypes.data_as(_u32p)))
+        return out
+
+    def logits(self):
+        out = np.empty(self.cfg.vocab, np.float32)
+        _check(lib().dz_ctx_logits(self._h, _f(out)))
+        return out
+
+    def mixer_step(self, layer, h):
+        h = np.ascontiguousarray(h, np.float32).copy()
+        _check(lib().dz_ctx_mixer_step(self._h, int(layer), _f(h)))
+        return h
+
+    def set_ssm_state(self, layer, state, conv, head):
+        _check(lib().dz_ctx_set_ssm_state(self._h, int(layer), _f(np.ascontiguousarray(state, np.float32)),
+                                          _f(np.ascontiguousarray(conv, np.float32)), int(head)))
+
+    def get_ssm_state(self, layer):
+        c = self.cfg
+        st = np.empty((c.ssm_v_heads, c.ssm_state, c.ssm_state), np.float32)
+        conv = np.empty((c.ssm_conv_kernel, c.qkv_dim), np.float32)
+        head = ctypes.c_int()
+        _check(lib().dz_ctx_get_ssm_state(self._h, int(layer), _f(st), _f(conv), ctypes.byref(head)))
+        return st, conv, head.value
+
+    def set_kv(self, layer, k, v):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        _check(lib().dz_ctx_set_kv(self._h, int(layer), _f(k), _f(v), k.shape[1]))
+
+    def get_kv(self, layer, n):
+        c = self.cfg
+        k = np.empty((c.n_head_kv, n, c.head_dim), np.float32)
+        v = np.empty_like(k)
+        _check(lib().dz_ctx_get_kv(self._h, int(layer), _f(k), _f(v), int(n)))
+        return k, v
+
+    def stream(self):
+        return lib().dz_ctx_stream(self._h)

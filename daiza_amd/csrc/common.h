@@ -1,0 +1,51 @@
+// common.h — shared definitions of the gfx950 decode library (device + host).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "daiza_hip.h"
+
+namespace dz {
+
+// Q1_0 geometry (Daiza-engine/src/tensor/dtype.rs:11,14)
+constexpr int kGroup = 128;      // weights per scale
+constexpr int kBlockBytes = 18;  // 2-byte f16 scale + 16 sign bytes
+
+// GEMV tiling: one LDS table serves a 512-column K tile; 64 rows per wave (one row per lane).
+constexpr int kTileCols = 512;                       // 64 sign-byte positions
+constexpr int kTilePos = kTileCols / 8;              // 64
+constexpr int kRowBlock = 64;                        // rows per row-block (= lanes per wave)
+constexpr int kUnitSignBytes = kRowBlock * kTilePos; // 4096 B of sign bytes per (row-block, tile)
+constexpr int kUnitScaleBytes = kRowBlock * 4 * 2;   // 4 f16 scales per lane
+constexpr int kUnitBytes = kUnitSignBytes + kUnitScaleBytes;  // 4608
+constexpr int kLutBytes = 256 * kTilePos * 4;        // 64 KiB: f32 [256 sign-byte values][64 positions]
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Device copy of one Q1_0 matrix in the GEMV layout.
+//   unit (rb, t) at byte offset (rb * T + t) * kUnitBytes:
+//     [chunk c 0..3][lane L 0..63][16 B]  stored sign byte s = 16c + i of lane L is the original
+//                                          sign byte at tile position p = L ^ s
+//     [lane L][4 x f16]                    scale slot j of lane L is tile group (L >> 4) ^ j
+//   Row r = 64 rb + L; tile position p = 16 * (group within tile) + (byte within group).
+struct Q1Dev {
+  uint8_t* data = nullptr;
+  int64_t rows = 0, cols = 0;  // logical shape
+  int64_t nrb = 0;             // row-blocks (rows padded to 64)
+  int64_t ntiles = 0;          // K tiles (cols padded to 512)
+};
+
+}  // namespace dz
+
+#define DZ_HIP_CHECK(expr)                                                     \
+  do {                                                                         \
+    hipError_t _e = (expr);                                                    \
+    if (_e != hipSuccess) return dz::set_error(DZ_ERR_DEVICE, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, __LINE__); \
+  } while (0)
+
+namespace dz {
+int set_error(int code, const char* fmt, ...);
+}

@@ -1,0 +1,958 @@
+// model.hip — the batch-1 decode loop on one gfx950 device: weights, context state, the
+// per-token kernel sequence (captured once as a hipGraph) and the model-level C ABI
+// (forward_single_token / forward_batch / ModelState, Daiza-engine/src/model/forward.rs).
+#include "runtime.h"
+#include "model_kernels.h"
+#include "daiza_synth.h"
+
+#include <cmath>
+#include <functional>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+using namespace dz;
+
+namespace dz {
+
+struct LayerDev {
+  bool attn = false;
+  int kind_idx = 0;                  // index among SSM layers or among attention layers
+  float* attn_norm = nullptr;
+  float* post_norm = nullptr;
+  Q1Dev in_proj, out_proj, gate_up, down;  // in_proj: SSM [qkv|z|alpha|beta], attention [q|k|v]
+  float* conv_w = nullptr;           // [4][qkvd], tap 3 newest
+  float* ssm_a = nullptr;
+  float* dt_bias = nullptr;
+  float* ssm_norm = nullptr;
+  float* q_norm = nullptr;
+  float* k_norm = nullptr;
+};
+
+}  // namespace dz
+
+struct dz_model {
+  dz_config cfg;
+  std::vector<LayerDev> L;
+  Q1Dev lm_head;
+  float* output_norm = nullptr;
+  uint16_t* emb_f16 = nullptr;
+  Q1Dev emb_q1;
+  uint64_t q1_bytes = 0;
+  int n_ssm = 0, n_attn = 0;
+  std::vector<void*> allocs;
+};
+
+struct dz_ctx {
+  dz_model* m = nullptr;
+  hipStream_t s = nullptr;
+  TokState* st = nullptr;
+  int* feed = nullptr;
+  int feed_cap = 0;
+  int* toklog = nullptr;
+  float* emb_row = nullptr;
+  float* h[2] = {nullptr, nullptr};
+  float* ss[2] = {nullptr, nullptr};
+  float *p_in = nullptr, *p_o = nullptr, *p_gu = nullptr, *p_down = nullptr;
+  float *y = nullptr, *zs = nullptr, *apart = nullptr;
+  float *h_fin = nullptr, *ss_fin = nullptr, *logits = nullptr, *am_val = nullptr;
+  int* am_idx = nullptr;
+  int n_am = 0;
+  float* ssm_state = nullptr;  // [n_ssm][nvh][128 j][128 i]
+  float* conv = nullptr;       // [n_ssm][4][qkvd]
+  float* kv = nullptr;         // [n_attn][2][nkv][max_ctx][hd]
+  float* rope = nullptr;       // [max_ctx][rope_dim]
+  std::vector<int> ring_base;  // per SSM layer
+  int* ring_base_dev = nullptr;
+  int gmax = 64;
+  int pos_host = 0;            // mirror of TokState::pos_next
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  std::vector<void*> allocs;
+};
+
+namespace dz {
+
+static int alloc_dev(std::vector<void*>& owner, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 16;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return set_error(DZ_ERR_DEVICE, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  owner.push_back(*p);
+  return DZ_OK;
+}
+
+template <class T>
+static int alloc_t(std::vector<void*>& owner, T** p, size_t n) {
+  return alloc_dev(owner, reinterpret_cast<void**>(p), n * sizeof(T));
+}
+
+static int upload_f32(std::vector<void*>& owner, float** dst, const float* src, size_t n) {
+  int rc = alloc_t(owner, dst, n);
+  if (rc) return rc;
+  DZ_HIP_CHECK(hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+  return DZ_OK;
+}
+
+// Repacks AoS Q1_0 bytes (host) into the GEMV layout (device); the matrix API does the same.
+int upload_q1_host(const uint8_t* aos, int64_t rows, int64_t cols, Q1Dev* out, std::vector<void*>& owner);
+
+static int cfg_check(const dz_config* c) {
+  if (!c) return set_error(DZ_ERR_MODEL, "null config");
+  if (c->n_layers < 1 || c->hidden < 128 || c->hidden % 128 || c->ffn % 128 || c->vocab < 1)
+    return set_error(DZ_ERR_MODEL, "config: bad dimensions");
+  if (c->head_dim != 256) return set_error(DZ_ERR_UNSUPPORTED, "head_dim %d (this build: 256)", c->head_dim);
+  if (c->ssm_state != 128) return set_error(DZ_ERR_UNSUPPORTED, "ssm_state %d (this build: 128)", c->ssm_state);
+  if (c->ssm_conv_kernel != 4) return set_error(DZ_ERR_UNSUPPORTED, "ssm_conv_kernel %d (this build: 4)", c->ssm_conv_kernel);
+  if (c->n_head_kv < 1 || c->n_head % c->n_head_kv) return set_error(DZ_ERR_MODEL, "n_head %% n_head_kv != 0");
+  const int grp = c->n_head / c->n_head_kv;
+  if (grp != 1 && grp != 2 && grp != 3 && grp != 4 && grp != 6 && grp != 8)
+    return set_error(DZ_ERR_UNSUPPORTED, "GQA group %d (this build: 1,2,3,4,6,8)", grp);
+  if (c->rope_dim < 2 || c->rope_dim > c->head_dim || c->rope_dim % 2) return set_error(DZ_ERR_MODEL, "rope_dim %d", c->rope_dim);
+  if (c->ssm_k_heads < 1 || c->ssm_v_heads % c->ssm_k_heads) return set_error(DZ_ERR_MODEL, "ssm heads");
+  if (c->max_ctx < 1) return set_error(DZ_ERR_MODEL, "max_ctx %d", c->max_ctx);
+  return DZ_OK;
+}
+
+static bool is_attn_layer(const dz_config* c, int i) {
+  if (c->full_attn_interval == 0) return true;
+  return i % c->full_attn_interval == c->full_attn_interval - 1;
+}
+
+// ---------------------------------------------------------------- synthetic weights (daiza_synth.h)
+
+static void par_rows(int64_t rows, const std::function<void(int64_t, int64_t)>& fn) {
+  unsigned nt = std::thread::hardware_concurrency();
+  if (nt < 1) nt = 1;
+  if (nt > 16) nt = 16;
+  if (rows < 256) nt = 1;
+  std::vector<std::thread> th;
+  const int64_t per = (rows + nt - 1) / nt;
+  for (unsigned t = 0; t < nt; ++t) {
+    const int64_t a = t * per, b = std::min<int64_t>(rows, a + per);
+    if (a >= b) break;
+    th.emplace_back(fn, a, b);
+  }
+  for (auto& x : th) x.join();
+}
+
+// AoS bytes of the synthetic matrix (kind, layer) rows [0, rows) appended to `buf`.
+static void synth_q1_append(std::vector<uint8_t>& buf, uint64_t seed, int kind, int layer, int64_t rows, int64_t cols) {
+  const size_t rb = (size_t)(cols / kGroup) * kBlockBytes;
+  const size_t off = buf.size();
+  buf.resize(off + (size_t)rows * rb);
+  const uint64_t key = dz_key(seed, (uint32_t)kind, (uint32_t)layer);
+  uint8_t* base = buf.data() + off;
+  par_rows(rows, [&](int64_t a, int64_t b) { dz_synth_q1_0_rows(key, (uint64_t)cols, (uint64_t)a, (uint64_t)b, base + a * rb); });
+}
+
+__global__ void synth_embd_kernel(uint64_t key, int64_t n, uint16_t* out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = dz_f32_to_f16(dz_uniform_f32(key, (uint64_t)i, -1.0f, 1.0f));
+}
+
+}  // namespace dz
+
+// ---------------------------------------------------------------- model creation
+
+static int model_finish_common(dz_model* m) {
+  const dz_config& c = m->cfg;
+  int nssm = 0, nattn = 0;
+  for (int i = 0; i < c.n_layers; ++i) {
+    LayerDev& l = m->L[i];
+    l.kind_idx = l.attn ? nattn++ : nssm++;
+  }
+  m->n_ssm = nssm;
+  m->n_attn = nattn;
+  uint64_t b = 0;
+  auto q1b = [](const Q1Dev& q) { return (uint64_t)q.rows * (uint64_t)(q.cols / kGroup) * kBlockBytes; };
+  for (auto& l : m->L) b += q1b(l.in_proj) + q1b(l.out_proj) + q1b(l.gate_up) + q1b(l.down);
+  b += q1b(m->lm_head);
+  m->q1_bytes = b;
+  return DZ_OK;
+}
+
+static void model_release(dz_model* m) {
+  if (!m) return;
+  for (void* p : m->allocs) (void)hipFree(p);
+  delete m;
+}
+
+extern "C" int dz_model_create_synth(const dz_config* cfg, uint64_t seed, dz_model** out) {
+  int rc = cfg_check(cfg);
+  if (rc) return rc;
+  if (!out) return set_error(DZ_ERR_MODEL, "null output");
+  rc = ensure_device();
+  if (rc) return rc;
+  dz_model* m = new dz_model();
+  m->cfg = *cfg;
+  const dz_config& c = *cfg;
+  const int64_t H = c.hidden, F = c.ffn, hd = c.ssm_state;
+  const int64_t kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd, qkvd = 2 * kdim + inner;
+  const int64_t qdim = (int64_t)c.n_head * c.head_dim, kvdim = (int64_t)c.n_head_kv * c.head_dim;
+  m->L.resize(c.n_layers);
+  auto fail = [&](int code) { model_release(m); return code; };
+  std::vector<uint8_t> buf;
+  std::vector<float> fbuf;
+  auto uni = [&](int kind, int layer, int64_t n, float lo, float hi, float** dst) {
+    fbuf.resize(n);
+    dz_synth_uniform_f32(dz_key(seed, (uint32_t)kind, (uint32_t)layer), 0, (uint64_t)n, lo, hi, fbuf.data());
+    return upload_f32(m->allocs, dst, fbuf.data(), (size_t)n);
+  };
+  for (int i = 0; i < c.n_layers; ++i) {
+    LayerDev& l = m->L[i];
+    l.attn = is_attn_layer(&c, i);
+    if ((rc = uni(DZ_K_ATTN_NORM, i, H, 0.8f, 1.2f, &l.attn_norm))) return fail(rc);
+    if ((rc = uni(DZ_K_POST_NORM, i, H, 0.8f, 1.2f, &l.post_norm))) return fail(rc);
+    buf.clear();
+    synth_q1_append(buf, seed, DZ_K_FFN_GATE, i, F, H);
+    synth_q1_append(buf, seed, DZ_K_FFN_UP, i, F, H);
+    if ((rc = upload_q1_host(buf.data(), 2 * F, H, &l.gate_up, m->allocs))) return fail(rc);
+    buf.clear();
+    synth_q1_append(buf, seed, DZ_K_FFN_DOWN, i, H, F);
+    if ((rc = upload_q1_host(buf.data(), H, F, &l.down, m->allocs))) return fail(rc);
+    if (!l.attn) {
+      buf.clear();
+      synth_q1_append(buf, seed, DZ_K_SSM_QKV, i, qkvd, H);
+      synth_q1_append(buf, seed, DZ_K_SSM_Z, i, inner, H);
+      synth_q1_append(buf, seed, DZ_K_SSM_ALPHA, i, c.ssm_v_heads, H);
+      synth_q1_append(buf, seed, DZ_K_SSM_BETA, i, c.ssm_v_heads, H);
+      if ((rc = upload_q1_host(buf.data(), qkvd + inner + 2 * c.ssm_v_heads, H, &l.in_proj, m->allocs))) return fail(rc);
+      buf.clear();
+      synth_q1_append(buf, seed, DZ_K_SSM_OUT, i, H, inner);
+      if ((rc = upload_q1_host(buf.data(), H, inner, &l.out_proj, m->allocs))) return fail(rc);
+      // conv1d: GGUF order [qkvd][4], stored tap-major (weights.rs:1339-1356)
+      const int64_t ck = c.ssm_conv_kernel;
+      std::vector<float> raw((size_t)(qkvd * ck)), tr((size_t)(qkvd * ck));
+      dz_synth_normal_f32(dz_key(seed, DZ_K_SSM_CONV, (uint32_t)i), 0, (uint64_t)(qkvd * ck), 0.0, 0.25, raw.data());
+      for (int64_t ch = 0; ch < qkvd; ++ch)
+        for (int64_t t = 0; t < ck; ++t) tr[(size_t)(t * qkvd + ch)] = raw[(size_t)(ch * ck + t)];
+      if ((rc = upload_f32(m->allocs, &l.conv_w, tr.data(), tr.size()))) return fail(rc);
+      std::vector<float> v((size_t)c.ssm_v_heads);
+      dz_synth_ssm_a(dz_key(seed, DZ_K_SSM_A, (uint32_t)i), (uint64_t)c.ssm_v_heads, v.data());
+      if ((rc = upload_f32(m->allocs, &l.ssm_a, v.data(), v.size()))) return fail(rc);
+      dz_synth_normal_f32(dz_key(seed, DZ_K_SSM_DT, (uint32_t)i), 0, (uint64_t)c.ssm_v_heads, 0.0, 0.1, v.data());
+      if ((rc = upload_f32(m->allocs, &l.dt_bias, v.data(), v.size()))) return fail(rc);
+      if ((rc = uni(DZ_K_SSM_NORM, i, hd, 0.8f, 1.2f, &l.ssm_norm))) return fail(rc);
+    } else {
+      buf.clear();
+      synth_q1_append(buf, seed, DZ_K_ATT_Q, i, 2 * qdim, H);
+      synth_q1_append(buf, seed, DZ_K_ATT_K, i, kvdim, H);
+      synth_q1_append(buf, seed, DZ_K_ATT_V, i, kvdim, H);
+      if ((rc = upload_q1_host(buf.data(), 2 * qdim + 2 * kvdim, H, &l.in_proj, m->allocs))) return fail(rc);
+      buf.clear();
+      synth_q1_append(buf, seed, DZ_K_ATT_O, i, H, qdim);
+      if ((rc = upload_q1_host(buf.data(), H, qdim, &l.out_proj, m->allocs))) return fail(rc);
+      if ((rc = uni(DZ_K_ATT_QNORM, i, c.head_dim, 0.8f, 1.2f, &l.q_norm))) return fail(rc);
+      if ((rc = uni(DZ_K_ATT_KNORM, i, c.head_dim, 0.8f, 1.2f, &l.k_norm))) return fail(rc);
+    }
+  }
+  if ((rc = uni(DZ_K_OUTPUT_NORM, -1, H, 0.8f, 1.2f, &m->output_norm))) return fail(rc);
+  buf.clear();
+  synth_q1_append(buf, seed, DZ_K_OUTPUT, -1, c.vocab, H);
+  if ((rc = upload_q1_host(buf.data(), c.vocab, H, &m->lm_head, m->allocs))) return fail(rc);
+  buf.clear();
+  buf.shrink_to_fit();
+  if (c.embd_f16) {
+    const int64_t n = (int64_t)c.vocab * H;
+    if ((rc = alloc_t(m->allocs, &m->emb_f16, (size_t)n))) return fail(rc);
+    hipLaunchKernelGGL(synth_embd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, lib_stream(),
+                       dz_key(seed, DZ_K_EMBD, (uint32_t)-1), n, m->emb_f16);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
+    if (e != hipSuccess) return fail(set_error(DZ_ERR_DEVICE, "embedding synth: %s", hipGetErrorString(e)));
+  } else {
+    std::vector<uint8_t> eb;
+    synth_q1_append(eb, seed, DZ_K_EMBD, -1, c.vocab, H);
+    if ((rc = upload_q1_host(eb.data(), c.vocab, H, &m->emb_q1, m->allocs))) return fail(rc);
+  }
+  model_finish_common(m);
+  *out = m;
+  return DZ_OK;
+}
+
+// GGUF-named host tensors (LoadedWeights::load_all, weights.rs:1308-1379).
+extern "C" int dz_model_create(const dz_config* cfg, const dz_tensor* tensors, int n_tensors, dz_model** out) {
+  int rc = cfg_check(cfg);
+  if (rc) return rc;
+  if (!out || (!tensors && n_tensors)) return set_error(DZ_ERR_MODEL, "null argument");
+  rc = ensure_device();
+  if (rc) return rc;
+  std::unordered_map<std::string, const dz_tensor*> byname;
+  for (int i = 0; i < n_tensors; ++i) byname[tensors[i].name] = &tensors[i];
+  dz_model* m = new dz_model();
+  m->cfg = *cfg;
+  const dz_config& c = *cfg;
+  const int64_t H = c.hidden, F = c.ffn, hd = c.ssm_state;
+  const int64_t kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd, qkvd = 2 * kdim + inner;
+  const int64_t qdim = (int64_t)c.n_head * c.head_dim, kvdim = (int64_t)c.n_head_kv * c.head_dim;
+  auto fail = [&](int code) { model_release(m); return code; };
+  auto find = [&](const std::string& name, int type, size_t bytes, const dz_tensor** t) {
+    auto it = byname.find(name);
+    if (it == byname.end()) return set_error(DZ_ERR_MODEL, "tensor %s not found", name.c_str());
+    if (it->second->type != type) return set_error(DZ_ERR_MODEL, "tensor %s: type %d, expected %d", name.c_str(), it->second->type, type);
+    if (it->second->n_bytes != bytes)
+      return set_error(DZ_ERR_TENSOR, "tensor %s: %zu bytes, expected %zu", name.c_str(), it->second->n_bytes, bytes);
+    *t = it->second;
+    return DZ_OK;
+  };
+  auto q1bytes = [](int64_t r, int64_t k) { return (size_t)r * (size_t)(k / kGroup) * kBlockBytes; };
+  std::vector<uint8_t> buf;
+  auto cat_q1 = [&](const std::string& name, int64_t rows, int64_t cols) {
+    const dz_tensor* t;
+    int r = find(name, 41, q1bytes(rows, cols), &t);
+    if (r) return r;
+    const uint8_t* p = static_cast<const uint8_t*>(t->data);
+    buf.insert(buf.end(), p, p + t->n_bytes);
+    return DZ_OK;
+  };
+  auto f32 = [&](const std::string& name, int64_t n, float** dst) {
+    const dz_tensor* t;
+    int r = find(name, 0, (size_t)n * 4, &t);
+    if (r) return r;
+    return upload_f32(m->allocs, dst, static_cast<const float*>(t->data), (size_t)n);
+  };
+  m->L.resize(c.n_layers);
+  for (int i = 0; i < c.n_layers; ++i) {
+    LayerDev& l = m->L[i];
+    l.attn = is_attn_layer(&c, i);
+    const std::string b = "blk." + std::to_string(i) + ".";
+    if ((rc = f32(b + "attn_norm.weight", H, &l.attn_norm))) return fail(rc);
+    if ((rc = f32(b + "post_attention_norm.weight", H, &l.post_norm))) return fail(rc);
+    buf.clear();
+    if ((rc = cat_q1(b + "ffn_gate.weight", F, H)) || (rc = cat_q1(b + "ffn_up.weight", F, H))) return fail(rc);
+    if ((rc = upload_q1_host(buf.data(), 2 * F, H, &l.gate_up, m->allocs))) return fail(rc);
+    buf.clear();
+    if ((rc = cat_q1(b + "ffn_down.weight", H, F))) return fail(rc);
+    if ((rc = upload_q1_host(buf.data(), H, F, &l.down, m->allocs))) return fail(rc);
+    if (!l.attn) {
+      buf.clear();
+      if ((rc = cat_q1(b + "attn_qkv.weight", qkvd, H)) || (rc = cat_q1(b + "attn_gate.weight", inner, H)) ||
+          (rc = cat_q1(b + "ssm_alpha.weight", c.ssm_v_heads, H)) || (rc = cat_q1(b + "ssm_beta.weight", c.ssm_v_heads, H)))
+        return fail(rc);
+      if ((rc = upload_q1_host(buf.data(), qkvd + inner + 2 * c.ssm_v_heads, H, &l.in_proj, m->allocs))) return fail(rc);
+      buf.clear();
+      if ((rc = cat_q1(b + "ssm_out.weight", H, inner))) return fail(rc);
+      if ((rc = upload_q1_host(buf.data(), H, inner, &l.out_proj, m->allocs))) return fail(rc);
+      const dz_tensor* t;
+      const int64_t ck = c.ssm_conv_kernel;
+      if ((rc = find(b + "ssm_conv1d.weight", 0, (size_t)(qkvd * ck) * 4, &t))) return fail(rc);
+      const float* raw = static_cast<const float*>(t->data);
+      std::vector<float> tr((size_t)(qkvd * ck));
+      for (int64_t ch = 0; ch < qkvd; ++ch)
+        for (int64_t k = 0; k < ck; ++k) tr[(size_t)(k * qkvd + ch)] = raw[(size_t)(ch * ck + k)];
+      if ((rc = upload_f32(m->allocs, &l.conv_w, tr.data(), tr.size()))) return fail(rc);
+      if ((rc = f32(b + "ssm_a", c.ssm_v_heads, &l.ssm_a))) return fail(rc);
+      if ((rc = f32(b + "ssm_dt.bias", c.ssm_v_heads, &l.dt_bias))) return fail(rc);
+      if ((rc = f32(b + "ssm_norm.weight", hd, &l.ssm_norm))) return fail(rc);
+    } else {
+      buf.clear();
+      if ((rc = cat_q1(b + "attn_q.weight", 2 * qdim, H)) || (rc = cat_q1(b + "attn_k.weight", kvdim, H)) ||
+          (rc = cat_q1(b + "attn_v.weight", kvdim, H)))
+        return fail(rc);
+      if ((rc = upload_q1_host(buf.data(), 2 * qdim + 2 * kvdim, H, &l.in_proj, m->allocs))) return fail(rc);
+      buf.clear();
+      if ((rc = cat_q1(b + "attn_output.weight", H, qdim))) return fail(rc);
+      if ((rc = upload_q1_host(buf.data(), H, qdim, &l.out_proj, m->allocs))) return fail(rc);
+      if ((rc = f32(b + "attn_q_norm.weight", c.head_dim, &l.q_norm))) return fail(rc);
+      if ((rc = f32(b + "attn_k_norm.weight", c.head_dim, &l.k_norm))) return fail(rc);
+    }
+  }
+  if ((rc = f32("output_norm.weight", H, &m->output_norm))) return fail(rc);
+  buf.clear();
+  if ((rc = cat_q1("output.weight", c.vocab, H))) return fail(rc);
+  if ((rc = upload_q1_host(buf.data(), c.vocab, H, &m->lm_head, m->allocs))) return fail(rc);
+  buf.clear();
+  if (c.embd_f16) {
+    const dz_tensor* t;
+    if ((rc = find("token_embd.weight", 1, (size_t)c.vocab * H * 2, &t))) return fail(rc);
+    if ((rc = alloc_t(m->allocs, &m->emb_f16, (size_t)c.vocab * H))) return fail(rc);
+    DZ_HIP_CHECK(hipMemcpy(m->emb_f16, t->data, t->n_bytes, hipMemcpyHostToDevice));
+  } else {
+    if ((rc = cat_q1("token_embd.weight", c.vocab, H))) return fail(rc);
+    if ((rc = upload_q1_host(buf.data(), c.vocab, H, &m->emb_q1, m->allocs))) return fail(rc);
+  }
+  model_finish_common(m);
+  *out = m;
+  return DZ_OK;
+}
+
+extern "C" int dz_model_free(dz_model* m) {
+  model_release(m);
+  return DZ_OK;
+}
+
+extern "C" int dz_model_weight_bytes(const dz_model* m, uint64_t* q1_bytes) {
+  if (!m || !q1_bytes) return set_error(DZ_ERR_MODEL, "null argument");
+  *q1_bytes = m->q1_bytes;
+  return DZ_OK;
+}
+
+// ---------------------------------------------------------------- context
+
+namespace dz {
+
+static int ctx_dims(const dz_model* m, int64_t* ld_in, int64_t* ld_h, int64_t* ld_gu, int* th, int* to, int* tf) {
+  const dz_config& c = m->cfg;
+  int64_t mx = 0;
+  for (auto& l : m->L) mx = std::max<int64_t>(mx, l.in_proj.nrb * kRowBlock);
+  *ld_in = mx;
+  *ld_h = ((int64_t)c.hidden + kRowBlock - 1) / kRowBlock * kRowBlock;
+  *ld_gu = (2 * (int64_t)c.ffn + kRowBlock - 1) / kRowBlock * kRowBlock;
+  *th = (int)((c.hidden + kTileCols - 1) / kTileCols);
+  int64_t ko = std::max<int64_t>((int64_t)c.ssm_v_heads * c.ssm_state, (int64_t)c.n_head * c.head_dim);
+  *to = (int)((ko + kTileCols - 1) / kTileCols);
+  *tf = (int)((c.ffn + kTileCols - 1) / kTileCols);
+  return DZ_OK;
+}
+
+static void rope_table(const dz_config& c, std::vector<float>& out) {
+  // rope.rs:27-38 and 82-101: freq_i = 1 / base^(2i/d); theta = (pos as f32) * freq_i
+  const int half = c.rope_dim / 2;
+  std::vector<float> fr(half);
+  for (int i = 0; i < half; ++i) fr[i] = 1.0f / powf(c.rope_base, (float)(2 * i) / (float)c.rope_dim);
+  out.resize((size_t)c.max_ctx * c.rope_dim);
+  for (int p = 0; p < c.max_ctx; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float th = (float)p * fr[i];
+      out[(size_t)p * c.rope_dim + i] = cosf(th);
+      out[(size_t)p * c.rope_dim + half + i] = sinf(th);
+    }
+}
+
+template <class Src, class Dst>
+static int gemv(const Q1Dev& mat, int tpw, const Src& src, const Dst& dst, hipStream_t s, int64_t* ld = nullptr) {
+  const Q1Dev* ms[1] = {&mat};
+  GemvPlan p;
+  int rc = plan_gemv(ms, 1, tpw, &p);
+  if (rc) return rc;
+  if (ld) *ld = p.ld;
+  DZ_HIP_CHECK(launch_gemv(p, src, dst, s));
+  return DZ_OK;
+}
+
+static int launch_attention(int grp, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  switch (grp) {
+    case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL(attention_kernel<6>, grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, s, a); break;
+    default: return set_error(DZ_ERR_UNSUPPORTED, "GQA group %d", grp);
+  }
+  DZ_HIP_CHECK(hipGetLastError());
+  return DZ_OK;
+}
+
+// The mixer of one layer on the residual held in (h_in + parts): norm + in-proj GEMV, then the
+// DeltaNet or attention kernel, then the out-projection GEMV into p_o.  `h_mid` receives the
+// materialised layer input with its tile sums of squares in `ss_mid`.
+static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* parts, int np, int64_t ldp, float* h_mid,
+                         float* ss_mid, hipStream_t s) {
+  dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  LayerDev& l = m->L[li];
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int64_t H = c.hidden, hd = c.ssm_state;
+  const int64_t kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd, qkvd = 2 * kdim + inner;
+  int rc;
+  int64_t ld_l = 0;
+  {
+    ResidSrc src{h_in, parts, np, ldp, l.attn_norm, h_mid, ss_mid, H};
+    PartialDst dst{x->p_in, l.in_proj.nrb * kRowBlock};
+    if ((rc = gemv(l.in_proj, 1, src, dst, s, &ld_l))) return rc;
+  }
+  const int nin = (int)l.in_proj.ntiles;
+  if (!l.attn) {
+    DeltaArgs a;
+    a.st = x->st;
+    a.p_in = x->p_in;
+    a.np = nin;
+    a.ldp = ld_l;
+    a.ss = ss_mid;
+    a.nss = th;
+    a.H = H;
+    a.rms_eps = c.rms_eps;
+    a.conv = x->conv + (size_t)l.kind_idx * 4 * qkvd;
+    a.conv_w = l.conv_w;
+    a.ssm_a = l.ssm_a;
+    a.dt_bias = l.dt_bias;
+    a.state = x->ssm_state + (size_t)l.kind_idx * c.ssm_v_heads * hd * hd;
+    a.y = x->y;
+    a.zs = x->zs;
+    a.nkh = c.ssm_k_heads;
+    a.nvh = c.ssm_v_heads;
+    a.qkvd = qkvd;
+    a.off_z = qkvd;
+    a.off_a = qkvd + inner;
+    a.off_b = qkvd + inner + c.ssm_v_heads;
+    a.ring_base_ptr = x->ring_base_dev + l.kind_idx;
+    hipLaunchKernelGGL(deltanet_kernel, dim3((unsigned)(c.ssm_v_heads * 4)), dim3(256), 0, s, a);
+    DZ_HIP_CHECK(hipGetLastError());
+    GatedYSrc src{x->y, x->zs, l.ssm_norm, inner, 1e-6f};
+    PartialDst dst{x->p_o, ld_h};
+    if ((rc = gemv(l.out_proj, 1, src, dst, s))) return rc;
+  } else {
+    AttnArgs a;
+    a.st = x->st;
+    a.p_in = x->p_in;
+    a.np = nin;
+    a.ldp = ld_l;
+    a.ss = ss_mid;
+    a.nss = th;
+    a.H = H;
+    a.eps = c.rms_eps;
+    a.q_norm = l.q_norm;
+    a.k_norm = l.k_norm;
+    a.rope = x->rope;
+    a.rope_dim = c.rope_dim;
+    const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
+    a.kcache = x->kv + (size_t)l.kind_idx * 2 * kvsz;
+    a.vcache = a.kcache + kvsz;
+    a.max_ctx = c.max_ctx;
+    a.apart = x->apart;
+    a.gmax = x->gmax;
+    a.nq = c.n_head;
+    a.nkv = c.n_head_kv;
+    if ((rc = launch_attention(c.n_head / c.n_head_kv, dim3((unsigned)(c.n_head_kv * x->gmax)), a, s))) return rc;
+    AttnOutSrc src{x->apart, x->gmax, c.head_dim, (int64_t)c.n_head * c.head_dim, x->st, x->p_in, nin, ld_l,
+                   ss_mid, th, H, c.rms_eps};
+    PartialDst dst{x->p_o, ld_h};
+    if ((rc = gemv(l.out_proj, 1, src, dst, s))) return rc;
+  }
+  return DZ_OK;
+}
+
+// One token (forward_single_token): select/embed, all blocks, final norm, lm_head.
+static int enqueue_token(dz_ctx* x, hipStream_t s) {
+  dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int64_t H = c.hidden, F = c.ffn;
+  int rc;
+  SelectArgs sa;
+  sa.st = x->st;
+  sa.feed = x->feed;
+  sa.am_val = x->am_val;
+  sa.am_idx = x->am_idx;
+  sa.n_am = x->n_am;
+  sa.toklog = x->toklog;
+  sa.emb_f16 = m->emb_f16;
+  sa.emb_q1 = m->emb_q1.data;
+  sa.emb_ntiles = m->emb_q1.ntiles;
+  sa.H = H;
+  sa.emb_out = x->emb_row;
+  sa.commit = 1;
+  hipLaunchKernelGGL(select_token_kernel, dim3(1), dim3(1024), 0, s, sa);
+  DZ_HIP_CHECK(hipGetLastError());
+  for (int li = 0; li < c.n_layers; ++li) {
+    LayerDev& l = m->L[li];
+    const float* h_in = li == 0 ? x->emb_row : x->h[1];
+    const int np = li == 0 ? 0 : (int)m->L[li - 1].down.ntiles;
+    if ((rc = enqueue_mixer(x, li, h_in, x->p_down, np, ld_h, x->h[0], x->ss[0], s))) return rc;
+    // post-attention norm + gate/up (block.rs:101-120, mlp.rs:28-47)
+    {
+      ResidSrc src{x->h[0], x->p_o, (int)l.out_proj.ntiles, ld_h, l.post_norm, x->h[1], x->ss[1], H};
+      PartialDst dst{x->p_gu, ld_gu};
+      if ((rc = gemv(l.gate_up, 1, src, dst, s))) return rc;
+    }
+    {
+      SwigluSrc src{x->p_gu, (int)l.gate_up.ntiles, ld_gu, F, x->ss[1], th, H, c.rms_eps};
+      PartialDst dst{x->p_down, ld_h};
+      if ((rc = gemv(l.down, 1, src, dst, s))) return rc;
+    }
+  }
+  FinalArgs fa{x->h[1], x->p_down, (int)m->L[c.n_layers - 1].down.ntiles, ld_h, x->h_fin, x->ss_fin, H};
+  hipLaunchKernelGGL(final_reduce_kernel, dim3((unsigned)th), dim3(512), 0, s, fa);
+  DZ_HIP_CHECK(hipGetLastError());
+  NormedSrc src{x->h_fin, m->output_norm, x->ss_fin, th, H, c.rms_eps};
+  LogitsDst dst{x->logits, c.vocab, x->am_val, x->am_idx};
+  if ((rc = gemv(m->lm_head, (int)m->lm_head.ntiles, src, dst, s))) return rc;
+  return DZ_OK;
+}
+
+template <class Src, class Dst>
+static int set_gemv_attr() {
+  DZ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_lut_kernel<kGemvWaves, kGemvM, Src, Dst>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, kGemvShmemMax));
+  return DZ_OK;
+}
+
+}  // namespace dz
+
+// Dynamic-LDS limits of every GEMV instantiation, set once before any launch or graph capture.
+int dz::prepare_gemv_kernels() {
+  static bool done = false;
+  if (done) return DZ_OK;
+  int rc;
+  if ((rc = set_gemv_attr<ResidSrc, PartialDst>())) return rc;
+  if ((rc = set_gemv_attr<SwigluSrc, PartialDst>())) return rc;
+  if ((rc = set_gemv_attr<GatedYSrc, PartialDst>())) return rc;
+  if ((rc = set_gemv_attr<AttnOutSrc, PartialDst>())) return rc;
+  if ((rc = set_gemv_attr<NormedSrc, LogitsDst>())) return rc;
+  if ((rc = set_gemv_attr<PlainSrc, PartialDst>())) return rc;
+  done = true;
+  return DZ_OK;
+}
+
+namespace dz {
+
+static int ctx_build_graph(dz_ctx* x) {
+  if (x->gexec) return DZ_OK;
+  DZ_HIP_CHECK(hipStreamBeginCapture(x->s, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_token(x, x->s);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(x->s, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return set_error(DZ_ERR_DEVICE, "graph capture: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(&x->gexec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return set_error(DZ_ERR_DEVICE, "graph instantiate: %s", hipGetErrorString(e));
+  }
+  x->graph = g;
+  return DZ_OK;
+}
+
+}  // namespace dz
+
+// ---------------------------------------------------------------- context C ABI
+
+namespace dz {
+
+static void ctx_release(dz_ctx* x) {
+  if (!x) return;
+  if (x->gexec) (void)hipGraphExecDestroy(x->gexec);
+  if (x->graph) (void)hipGraphDestroy(x->graph);
+  if (x->s) (void)hipStreamSynchronize(x->s);
+  for (void* p : x->allocs) (void)hipFree(p);
+  if (x->s) (void)hipStreamDestroy(x->s);
+  delete x;
+}
+
+static int ctx_zero_state(dz_ctx* x) {
+  const dz_config& c = x->m->cfg;
+  const int64_t hd = c.ssm_state, qkvd = (2 * (int64_t)c.ssm_k_heads + c.ssm_v_heads) * hd;
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
+  if (x->m->n_ssm) {
+    DZ_HIP_CHECK(hipMemsetAsync(x->ssm_state, 0, (size_t)x->m->n_ssm * c.ssm_v_heads * hd * hd * 4, x->s));
+    DZ_HIP_CHECK(hipMemsetAsync(x->conv, 0, (size_t)x->m->n_ssm * 4 * qkvd * 4, x->s));
+    DZ_HIP_CHECK(hipMemsetAsync(x->ring_base_dev, 0, (size_t)x->m->n_ssm * 4, x->s));
+  }
+  if (x->m->n_attn) DZ_HIP_CHECK(hipMemsetAsync(x->kv, 0, (size_t)x->m->n_attn * 2 * kvsz * 4, x->s));
+  std::fill(x->ring_base.begin(), x->ring_base.end(), 0);
+  TokState st;
+  memset(&st, 0, sizeof st);
+  DZ_HIP_CHECK(hipMemcpyAsync(x->st, &st, sizeof st, hipMemcpyHostToDevice, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  x->pos_host = 0;
+  return DZ_OK;
+}
+
+// Host-fed token ids consumed by the next forwards (TokState::feed_len / feed_idx).
+static int ctx_feed(dz_ctx* x, const uint32_t* ids, int n) {
+  if (n > x->feed_cap) return set_error(DZ_ERR_TENSOR, "feed of %d ids exceeds capacity %d", n, x->feed_cap);
+  for (int i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)x->m->cfg.vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", ids[i], x->m->cfg.vocab);
+  if (n) DZ_HIP_CHECK(hipMemcpyAsync(x->feed, ids, (size_t)n * 4, hipMemcpyHostToDevice, x->s));
+  int two[2] = {n, 0};
+  DZ_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<char*>(x->st) + offsetof(TokState, feed_len), two, sizeof two,
+                              hipMemcpyHostToDevice, x->s));
+  // the copies above read pageable host memory: make them complete before `ids` may change
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+static int ctx_run(dz_ctx* x, int n) {
+  if (x->pos_host + n > x->m->cfg.max_ctx)
+    return set_error(DZ_ERR_TENSOR, "context full: pos %d + %d > max_ctx %d", x->pos_host, n, x->m->cfg.max_ctx);
+  int rc = ctx_build_graph(x);
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i) DZ_HIP_CHECK(hipGraphLaunch(x->gexec, x->s));
+  x->pos_host += n;
+  return DZ_OK;
+}
+
+// Writes the greedy token of the current logits to toklog[pos_next] without consuming it.
+static int ctx_peek_argmax(dz_ctx* x) {
+  SelectArgs sa;
+  memset(&sa, 0, sizeof sa);
+  sa.st = x->st;
+  sa.feed = x->feed;
+  sa.am_val = x->am_val;
+  sa.am_idx = x->am_idx;
+  sa.n_am = x->n_am;
+  sa.toklog = x->toklog;
+  sa.H = x->m->cfg.hidden;
+  sa.commit = 0;
+  hipLaunchKernelGGL(select_token_kernel, dim3(1), dim3(1024), 0, x->s, sa);
+  DZ_HIP_CHECK(hipGetLastError());
+  return DZ_OK;
+}
+
+static int ctx_set_pos_dev(dz_ctx* x, int pos) {
+  int v[2] = {pos, pos};  // TokState.pos_next and a consistent .pos for direct mixer launches
+  DZ_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos_next), &v[0], 4,
+                              hipMemcpyHostToDevice, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  x->pos_host = pos;
+  return DZ_OK;
+}
+
+}  // namespace dz
+
+extern "C" {
+
+int dz_ctx_create(dz_model* m, dz_ctx** out) {
+  if (!m || !out) return set_error(DZ_ERR_MODEL, "null argument");
+  int rc = ensure_device();
+  if (rc) return rc;
+  if ((rc = prepare_gemv_kernels())) return rc;
+  dz_ctx* x = new dz_ctx();
+  x->m = m;
+  const dz_config& c = m->cfg;
+  auto fail = [&](int code) { ctx_release(x); return code; };
+  hipError_t e = hipStreamCreateWithFlags(&x->s, hipStreamNonBlocking);
+  if (e != hipSuccess) return fail(set_error(DZ_ERR_DEVICE, "stream: %s", hipGetErrorString(e)));
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int64_t hd = c.ssm_state, inner = (int64_t)c.ssm_v_heads * hd;
+  const int64_t qkvd = 2 * (int64_t)c.ssm_k_heads * hd + inner;
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
+  auto& A = x->allocs;
+  x->feed_cap = c.max_ctx;
+  x->n_am = (int)m->lm_head.nrb;
+  if ((rc = alloc_t(A, &x->st, 1)) || (rc = alloc_t(A, &x->feed, (size_t)x->feed_cap)) ||
+      (rc = alloc_t(A, &x->toklog, (size_t)c.max_ctx + 1)) || (rc = alloc_t(A, &x->emb_row, (size_t)c.hidden)) ||
+      (rc = alloc_t(A, &x->h[0], (size_t)ld_h)) || (rc = alloc_t(A, &x->h[1], (size_t)ld_h)) ||
+      (rc = alloc_t(A, &x->ss[0], (size_t)th)) || (rc = alloc_t(A, &x->ss[1], (size_t)th)) ||
+      (rc = alloc_t(A, &x->p_in, (size_t)th * ld_in)) || (rc = alloc_t(A, &x->p_o, (size_t)to * ld_h)) ||
+      (rc = alloc_t(A, &x->p_gu, (size_t)th * ld_gu)) || (rc = alloc_t(A, &x->p_down, (size_t)tf * ld_h)) ||
+      (rc = alloc_t(A, &x->y, (size_t)inner)) || (rc = alloc_t(A, &x->zs, (size_t)inner)) ||
+      (rc = alloc_t(A, &x->apart, (size_t)c.n_head * x->gmax * (2 + c.head_dim))) ||
+      (rc = alloc_t(A, &x->h_fin, (size_t)ld_h)) || (rc = alloc_t(A, &x->ss_fin, (size_t)th)) ||
+      (rc = alloc_t(A, &x->logits, (size_t)m->lm_head.nrb * kRowBlock)) ||
+      (rc = alloc_t(A, &x->am_val, (size_t)x->n_am)) || (rc = alloc_t(A, &x->am_idx, (size_t)x->n_am)) ||
+      (rc = alloc_t(A, &x->ssm_state, (size_t)std::max(1, m->n_ssm) * c.ssm_v_heads * hd * hd)) ||
+      (rc = alloc_t(A, &x->conv, (size_t)std::max(1, m->n_ssm) * 4 * qkvd)) ||
+      (rc = alloc_t(A, &x->ring_base_dev, (size_t)std::max(1, m->n_ssm))) ||
+      (rc = alloc_t(A, &x->kv, (size_t)std::max(1, m->n_attn) * 2 * kvsz)))
+    return fail(rc);
+  x->ring_base.assign((size_t)m->n_ssm, 0);
+  std::vector<float> rope;
+  rope_table(c, rope);
+  if ((rc = upload_f32(A, &x->rope, rope.data(), rope.size()))) return fail(rc);
+  // argmax partials of "no logits yet": value -inf everywhere, selects token 0 if ever read
+  if ((rc = ctx_zero_state(x))) return fail(rc);
+  *out = x;
+  return DZ_OK;
+}
+
+int dz_ctx_free(dz_ctx* x) {
+  ctx_release(x);
+  return DZ_OK;
+}
+
+int dz_ctx_reset(dz_ctx* x) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  return ctx_zero_state(x);
+}
+
+int dz_ctx_pos(const dz_ctx* x) { return x ? x->pos_host : -1; }
+
+void* dz_ctx_stream(dz_ctx* x) { return x ? (void*)x->s : nullptr; }
+
+int dz_forward_token(dz_ctx* x, uint32_t token, float* logits, uint32_t* argmax) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  int rc = ctx_feed(x, &token, 1);
+  if (rc) return rc;
+  if ((rc = ctx_run(x, 1))) return rc;
+  if (argmax) {
+    if ((rc = ctx_peek_argmax(x))) return rc;
+    int t;
+    DZ_HIP_CHECK(hipMemcpyAsync(&t, x->toklog + x->pos_host, 4, hipMemcpyDeviceToHost, x->s));
+    DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+    *argmax = (uint32_t)t;
+  }
+  if (logits) DZ_HIP_CHECK(hipMemcpyAsync(logits, x->logits, (size_t)x->m->cfg.vocab * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float* last_logits, float* per_pos) {
+  if (!x || (!ids && n)) return set_error(DZ_ERR_MODEL, "null argument");
+  if (n < 1) return set_error(DZ_ERR_TENSOR, "forward_batch: empty batch");
+  if (start_pos != x->pos_host)
+    return set_error(DZ_ERR_TENSOR, "forward_batch: start_pos %d != context position %d", start_pos, x->pos_host);
+  if (x->pos_host + n > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "forward_batch: context full");
+  int rc = ctx_feed(x, ids, n);
+  if (rc) return rc;
+  const size_t V = (size_t)x->m->cfg.vocab;
+  for (int i = 0; i < n; ++i) {
+    if ((rc = ctx_run(x, 1))) return rc;
+    if (per_pos) DZ_HIP_CHECK(hipMemcpyAsync(per_pos + (size_t)i * V, x->logits, V * 4, hipMemcpyDeviceToHost, x->s));
+  }
+  if (last_logits) DZ_HIP_CHECK(hipMemcpyAsync(last_logits, x->logits, V * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_tokens) {
+  if (!x || !out_tokens) return set_error(DZ_ERR_MODEL, "null argument");
+  if (n < 1) return DZ_OK;
+  const int p0 = x->pos_host;
+  int rc = ctx_feed(x, &first_token, 1);
+  if (rc) return rc;
+  if ((rc = ctx_run(x, n))) return rc;
+  if ((rc = ctx_peek_argmax(x))) return rc;
+  DZ_HIP_CHECK(hipMemcpyAsync(out_tokens, x->toklog + p0 + 1, (size_t)n * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+int dz_ctx_logits(dz_ctx* x, float* logits) {
+  if (!x || !logits) return set_error(DZ_ERR_MODEL, "null argument");
+  DZ_HIP_CHECK(hipMemcpyAsync(logits, x->logits, (size_t)x->m->cfg.vocab * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+static int layer_of(dz_ctx* x, int layer, bool want_attn, LayerDev** out) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (layer < 0 || layer >= x->m->cfg.n_layers) return set_error(DZ_ERR_TENSOR, "layer %d out of range", layer);
+  LayerDev& l = x->m->L[layer];
+  if (l.attn != want_attn) return set_error(DZ_ERR_TENSOR, "layer %d is not a%s layer", layer, want_attn ? "n attention" : " DeltaNet");
+  *out = &l;
+  return DZ_OK;
+}
+
+int dz_ctx_set_ssm_state(dz_ctx* x, int layer, const float* state, const float* conv_hist, int conv_head) {
+  LayerDev* l;
+  int rc = layer_of(x, layer, false, &l);
+  if (rc) return rc;
+  const dz_config& c = x->m->cfg;
+  const int64_t hd = c.ssm_state, nvh = c.ssm_v_heads, qkvd = (2 * (int64_t)c.ssm_k_heads + nvh) * hd;
+  if (conv_head < 0 || conv_head > 3) return set_error(DZ_ERR_TENSOR, "conv_head %d", conv_head);
+  std::vector<float> tr((size_t)(nvh * hd * hd));
+  for (int64_t v = 0; v < nvh; ++v)
+    for (int64_t i = 0; i < hd; ++i)
+      for (int64_t j = 0; j < hd; ++j) tr[(size_t)((v * hd + j) * hd + i)] = state[(size_t)((v * hd + i) * hd + j)];
+  DZ_HIP_CHECK(hipMemcpy(x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, tr.data(), tr.size() * 4, hipMemcpyHostToDevice));
+  DZ_HIP_CHECK(hipMemcpy(x->conv + (size_t)l->kind_idx * 4 * qkvd, conv_hist, (size_t)(4 * qkvd) * 4, hipMemcpyHostToDevice));
+  const int base = ((conv_head - x->pos_host) % 4 + 4) % 4;
+  x->ring_base[l->kind_idx] = base;
+  DZ_HIP_CHECK(hipMemcpy(x->ring_base_dev + l->kind_idx, &base, 4, hipMemcpyHostToDevice));
+  return DZ_OK;
+}
+
+int dz_ctx_get_ssm_state(dz_ctx* x, int layer, float* state, float* conv_hist, int* conv_head) {
+  LayerDev* l;
+  int rc = layer_of(x, layer, false, &l);
+  if (rc) return rc;
+  const dz_config& c = x->m->cfg;
+  const int64_t hd = c.ssm_state, nvh = c.ssm_v_heads, qkvd = (2 * (int64_t)c.ssm_k_heads + nvh) * hd;
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  std::vector<float> tr((size_t)(nvh * hd * hd));
+  DZ_HIP_CHECK(hipMemcpy(tr.data(), x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, tr.size() * 4, hipMemcpyDeviceToHost));
+  if (state)
+    for (int64_t v = 0; v < nvh; ++v)
+      for (int64_t i = 0; i < hd; ++i)
+        for (int64_t j = 0; j < hd; ++j) state[(size_t)((v * hd + i) * hd + j)] = tr[(size_t)((v * hd + j) * hd + i)];
+  if (conv_hist)
+    DZ_HIP_CHECK(hipMemcpy(conv_hist, x->conv + (size_t)l->kind_idx * 4 * qkvd, (size_t)(4 * qkvd) * 4, hipMemcpyDeviceToHost));
+  if (conv_head) *conv_head = (x->ring_base[l->kind_idx] + x->pos_host) & 3;
+  return DZ_OK;
+}
+
+int dz_ctx_set_kv(dz_ctx* x, int layer, const float* k, const float* v, int len) {
+  LayerDev* l;
+  int rc = layer_of(x, layer, true, &l);
+  if (rc) return rc;
+  const dz_config& c = x->m->cfg;
+  if (len < 0 || len > c.max_ctx) return set_error(DZ_ERR_TENSOR, "kv len %d", len);
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim, hd = (size_t)c.head_dim;
+  float* kb = x->kv + (size_t)l->kind_idx * 2 * kvsz;
+  for (int h = 0; h < c.n_head_kv; ++h) {
+    DZ_HIP_CHECK(hipMemcpy(kb + (size_t)h * c.max_ctx * hd, k + (size_t)h * len * hd, (size_t)len * hd * 4, hipMemcpyHostToDevice));
+    DZ_HIP_CHECK(hipMemcpy(kb + kvsz + (size_t)h * c.max_ctx * hd, v + (size_t)h * len * hd, (size_t)len * hd * 4,
+                           hipMemcpyHostToDevice));
+  }
+  return DZ_OK;
+}
+
+int dz_ctx_get_kv(dz_ctx* x, int layer, float* k, float* v, int len) {
+  LayerDev* l;
+  int rc = layer_of(x, layer, true, &l);
+  if (rc) return rc;
+  const dz_config& c = x->m->cfg;
+  if (len < 0 || len > c.max_ctx) return set_error(DZ_ERR_TENSOR, "kv len %d", len);
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim, hd = (size_t)c.head_dim;
+  const float* kb = x->kv + (size_t)l->kind_idx * 2 * kvsz;
+  for (int h = 0; h < c.n_head_kv; ++h) {
+    DZ_HIP_CHECK(hipMemcpy(k + (size_t)h * len * hd, kb + (size_t)h * c.max_ctx * hd, (size_t)len * hd * 4, hipMemcpyDeviceToHost));
+    DZ_HIP_CHECK(hipMemcpy(v + (size_t)h * len * hd, kb + kvsz + (size_t)h * c.max_ctx * hd, (size_t)len * hd * 4,
+                           hipMemcpyDeviceToHost));
+  }
+  return DZ_OK;
+}
+
+// In this build every attention layer holds exactly `pos` cached positions.
+int dz_ctx_kv_len(dz_ctx* x, int layer) {
+  LayerDev* l;
+  if (layer_of(x, layer, true, &l)) return -1;
+  return x->pos_host;
+}
+
+int dz_kv_truncate(dz_ctx* x, int len) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (len >= x->pos_host) return DZ_OK;  // KvCache::truncate keeps longer requests as no-ops
+  if (len < 0) return set_error(DZ_ERR_TENSOR, "truncate to %d", len);
+  return ctx_set_pos_dev(x, len);
+}
+
+int dz_ctx_set_pos(dz_ctx* x, int pos) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (pos < 0 || pos >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "pos %d out of [0, max_ctx)", pos);
+  // ring heads are stored relative to pos: keep each layer's physical head unchanged
+  const int old = x->pos_host;
+  for (size_t i = 0; i < x->ring_base.size(); ++i) x->ring_base[i] = ((x->ring_base[i] + old - pos) % 4 + 4) % 4;
+  if (!x->ring_base.empty())
+    DZ_HIP_CHECK(hipMemcpy(x->ring_base_dev, x->ring_base.data(), x->ring_base.size() * 4, hipMemcpyHostToDevice));
+  return ctx_set_pos_dev(x, pos);
+}
+
+int dz_ctx_mixer_step(dz_ctx* x, int layer, float* h) {
+  if (!x || !h) return set_error(DZ_ERR_MODEL, "null argument");
+  if (layer < 0 || layer >= x->m->cfg.n_layers) return set_error(DZ_ERR_TENSOR, "layer %d out of range", layer);
+  if (x->pos_host >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "context full");
+  const dz_config& c = x->m->cfg;
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(x->m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int P = x->pos_host;
+  // this token's position: TokState.pos = P, pos_next = P + 1
+  int pp[1] = {P};
+  DZ_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos), pp, 4, hipMemcpyHostToDevice, x->s));
+  DZ_HIP_CHECK(hipMemcpyAsync(x->h[1], h, (size_t)c.hidden * 4, hipMemcpyHostToDevice, x->s));
+  int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s);
+  if (rc) return rc;
+  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden};
+  hipLaunchKernelGGL(final_reduce_kernel, dim3((unsigned)th), dim3(512), 0, x->s, fa);
+  DZ_HIP_CHECK(hipGetLastError());
+  DZ_HIP_CHECK(hipMemcpyAsync(h, x->h_fin, (size_t)c.hidden * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return ctx_set_pos_dev(x, P + 1);
+}
+
+}  // extern "C"

@@ -1,0 +1,701 @@
+// model_kernels.h — device side of the per-token forward (forward_single_token, forward.rs:204-375).
+//
+// One token is a fixed sequence of kernels (captured once in a hipGraph):
+//   select_token -> per layer { GEMV(norm+in-proj) -> DeltaNet | attention -> GEMV(out-proj)
+//                              -> GEMV(norm+gate/up) -> GEMV(swiglu+down) } -> final_reduce -> lm_head.
+// GEMV kernels write split-K partials part[tile][row]; the consumer of a GEMV sums its tiles in
+// order 0..T-1 while staging its own inputs, so no reduction kernel sits between phases.  The
+// residual stream h is materialised tile by tile by the chunk-0 workgroup of each consuming GEMV
+// (double buffered), together with that tile's sum of squares; RMSNorm's 1/rms is applied to
+// the GEMV result (y = inv * W(h*w), equal to W((h*inv)*w) up to rounding).
+#pragma once
+#include "q1_gemv.h"
+
+namespace dz {
+
+// Position/token bookkeeping of the token being processed (device resident).
+struct TokState {
+  int pos;        // position of this token
+  int token;      // its id
+  int feed_len;   // host-fed ids remaining in `feed` are consumed first
+  int feed_idx;
+  int pos_next;   // position the next token will take
+  int pad[3];
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Deterministic block sum (wave sums, then wave order).  All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red, unsigned tid, int nt) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((tid & 63u) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < nt / 64; ++w) s += red[w];
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
+
+// inverse RMS of a vector whose per-tile sums of squares are ss[0..nt) (rmsnorm.rs:53-55)
+__device__ __forceinline__ float inv_rms_from(const float* ss, int nss, int64_t n, float eps) {
+  float s = 0.f;
+  for (int i = 0; i < nss; ++i) s += ss[i];
+  return 1.0f / sqrtf(s / (float)n + eps);
+}
+
+// ---------------------------------------------------------------- GEMV sources
+
+// LUT input (h + sum_k part_k) * w; chunk 0 also writes h_out and the tile's sum of squares.
+struct ResidSrc {
+  const float* h_in;
+  const float* part;
+  int np;
+  int64_t ldp;
+  const float* w;
+  float* h_out;
+  float* ss_out;
+  int64_t H;
+  __device__ __forceinline__ void stage(float* xs, float* red, int t, unsigned tid, int nt, int64_t chunk) const {
+    float ssl = 0.f;
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      float u = 0.f;
+      if (col < H) {
+        float d = 0.f;
+        for (int k = 0; k < np; ++k) d += part[(size_t)k * ldp + col];
+        const float v = np ? h_in[col] + d : h_in[col];
+        u = v * w[col];
+        if (chunk == 0) h_out[col] = v;
+        ssl = __builtin_fmaf(v, v, ssl);
+      }
+      xs[i] = u;
+    }
+    if (chunk == 0) {
+      const float s = block_sum(ssl, red, tid, nt);
+      if (tid == 0) ss_out[t] = s;
+    }
+  }
+};
+
+// LUT input silu(g) * u with g, u = inv_rms * sum of gate/up partials (swiglu_inplace_simd, simd_exp.rs:273-296).
+struct SwigluSrc {
+  const float* part;  // [np][ldp]: gate rows [0, F), up rows [F, 2F)
+  int np;
+  int64_t ldp;
+  int64_t F;
+  const float* ss;
+  int nss;
+  int64_t H;
+  float eps;
+  __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
+    const float inv = inv_rms_from(ss, nss, H, eps);
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      float u = 0.f;
+      if (col < F) {
+        float g = 0.f, up = 0.f;
+        for (int k = 0; k < np; ++k) {
+          g += part[(size_t)k * ldp + col];
+          up += part[(size_t)k * ldp + F + col];
+        }
+        g *= inv;
+        up *= inv;
+        u = siluf_(g) * up;
+      }
+      xs[i] = u;
+    }
+  }
+};
+
+// LUT input of the DeltaNet out-projection: per v-head RMSNorm * weight * silu(z)
+// (Qwen3NextRMSNormGated, ssm_output_gate_avx2 in model/ssm.rs:246-286).
+struct GatedYSrc {
+  const float* y;
+  const float* zs;
+  const float* nw;  // [128]
+  int64_t K;        // v_heads * 128
+  float eps;
+  __device__ __forceinline__ void stage(float* xs, float* red, int t, unsigned tid, int nt, int64_t) const {
+    // 512 columns = 4 heads of 128; wave h (< 4) reduces head h
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      xs[i] = col < K ? y[col] : 0.f;
+    }
+    __syncthreads();
+    const unsigned w = tid >> 6, l = tid & 63u;
+    if (w < 4) {
+      const float a = xs[w * 128 + l], b = xs[w * 128 + 64 + l];
+      const float s = wave_sum(__builtin_fmaf(a, a, b * b));
+      if (l == 0) red[w] = 1.0f / sqrtf(s * (1.0f / 128.0f) + eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      xs[i] = col < K ? ((xs[i] * red[i >> 7]) * nw[i & 127]) * zs[col] : 0.f;
+    }
+  }
+};
+
+// LUT input of the attention out-projection: combine the split-K softmax partials of the head
+// and gate with sigmoid (attention.rs:189-203).  Partial record: [m, l, o[head_dim]].
+struct AttnOutSrc {
+  const float* apart;  // [n_head][gmax][2 + hd]
+  int gmax;
+  int hd;
+  int64_t K;          // n_head * hd
+  const TokState* st;
+  const float* p_in;  // qkv partials (gate half of each q-head)
+  int np;
+  int64_t ldp;
+  const float* ss;
+  int nss;
+  int64_t H;
+  float eps;
+  __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
+    const int ctx = st->pos + 1;
+    int chunk = (ctx + gmax - 1) / gmax;
+    if (chunk < 16) chunk = 16;
+    const int geff = (ctx + chunk - 1) / chunk;
+    const float inv = inv_rms_from(ss, nss, H, eps);
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      float u = 0.f;
+      if (col < K) {
+        const int h = (int)(col / hd), d = (int)(col % hd);
+        const float* rec = apart + (size_t)h * gmax * (2 + hd);
+        float M = -INFINITY;
+        for (int g = 0; g < geff; ++g) M = fmaxf(M, rec[(size_t)g * (2 + hd)]);
+        float l = 0.f, o = 0.f;
+        for (int g = 0; g < geff; ++g) {
+          const float* r = rec + (size_t)g * (2 + hd);
+          const float e = expf(r[0] - M);
+          l = __builtin_fmaf(r[1], e, l);
+          o = __builtin_fmaf(r[2 + d], e, o);
+        }
+        float gate = 0.f;
+        const int64_t grow = (int64_t)h * 2 * hd + hd + d;
+        for (int k = 0; k < np; ++k) gate += p_in[(size_t)k * ldp + grow];
+        gate *= inv;
+        u = (o * (1.0f / l)) * sigmoidf_(gate);
+      }
+      xs[i] = u;
+    }
+  }
+};
+
+// LUT input (h * inv_rms) * w with h already final (output norm before lm_head, forward.rs:332).
+struct NormedSrc {
+  const float* h;
+  const float* w;
+  const float* ss;
+  int nss;
+  int64_t H;
+  float eps;
+  __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
+    const float inv = inv_rms_from(ss, nss, H, eps);
+    for (int i = tid; i < kTileCols; i += nt) {
+      const int64_t col = (int64_t)t * kTileCols + i;
+      xs[i] = col < H ? (h[col] * inv) * w[col] : 0.f;
+    }
+  }
+};
+
+// ---------------------------------------------------------------- GEMV destinations
+
+// (value, index) order of greedy argmax: larger value wins, equal values keep the lower index,
+// NaN never wins (argmax_avx2 compares with `>`, simd_exp.rs:551-598).
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (am_better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// Final logits plus one (max, first index) per row-block for greedy argmax.
+struct LogitsDst {
+  float* logits;
+  int64_t V;
+  float* am_val;  // [nrb]
+  int* am_idx;
+  __device__ __forceinline__ void store(int, int64_t rb, unsigned lane, float v) const {
+    const int64_t row = rb * kRowBlock + lane;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    if (row < V) {
+      logits[row] = v;
+      bv = v;
+      bi = (int)row;
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) {
+      am_val[rb] = bv;
+      am_idx[rb] = bi;
+    }
+  }
+};
+
+// ---------------------------------------------------------------- token selection
+
+struct SelectArgs {
+  TokState* st;
+  const int* feed;      // host-fed token ids (prompt / forced tokens)
+  const float* am_val;  // argmax partials of the previous lm_head
+  const int* am_idx;
+  int n_am;
+  int* toklog;          // toklog[pos] = token consumed at pos
+  // embedding row -> emb_out (f32): f16 table, or Q1_0 GEMV layout with the reference's dequant
+  const uint16_t* emb_f16;
+  const uint8_t* emb_q1;
+  int64_t emb_ntiles;
+  int64_t H;
+  float* emb_out;
+  int commit;           // 1: consume the token (advance pos); 0: only publish the argmax to toklog[pos_next]
+};
+
+__device__ __forceinline__ float ref_f16_to_f32_dev(unsigned bits) {
+  const unsigned sign = (bits >> 15) & 1u, exp = (bits >> 10) & 0x1Fu, mant = bits & 0x3FFu;
+  const unsigned s32 = sign << 31;
+  unsigned out;
+  if (exp == 0) {
+    if (mant == 0) {
+      out = s32;
+    } else {
+      unsigned m = mant, e = 1;
+      while ((m & 0x400u) == 0) { m <<= 1; ++e; }
+      out = s32 | ((112u + e) << 23) | ((m & 0x3FFu) << 13);
+    }
+  } else if (exp == 0x1F) {
+    out = s32 | 0x7F800000u | (mant << 13);
+  } else {
+    out = s32 | ((exp + 112u) << 23) | (mant << 13);
+  }
+  return __builtin_bit_cast(float, out);
+}
+
+// One workgroup: pick the next token (host feed first, else argmax of the last logits),
+// bump the position and write its embedding row (forward.rs:212-213).
+__global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  __shared__ int tok_s;
+  const unsigned tid = threadIdx.x;
+  TokState* st = a.st;
+  const bool fed = a.commit && st->feed_idx < st->feed_len;
+  if (!fed) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = tid; i < a.n_am; i += blockDim.x)
+      if (am_better(a.am_val[i], a.am_idx[i], bv, bi)) { bv = a.am_val[i]; bi = a.am_idx[i]; }
+    wave_argmax(bv, bi);
+    if ((tid & 63u) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+      for (unsigned w = 1; w < blockDim.x / 64; ++w)
+        if (am_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+      tok_s = bi == 0x7FFFFFFF ? 0 : bi;
+    }
+  } else if (tid == 0) {
+    tok_s = a.feed[st->feed_idx];
+  }
+  __syncthreads();
+  const int tok = tok_s;
+  if (!a.commit) {
+    if (tid == 0) a.toklog[st->pos_next] = tok;
+    return;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (fed) st->feed_idx += 1;
+    st->pos = st->pos_next;
+    st->pos_next += 1;
+    st->token = tok;
+    a.toklog[st->pos] = tok;
+  }
+  if (a.emb_f16) {
+    const uint16_t* row = a.emb_f16 + (size_t)tok * a.H;
+    for (int64_t c = tid; c < a.H; c += blockDim.x)
+      a.emb_out[c] = (float)__builtin_bit_cast(_Float16, row[c]);
+  } else {
+    // dequantize_q1_0_row_into (quant.rs:161-194) from the GEMV layout
+    const int64_t rb = tok / kRowBlock;
+    const unsigned L = (unsigned)(tok % kRowBlock);
+    for (int64_t k = tid; k < a.H; k += blockDim.x) {
+      const int t = (int)(k / kTileCols);
+      const unsigned p = (unsigned)((k % kTileCols) / 8), j = (unsigned)(k % 8), s = L ^ p;
+      const uint8_t* u = a.emb_q1 + ((size_t)rb * a.emb_ntiles + t) * kUnitBytes;
+      const unsigned byte = u[((s >> 4) * 64 + L) * 16 + (s & 15)];
+      const uint16_t* scp = reinterpret_cast<const uint16_t*>(u + kUnitSignBytes);
+      const float scale = ref_f16_to_f32_dev(scp[L * 4 + ((p >> 4) ^ (L >> 4))]);
+      a.emb_out[k] = ((float)((byte >> j) & 1u) * 2.0f - 1.0f) * scale;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- Gated DeltaNet step
+
+struct DeltaArgs {
+  const TokState* st;
+  const float* p_in;  // in-proj partials [np][ldp]: rows [qkv | z | alpha | beta]
+  int np;
+  int64_t ldp;
+  const float* ss;    // sums of squares of the layer input, per tile
+  int nss;
+  int64_t H;
+  float rms_eps;
+  float* conv;        // ring [4][qkvd]
+  const int* ring_base_ptr;  // ring head at pos 0 (mod 4) of this layer
+  const float* conv_w;  // [4][qkvd] (tap-major, tap 3 = newest)
+  const float* ssm_a;   // [nvh]
+  const float* dt_bias; // [nvh]
+  float* state;         // [nvh][128 j][128 i]
+  float* y;             // [nvh*128] raw readout
+  float* zs;            // [nvh*128] silu(z)
+  int nkh, nvh;
+  int64_t qkvd, off_z, off_a, off_b;
+};
+
+// One workgroup per (v-head, quarter of its 128 rows); 256 threads = 32 rows x 8 slices of k.
+// Follows ssm_forward_into (model/ssm.rs:465-574): conv ring + causal conv (kernel 4) + SiLU,
+// per-head L2 norm of q/k, q *= 1/sqrt(128), g = A*softplus(alpha + dt_bias), decay = exp(g),
+// beta = sigmoid(b), then for each state row i: s *= decay; kv = s.k; d = (v_i - kv)*beta;
+// s += d*k; y_i = s.q.  k-head of v-head vh is vh % nkh (ssm.rs:558-561).
+__global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
+  constexpr int HD = 128;
+  __shared__ float qs[HD], ks[HD], vs[32], red[16], part[8][32], dsh[32], sc[4];
+  const unsigned tid = threadIdx.x;
+  const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % a.nkh;
+  const int i_loc = tid & 31, js = tid >> 5;
+  const int pos = a.st->pos;
+  const int hb = (*a.ring_base_ptr + pos) & 3;  // ring head before this token = slot of the new value
+  const float inv = inv_rms_from(a.ss, a.nss, a.H, a.rms_eps);
+  const int64_t kdim = (int64_t)a.nkh * HD;
+
+  auto proj = [&](int64_t row) {
+    float d = 0.f;
+    for (int k = 0; k < a.np; ++k) d += a.p_in[(size_t)k * a.ldp + row];
+    return d * inv;
+  };
+  auto conv_silu = [&](int64_t ch, bool write) {
+    const float xn = proj(ch);
+    const float* w = a.conv_w;
+    float o = 0.f;
+    o = __builtin_fmaf(a.conv[(size_t)((hb + 1) & 3) * a.qkvd + ch], w[ch], o);
+    o = __builtin_fmaf(a.conv[(size_t)((hb + 2) & 3) * a.qkvd + ch], w[a.qkvd + ch], o);
+    o = __builtin_fmaf(a.conv[(size_t)((hb + 3) & 3) * a.qkvd + ch], w[2 * a.qkvd + ch], o);
+    o = __builtin_fmaf(xn, w[3 * a.qkvd + ch], o);
+    if (write) a.conv[(size_t)hb * a.qkvd + ch] = xn;
+    return siluf_(o);
+  };
+
+  // q (threads 0..127) and k (threads 128..255) of k-head kh; v for this quarter's 32 rows
+  const bool owner = (vh < a.nkh) && quarter == 0;  // writes the shared q/k ring channels
+  float qk;
+  if (tid < HD) qk = conv_silu((int64_t)kh * HD + tid, owner);
+  else qk = conv_silu(kdim + (int64_t)kh * HD + (tid - HD), owner);
+  if (tid < 32) vs[tid] = conv_silu(2 * kdim + (int64_t)vh * HD + quarter * 32 + tid, true);
+  // L2 norms (ssm.rs:523-530): two 128-wide reductions, waves 0-1 for q and 2-3 for k
+  const float s2 = wave_sum(qk * qk);
+  if ((tid & 63u) == 0) red[tid >> 6] = s2;
+  __syncthreads();
+  if (tid < HD) {
+    const float inq = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
+    qs[tid] = (qk * inq) * (1.0f / sqrtf((float)HD));
+  } else {
+    const float ink = 1.0f / sqrtf((red[2] + red[3]) + 1e-6f);
+    ks[tid - HD] = qk * ink;
+  }
+  if (tid == 0) {
+    const float al = proj(a.off_a + vh), be = proj(a.off_b + vh);
+    const float x = al + a.dt_bias[vh];
+    const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
+    sc[0] = expf(a.ssm_a[vh] * sp);  // decay
+    sc[1] = sigmoidf_(be);            // beta
+  }
+  if (tid >= 64 && tid < 96) {
+    const int r = tid - 64;
+    const int64_t zi = (int64_t)vh * HD + quarter * 32 + r;
+    a.zs[zi] = siluf_(proj(a.off_z + zi));
+  }
+  __syncthreads();
+
+  // recurrence on rows i = 32*quarter + i_loc, k-slice j in [16*js, 16*js+16)
+  const float decay = sc[0], beta = sc[1];
+  const int i = quarter * 32 + i_loc;
+  float* S = a.state + (size_t)vh * HD * HD;
+  float s[16];
+  float kvp = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const int j = js * 16 + jj;
+    s[jj] = S[(size_t)j * HD + i] * decay;
+    kvp = __builtin_fmaf(s[jj], ks[j], kvp);
+  }
+  part[js][i_loc] = kvp;
+  __syncthreads();
+  if (js == 0) {
+    float kv = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) kv += part[q][i_loc];
+    dsh[i_loc] = (vs[i_loc] - kv) * beta;
+  }
+  __syncthreads();
+  const float d = dsh[i_loc];
+  float yp = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const int j = js * 16 + jj;
+    s[jj] = __builtin_fmaf(d, ks[j], s[jj]);
+    S[(size_t)j * HD + i] = s[jj];
+    yp = __builtin_fmaf(s[jj], qs[j], yp);
+  }
+  __syncthreads();
+  part[js][i_loc] = yp;
+  __syncthreads();
+  if (js == 0) {
+    float yy = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) yy += part[q][i_loc];
+    a.y[(size_t)vh * HD + i] = yy;
+  }
+}
+
+// ---------------------------------------------------------------- gated GQA attention (split-K)
+
+struct AttnArgs {
+  const TokState* st;
+  const float* p_in;  // qkv partials: rows [q+gate interleaved per head (n_head*2*hd) | k | v]
+  int np;
+  int64_t ldp;
+  const float* ss;
+  int nss;
+  int64_t H;
+  float eps;
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope;  // [max_ctx][rope_dim]: cos[0..half) sin[half..rope_dim)
+  int rope_dim;
+  float* kcache;      // [nkv][max_ctx][hd]
+  float* vcache;
+  int max_ctx;
+  float* apart;       // [n_head][gmax][2+hd]
+  int gmax;
+  int nq, nkv;
+};
+
+// Workgroup (kv-head, chunk g) runs the online softmax of attention.rs:124-199 over positions
+// [g*chunk, (g+1)*chunk) for the kv-head's n_head/n_kv query heads (grouped GQA: q-head
+// kvh*grp + gi, attention.rs:163-165) and writes (m, l, o) per q-head.  q/k get RMSNorm with
+// q_norm/k_norm, then the reference's partial RoPE on the first rope_dim dims with both terms
+// added (rope.rs:205-208), and q *= 1/sqrt(hd).  The chunk holding the new position also appends
+// its k/v to the cache.  hd = 256, 256 threads (4 waves).
+template <int GRP>
+__global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
+  constexpr int HD = 256;
+  __shared__ float qs[GRP][HD];
+  __shared__ float kn[HD], vn[HD];
+  __shared__ float red[GRP + 1][4];
+  __shared__ float wm[4][GRP], wl[4][GRP];
+  __shared__ float wo[4][GRP][HD];
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const int kvh = blockIdx.x / a.gmax, g = blockIdx.x % a.gmax;
+  const int P = a.st->pos, ctx = P + 1;
+  int chunk = (ctx + a.gmax - 1) / a.gmax;
+  if (chunk < 16) chunk = 16;
+  const int geff = (ctx + chunk - 1) / chunk;
+  if (g >= geff) return;
+  const int p0 = g * chunk, p1 = min(ctx, p0 + chunk);
+  const bool has_new = p1 == ctx;
+  const float inv = inv_rms_from(a.ss, a.nss, a.H, a.eps);
+  const int half = a.rope_dim / 2;
+  const float* cs = a.rope + (size_t)P * a.rope_dim;
+
+  auto proj = [&](int64_t row) {
+    float d = 0.f;
+    for (int k = 0; k < a.np; ++k) d += a.p_in[(size_t)k * a.ldp + row];
+    return d * inv;
+  };
+  // raw q of the group's heads, one dim per thread
+  float qv[GRP];
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) qv[gi] = proj((int64_t)(kvh * GRP + gi) * 2 * HD + tid);
+  float kvv = 0.f, vvv = 0.f;
+  if (has_new) {
+    kvv = proj((int64_t)a.nq * 2 * HD + (int64_t)kvh * HD + tid);
+    vvv = proj((int64_t)a.nq * 2 * HD + (int64_t)a.nkv * HD + (int64_t)kvh * HD + tid);
+  }
+  // per-head RMSNorm over 256 dims (rmsnorm_inplace, rmsnorm.rs:158-176)
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    const float sq = wave_sum(qv[gi] * qv[gi]);
+    if (lane == 0) red[gi][wave] = sq;
+  }
+  {
+    const float sq = wave_sum(kvv * kvv);
+    if (lane == 0) red[GRP][wave] = sq;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    const float ssum = (red[gi][0] + red[gi][1]) + (red[gi][2] + red[gi][3]);
+    const float in = 1.0f / sqrtf(ssum / (float)HD + a.eps);
+    qs[gi][tid] = (qv[gi] * in) * a.q_norm[tid];
+  }
+  if (has_new) {
+    const float ssum = (red[GRP][0] + red[GRP][1]) + (red[GRP][2] + red[GRP][3]);
+    const float in = 1.0f / sqrtf(ssum / (float)HD + a.eps);
+    kn[tid] = (kvv * in) * a.k_norm[tid];
+    vn[tid] = vvv;
+  }
+  __syncthreads();
+  // RoPE on dims [0, rope_dim): pairs (d, d+half); thread d < half rotates the pair
+  float r1[GRP], r2[GRP];
+  float kr1 = 0.f, kr2 = 0.f;
+  if ((int)tid < half) {
+    const float c = cs[tid], sn = cs[half + tid];
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      const float x1 = qs[gi][tid], x2 = qs[gi][tid + half];
+      r1[gi] = __builtin_fmaf(x1, c, x2 * sn);
+      r2[gi] = __builtin_fmaf(x2, c, x1 * sn);
+    }
+    if (has_new) {
+      const float x1 = kn[tid], x2 = kn[tid + half];
+      kr1 = __builtin_fmaf(x1, c, x2 * sn);
+      kr2 = __builtin_fmaf(x2, c, x1 * sn);
+    }
+  }
+  __syncthreads();
+  if ((int)tid < half) {
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      qs[gi][tid] = r1[gi];
+      qs[gi][tid + half] = r2[gi];
+    }
+    if (has_new) {
+      kn[tid] = kr1;
+      kn[tid + half] = kr2;
+    }
+  }
+  __syncthreads();
+  const float qscale = 1.0f / sqrtf((float)HD);
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) qs[gi][tid] *= qscale;
+  if (has_new) {
+    a.kcache[((size_t)kvh * a.max_ctx + P) * HD + tid] = kn[tid];
+    a.vcache[((size_t)kvh * a.max_ctx + P) * HD + tid] = vn[tid];
+  }
+  __syncthreads();
+
+  // online softmax over this wave's positions; lane holds dims 4*lane .. 4*lane+3
+  float m[GRP], l[GRP];
+  float4 o[GRP], q4[GRP];
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    m[gi] = -INFINITY;
+    l[gi] = 0.f;
+    o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+    q4[gi] = *reinterpret_cast<const float4*>(&qs[gi][4 * lane]);
+  }
+  const float* kb = a.kcache + (size_t)kvh * a.max_ctx * HD;
+  const float* vb = a.vcache + (size_t)kvh * a.max_ctx * HD;
+  for (int p = p0 + (int)wave; p < p1; p += 4) {
+    float4 k4, v4;
+    if (p == P) {
+      k4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
+      v4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
+    } else {
+      k4 = *reinterpret_cast<const float4*>(kb + (size_t)p * HD + 4 * lane);
+      v4 = *reinterpret_cast<const float4*>(vb + (size_t)p * HD + 4 * lane);
+    }
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      float dp = q4[gi].x * k4.x;
+      dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
+      dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
+      dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
+      const float score = wave_sum(dp);
+      const float mn = fmaxf(m[gi], score);
+      const float al = expf(m[gi] - mn), be = expf(score - mn);
+      l[gi] = l[gi] * al + be;
+      o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
+      o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
+      o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
+      o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
+      m[gi] = mn;
+    }
+  }
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    if (lane == 0) {
+      wm[wave][gi] = m[gi];
+      wl[wave][gi] = l[gi];
+    }
+    *reinterpret_cast<float4*>(&wo[wave][gi][4 * lane]) = o[gi];
+  }
+  __syncthreads();
+  // merge the 4 waves (a wave without positions has l = 0) and write each q-head's chunk record
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][gi]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      const float e = wl[w][gi] > 0.f ? expf(wm[w][gi] - M) : 0.f;
+      L = __builtin_fmaf(wl[w][gi], e, L);
+      O = __builtin_fmaf(wo[w][gi][tid], e, O);
+    }
+    float* rec = a.apart + ((size_t)(kvh * GRP + gi) * a.gmax + g) * (2 + HD);
+    if (tid == 0) {
+      rec[0] = M;
+      rec[1] = L;
+    }
+    rec[2 + tid] = O;
+  }
+}
+
+// h = h_in + sum_k part_k tile by tile with the tile's sum of squares (the output norm's input).
+struct FinalArgs {
+  const float* h_in;
+  const float* part;
+  int np;
+  int64_t ldp;
+  float* h_out;
+  float* ss_out;
+  int64_t H;
+};
+
+__global__ __launch_bounds__(512) void final_reduce_kernel(const FinalArgs a) {
+  __shared__ float red[16];
+  const int t = blockIdx.x;
+  const unsigned tid = threadIdx.x;
+  const int64_t col = (int64_t)t * kTileCols + tid;
+  float v = 0.f;
+  if (col < a.H) {
+    float d = 0.f;
+    for (int k = 0; k < a.np; ++k) d += a.part[(size_t)k * a.ldp + col];
+    v = a.h_in[col] + d;
+    a.h_out[col] = v;
+  }
+  const float s = block_sum(v * v, red, tid, 512);
+  if (tid == 0) a.ss_out[t] = s;
+}
+
+}  // namespace dz

@@ -1,0 +1,406 @@
+// q1_mat.hip — Q1_0 matrices on the device: upload/repack, dequant, and the matrix-level
+// C ABI (Q1_0Matrix::{from_gguf, row_into_slice, matvec_into_slice, matvec_add_into_slice,
+// matvec_multi_into_slice}, Daiza-engine/src/model/weights.rs:83-972).
+#include "runtime.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+struct dz_mat {
+  dz::Q1Dev d;
+};
+
+namespace dz {
+
+// ------------------------------------------------------------------ errors / device
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+static std::mutex g_mu;
+
+int ensure_device() {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_device >= 0) {
+    DZ_HIP_CHECK(hipSetDevice(g_device));
+    return DZ_OK;
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return set_error(DZ_ERR_DEVICE, "no HIP device visible");
+  hipDeviceProp_t prop;
+  DZ_HIP_CHECK(hipGetDeviceProperties(&prop, 0));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_error(DZ_ERR_DEVICE, "device 0 is %s; this library is built for gfx950 only", prop.gcnArchName);
+  DZ_HIP_CHECK(hipSetDevice(0));
+  DZ_HIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  g_device = 0;
+  return DZ_OK;
+}
+
+hipStream_t lib_stream() { return g_stream; }
+
+int Scratch::reserve(size_t n) {
+  if (n <= bytes) return DZ_OK;
+  if (ptr) DZ_HIP_CHECK(hipFree(ptr));
+  ptr = nullptr;
+  bytes = 0;
+  size_t want = n + (n >> 2);
+  DZ_HIP_CHECK(hipMalloc(&ptr, want));
+  bytes = want;
+  return DZ_OK;
+}
+
+// ------------------------------------------------------------------ kernels
+
+// AoS blocks -> GEMV layout.  One 64-thread block per (row-block, tile) unit; lane = row in block.
+__global__ __launch_bounds__(64) void repack_kernel(const uint8_t* __restrict__ aos, int64_t rows, int64_t cols,
+                                                    int64_t ntiles, uint8_t* __restrict__ out) {
+  const int64_t unit = blockIdx.x;
+  const unsigned L = threadIdx.x;
+  const int64_t rb = unit / ntiles;
+  const int t = (int)(unit % ntiles);
+  const int64_t row = rb * kRowBlock + L;
+  const int64_t gpr = cols / kGroup;
+  uint8_t* u = out + (size_t)unit * kUnitBytes;
+  const bool live = row < rows;
+  const uint8_t* rowp = aos + (size_t)(live ? row : 0) * gpr * kBlockBytes;
+  for (int c = 0; c < 4; ++c) {
+    unsigned w[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 16; ++i) {
+      const unsigned s = 16u * c + i, p = L ^ s;
+      const int64_t g = 4 * t + (p >> 4);
+      unsigned byte = 0;
+      if (live && g < gpr) byte = rowp[g * kBlockBytes + 2 + (p & 15)];
+      w[i >> 2] |= byte << (8 * (i & 3));
+    }
+    u32x4 v = {w[0], w[1], w[2], w[3]};
+    reinterpret_cast<u32x4*>(u)[c * 64 + L] = v;
+  }
+  unsigned sc[2] = {0, 0};
+  for (int j = 0; j < 4; ++j) {
+    const int64_t g = 4 * t + ((L >> 4) ^ j);
+    unsigned bits = 0;
+    if (live && g < gpr) bits = rowp[g * kBlockBytes] | (rowp[g * kBlockBytes + 1] << 8);
+    sc[j >> 1] |= bits << (16 * (j & 1));
+  }
+  u32x2 v2 = {sc[0], sc[1]};
+  reinterpret_cast<u32x2*>(u + kUnitSignBytes)[L] = v2;
+}
+
+// Daiza-engine/src/tensor/quant.rs:39-74 f16_to_f32, bit for bit.  Note: for a subnormal half the
+// reference adds the normalisation shift count to the exponent (127 - 15 + e) where IEEE would
+// subtract it, so subnormal scales dequantise larger than IEEE; the GEMV path uses the exact
+// hardware conversion, as the reference's _mm256_cvtph_ps does (quant.rs:649-660).
+__device__ __forceinline__ float ref_f16_to_f32(unsigned bits) {
+  const unsigned sign = (bits >> 15) & 1u, exp = (bits >> 10) & 0x1Fu, mant = bits & 0x3FFu;
+  const unsigned s32 = sign << 31;
+  unsigned out;
+  if (exp == 0) {
+    if (mant == 0) {
+      out = s32;
+    } else {
+      unsigned m = mant, e = 1;
+      while ((m & 0x400u) == 0) { m <<= 1; ++e; }
+      out = s32 | ((112u + e) << 23) | ((m & 0x3FFu) << 13);
+    }
+  } else if (exp == 0x1F) {
+    out = s32 | 0x7F800000u | (mant << 13);
+  } else {
+    out = s32 | ((exp + 112u) << 23) | (mant << 13);
+  }
+  return __builtin_bit_cast(float, out);
+}
+
+// dequantize_q1_0_row_into (quant.rs:161-194) from the GEMV layout: w = (bit*2 - 1) * scale.
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ data, int64_t cols, int64_t ntiles,
+                                                      int64_t r0, int64_t nrows, float* __restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= nrows * cols) return;
+  const int64_t row = r0 + i / cols, k = i % cols;
+  const int64_t rb = row / kRowBlock;
+  const unsigned L = (unsigned)(row % kRowBlock);
+  const int t = (int)(k / kTileCols);
+  const unsigned p = (unsigned)((k % kTileCols) / 8), j = (unsigned)(k % 8);
+  const unsigned s = L ^ p;
+  const uint8_t* u = data + ((size_t)rb * ntiles + t) * kUnitBytes;
+  const unsigned byte = u[((s >> 4) * 64 + L) * 16 + (s & 15)];
+  const unsigned slot = (p >> 4) ^ (L >> 4);
+  const uint16_t* scp = reinterpret_cast<const uint16_t*>(u + kUnitSignBytes);
+  const float scale = ref_f16_to_f32(scp[L * 4 + slot]);
+  const float bit = (float)((byte >> j) & 1u);
+  out[i] = (bit * 2.0f - 1.0f) * scale;
+}
+
+// y = [y +] sum over tile groups of part[tg][vrow], tile-group order 0..n_tg-1.
+struct ReduceArgs {
+  ReduceSeg seg[8];
+  int nseg;
+  const float* part;
+  int64_t ld;
+  int n_tg;
+  int accumulate;
+};
+
+__global__ __launch_bounds__(256) void partial_reduce_kernel(const ReduceArgs a) {
+  const int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  int s = 0;
+  while (s + 1 < a.nseg && v >= a.seg[s + 1].vrow_begin) ++s;
+  const int64_t r = v - a.seg[s].vrow_begin;
+  if (r < 0 || r >= a.seg[s].rows) return;
+  float acc = a.part[v];
+  for (int tg = 1; tg < a.n_tg; ++tg) acc += a.part[(size_t)tg * a.ld + v];
+  float* y = a.seg[s].y + r;
+  *y = a.accumulate ? *y + acc : acc;
+}
+
+hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const ReduceSeg* segs, int nseg,
+                                 int accumulate, hipStream_t s) {
+  ReduceArgs a;
+  memset(&a, 0, sizeof a);
+  for (int i = 0; i < nseg; ++i) a.seg[i] = segs[i];
+  a.nseg = nseg;
+  a.part = part;
+  a.ld = ld;
+  a.n_tg = n_tg;
+  a.accumulate = accumulate;
+  const int64_t n = ld;
+  hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+int plan_gemv(const Q1Dev* const* mats, int n, int tpw, GemvPlan* plan) {
+  if (n < 1 || n > 8) return set_error(DZ_ERR_TENSOR, "gemv: %d matrices (1..8 supported)", n);
+  GemvGrid g;
+  memset(&g, 0, sizeof g);
+  const int64_t cols = mats[0]->cols;
+  int64_t rb = 0;
+  for (int i = 0; i < n; ++i) {
+    if (mats[i]->cols != cols) return set_error(DZ_ERR_TENSOR, "gemv: matrices disagree on cols");
+    g.seg[i].data = mats[i]->data;
+    g.seg[i].rb_begin = rb;
+    g.seg[i].nrb = mats[i]->nrb;
+    rb += mats[i]->nrb;
+  }
+  g.nseg = n;
+  g.total_rb = rb;
+  g.ntiles = (int)mats[0]->ntiles;
+  if (tpw <= 0) tpw = 1;
+  if (tpw > g.ntiles) tpw = g.ntiles;
+  if (tpw > 16) return set_error(DZ_ERR_UNSUPPORTED, "gemv: tiles per workgroup %d > 16", tpw);
+  g.tpw = tpw;
+  g.n_tg = (g.ntiles + tpw - 1) / tpw;
+  g.rbw = kGemvWaves * kGemvM;
+  plan->g = g;
+  plan->nwg = (unsigned)(((rb + g.rbw - 1) / g.rbw) * g.n_tg);
+  plan->shmem = gemv_shmem(tpw);
+  plan->ld = rb * kRowBlock;
+  return DZ_OK;
+}
+
+int upload_q1_host(const uint8_t* aos, int64_t rows, int64_t cols, Q1Dev* d, std::vector<void*>* owner) {
+  if (cols % kGroup) return set_error(DZ_ERR_TENSOR, "upload: cols %lld is not a multiple of 128", (long long)cols);
+  d->rows = rows;
+  d->cols = cols;
+  d->nrb = (rows + kRowBlock - 1) / kRowBlock;
+  d->ntiles = (cols + kTileCols - 1) / kTileCols;
+  const size_t aos_bytes = (size_t)rows * (size_t)(cols / kGroup) * kBlockBytes;
+  const size_t dev_bytes = (size_t)d->nrb * d->ntiles * kUnitBytes;
+  uint8_t* tmp = nullptr;
+  d->data = nullptr;
+  hipError_t e = hipMalloc(&d->data, dev_bytes);
+  if (e == hipSuccess) e = hipMalloc(&tmp, aos_bytes);
+  if (e == hipSuccess) e = hipMemcpyAsync(tmp, aos, aos_bytes, hipMemcpyHostToDevice, lib_stream());
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)(d->nrb * d->ntiles)), dim3(64), 0, lib_stream(), tmp, rows, cols,
+                       d->ntiles, d->data);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(lib_stream());
+  if (tmp) (void)hipFree(tmp);
+  if (e != hipSuccess) {
+    if (d->data) (void)hipFree(d->data);
+    d->data = nullptr;
+    return set_error(DZ_ERR_DEVICE, "upload: %s", hipGetErrorString(e));
+  }
+  if (owner) owner->push_back(d->data);
+  return DZ_OK;
+}
+
+int upload_q1_host(const uint8_t* aos, int64_t rows, int64_t cols, Q1Dev* out, std::vector<void*>& owner) {
+  return upload_q1_host(aos, rows, cols, out, &owner);
+}
+
+// ------------------------------------------------------------------ matrix API state
+
+static Scratch g_x, g_y, g_part;
+
+static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* const* y_dev, int accumulate,
+                       hipStream_t s) {
+  int prc = prepare_gemv_kernels();
+  if (prc) return prc;
+  const Q1Dev* ds[8];
+  for (int i = 0; i < n; ++i) ds[i] = &mats[i]->d;
+  GemvPlan p;
+  int rc = plan_gemv(ds, n, 1, &p);
+  if (rc) return rc;
+  rc = g_part.reserve((size_t)p.g.n_tg * p.ld * sizeof(float));
+  if (rc) return rc;
+  float* part = static_cast<float*>(g_part.ptr);
+  PlainSrc src{x_dev, mats[0]->d.cols};
+  PartialDst dst{part, p.ld};
+  DZ_HIP_CHECK(launch_gemv(p, src, dst, s));
+  ReduceSeg segs[8];
+  for (int i = 0; i < n; ++i) {
+    segs[i].y = y_dev[i];
+    segs[i].vrow_begin = p.g.seg[i].rb_begin * kRowBlock;
+    segs[i].rows = mats[i]->d.rows;
+  }
+  DZ_HIP_CHECK(launch_partial_reduce(part, p.ld, p.g.n_tg, segs, n, accumulate, s));
+  return DZ_OK;
+}
+
+}  // namespace dz
+
+using namespace dz;
+
+extern "C" {
+
+const char* dz_last_error(void) { return g_err; }
+
+int dz_device_init(int device) {
+  if (device != 0) return set_error(DZ_ERR_UNSUPPORTED, "only device 0 is supported");
+  return ensure_device();
+}
+
+void dz_config_bonsai27b(dz_config* c, int32_t max_ctx) {
+  c->n_layers = 64;
+  c->hidden = 5120;
+  c->ffn = 17408;
+  c->vocab = 248320;
+  c->n_head = 24;
+  c->n_head_kv = 4;
+  c->head_dim = 256;
+  c->rope_dim = 64;
+  c->rope_base = 1.0e7f;
+  c->rms_eps = 1e-6f;
+  c->full_attn_interval = 4;
+  c->ssm_conv_kernel = 4;
+  c->ssm_state = 128;
+  c->ssm_k_heads = 16;
+  c->ssm_v_heads = 48;
+  c->embd_f16 = 1;
+  c->max_ctx = max_ctx;
+}
+
+int dz_q1_0_upload(const uint8_t* aos, size_t rows, size_t cols, dz_mat** out) {
+  if (!aos || !out || rows == 0 || cols == 0) return set_error(DZ_ERR_TENSOR, "upload: empty matrix or null pointer");
+  if (cols % kGroup) return set_error(DZ_ERR_TENSOR, "upload: cols %zu is not a multiple of 128", cols);
+  int rc = ensure_device();
+  if (rc) return rc;
+  dz_mat* m = new dz_mat();
+  rc = upload_q1_host(aos, (int64_t)rows, (int64_t)cols, &m->d, nullptr);
+  if (rc) {
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return DZ_OK;
+}
+
+int dz_q1_0_free(dz_mat* m) {
+  if (!m) return DZ_OK;
+  if (m->d.data) DZ_HIP_CHECK(hipFree(m->d.data));
+  delete m;
+  return DZ_OK;
+}
+
+int dz_q1_0_shape(const dz_mat* m, size_t* rows, size_t* cols) {
+  if (!m) return set_error(DZ_ERR_TENSOR, "shape: null matrix");
+  if (rows) *rows = (size_t)m->d.rows;
+  if (cols) *cols = (size_t)m->d.cols;
+  return DZ_OK;
+}
+
+int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream) {
+  if (!m || !x_dev || !y_dev) return set_error(DZ_ERR_TENSOR, "matvec_dev: null pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  dz_mat* ms[1] = {m};
+  float* ys[1] = {y_dev};
+  return matvec_impl(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
+}
+
+static int matvec_host(dz_mat* const* mats, int n, const float* x, float* const* ys, int accumulate) {
+  if (n < 1 || n > 8) return set_error(DZ_ERR_TENSOR, "matvec: %d matrices (1..8 supported)", n);
+  if (!x) return set_error(DZ_ERR_TENSOR, "matvec: null x");
+  int rc = ensure_device();
+  if (rc) return rc;
+  size_t ytot = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!mats[i] || !ys[i]) return set_error(DZ_ERR_TENSOR, "matvec: null matrix or output");
+    if (mats[i]->d.cols != mats[0]->d.cols) return set_error(DZ_ERR_TENSOR, "matvec: matrices disagree on cols");
+    ytot += (size_t)mats[i]->d.rows;
+  }
+  const size_t K = (size_t)mats[0]->d.cols;
+  rc = g_x.reserve(K * 4);
+  if (rc) return rc;
+  rc = g_y.reserve(ytot * 4);
+  if (rc) return rc;
+  hipStream_t s = lib_stream();
+  DZ_HIP_CHECK(hipMemcpyAsync(g_x.ptr, x, K * 4, hipMemcpyHostToDevice, s));
+  float* ydev[8];
+  size_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    ydev[i] = static_cast<float*>(g_y.ptr) + off;
+    if (accumulate)
+      DZ_HIP_CHECK(hipMemcpyAsync(ydev[i], ys[i], (size_t)mats[i]->d.rows * 4, hipMemcpyHostToDevice, s));
+    off += (size_t)mats[i]->d.rows;
+  }
+  rc = matvec_impl(mats, n, static_cast<const float*>(g_x.ptr), ydev, accumulate, s);
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i)
+    DZ_HIP_CHECK(hipMemcpyAsync(ys[i], ydev[i], (size_t)mats[i]->d.rows * 4, hipMemcpyDeviceToHost, s));
+  DZ_HIP_CHECK(hipStreamSynchronize(s));
+  return DZ_OK;
+}
+
+int dz_q1_0_matvec(dz_mat* m, const float* x, float* y, int accumulate) {
+  dz_mat* ms[1] = {m};
+  float* ys[1] = {y};
+  return matvec_host(ms, 1, x, ys, accumulate);
+}
+
+int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* const* ys) {
+  return matvec_host(mats, n, x, ys, 0);
+}
+
+int dz_q1_0_dequant_rows(dz_mat* m, size_t r0, size_t n, float* out) {
+  if (!m || !out) return set_error(DZ_ERR_TENSOR, "dequant: null pointer");
+  if (r0 + n > (size_t)m->d.rows) return set_error(DZ_ERR_TENSOR, "dequant: rows [%zu, %zu) out of range", r0, r0 + n);
+  if (n == 0) return DZ_OK;
+  int rc = ensure_device();
+  if (rc) return rc;
+  const size_t total = n * (size_t)m->d.cols;
+  rc = g_y.reserve(total * 4);
+  if (rc) return rc;
+  hipStream_t s = lib_stream();
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, m->d.data, m->d.cols,
+                     m->d.ntiles, (int64_t)r0, (int64_t)n, static_cast<float*>(g_y.ptr));
+  DZ_HIP_CHECK(hipGetLastError());
+  DZ_HIP_CHECK(hipMemcpyAsync(out, g_y.ptr, total * 4, hipMemcpyDeviceToHost, s));
+  DZ_HIP_CHECK(hipStreamSynchronize(s));
+  return DZ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// runtime.h — host-side helpers shared by the library's translation units.
+#pragma once
+#include "common.h"
+#include "q1_gemv.h"
+
+#include <vector>
+
+namespace dz {
+
+// Makes sure a gfx950 device is current for this thread (first call selects device 0).
+int ensure_device();
+// Library stream used by the matrix-level entry points.
+hipStream_t lib_stream();
+
+// Device scratch buffers owned by the library (grown on demand, reused across calls).
+struct Scratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  int reserve(size_t n);
+};
+
+// Launch shape of one GEMV: the segment table plus grid size and dynamic LDS bytes.
+struct GemvPlan {
+  GemvGrid g;
+  unsigned nwg = 0;
+  size_t shmem = 0;
+  int64_t ld = 0;  // rows of the virtual row space padded to 64 (partials leading dimension)
+};
+
+// Builds a plan over `mats` (stacked in order), all with the same cols.
+// tpw = tiles per workgroup; tpw <= 0 picks the default (1, or all tiles when ntiles == 1).
+int plan_gemv(const Q1Dev* const* mats, int n, int tpw, GemvPlan* plan);
+
+// Default launch shape: NWAVES waves per workgroup, M row-blocks per wave.
+constexpr int kGemvWaves = 8;
+constexpr int kGemvM = 1;
+// dynamic LDS: table + 16 reduction floats + up to 16 staged tiles
+constexpr size_t kGemvShmemMax = kLutBytes + 64 + 16 * kTileCols * 4;
+inline size_t gemv_shmem(int tpw) { return (size_t)kLutBytes + 64 + (size_t)tpw * kTileCols * 4; }
+
+// The kernel's dynamic-LDS limit must have been raised (hipFuncSetAttribute) before the first launch.
+template <class Src, class Dst>
+hipError_t launch_gemv(const GemvPlan& p, const Src& src, const Dst& dst, hipStream_t s) {
+  auto kfn = gemv_lut_kernel<kGemvWaves, kGemvM, Src, Dst>;
+  hipLaunchKernelGGL(kfn, dim3(p.nwg), dim3(kGemvWaves * 64), p.shmem, s, p.g, src, dst);
+  return hipGetLastError();
+}
+
+// Raises the dynamic-LDS limit of every GEMV instantiation the library launches (idempotent).
+int prepare_gemv_kernels();
+
+// Sum of the tile-group partials into each segment's output: y = [y +] sum_tg part[tg][row].
+struct ReduceSeg {
+  float* y;
+  int64_t vrow_begin;  // first virtual row of the segment
+  int64_t rows;        // logical rows
+};
+hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const ReduceSeg* segs, int nseg,
+                                 int accumulate, hipStream_t s);
+
+}  // namespace dz

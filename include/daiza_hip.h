@@ -1,0 +1,180 @@
+/*
+ * daiza_hip.h — C ABI of the MI355X (gfx950) batch-1 Q1_0 decode library.
+ *
+ * Every entry point returns int: DZ_OK (0) or a negative status.  The negative
+ * values map onto the reference's error enum BonsaiError (Daiza-engine/src/lib.rs:42-78):
+ *   DZ_ERR_TENSOR      -> BonsaiError::Tensor       (shape / layout violations)
+ *   DZ_ERR_MODEL       -> BonsaiError::Model        (bad config, missing tensor)
+ *   DZ_ERR_UNSUPPORTED -> BonsaiError::Unsupported  (shapes this build does not implement)
+ *   DZ_ERR_DEVICE      -> device/runtime failure (HIP error, no gfx950 device)
+ * dz_last_error() returns a thread-local message for the last failure.
+ *
+ * Ownership: the library owns device memory and handles.  Host pointers passed in
+ * are borrowed for the duration of the call; host outputs are written before the
+ * call returns (the reference reads ctx.logits_buf right after forward_single_token).
+ * A context owns one HIP stream and is not thread safe, the same contract as the
+ * reference's `&mut ForwardContext`.  No C++ exception crosses this boundary.
+ */
+#ifndef DAIZA_HIP_H
+#define DAIZA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DZ_OK 0
+#define DZ_ERR_TENSOR (-1)
+#define DZ_ERR_MODEL (-2)
+#define DZ_ERR_UNSUPPORTED (-3)
+#define DZ_ERR_DEVICE (-4)
+
+/*
+ * Model hyper-parameters.  Field meaning follows Config (Daiza-engine/src/model/config.rs:12-76);
+ * Bonsai-27B values in comments.  Layer i is full attention when (i+1) % full_attn_interval == 0
+ * (config.rs:161-167).
+ */
+typedef struct dz_config {
+  int32_t n_layers;            /* 64      block_count */
+  int32_t hidden;              /* 5120    embedding_length */
+  int32_t ffn;                 /* 17408   feed_forward_length */
+  int32_t vocab;               /* 248320 */
+  int32_t n_head;              /* 24      attention.head_count */
+  int32_t n_head_kv;           /* 4       attention.head_count_kv */
+  int32_t head_dim;            /* 256     attention.key_length (this build: 256) */
+  int32_t rope_dim;            /* 64      rope.dimension_count */
+  float rope_base;             /* 1e7     rope.freq_base */
+  float rms_eps;               /* 1e-6    attention.layer_norm_rms_epsilon */
+  int32_t full_attn_interval;  /* 4 */
+  int32_t ssm_conv_kernel;     /* 4       (this build: 4) */
+  int32_t ssm_state;           /* 128     ssm.state_size = head_k_dim = head_v_dim (this build: 128) */
+  int32_t ssm_k_heads;         /* 16      ssm.group_count */
+  int32_t ssm_v_heads;         /* 48      ssm.time_step_rank */
+  int32_t embd_f16;            /* 1: f16 token embedding; 0: Q1_0 (reference GGUF) */
+  int32_t max_ctx;             /* KV-cache capacity in tokens */
+} dz_config;
+
+/* Fills cfg with the Bonsai-27B shape (Config::default, config.rs:47-76) and max_ctx. */
+void dz_config_bonsai27b(dz_config* cfg, int32_t max_ctx);
+
+const char* dz_last_error(void);
+
+/* Selects the HIP device for subsequent calls on this thread; fails unless it is gfx950. */
+int dz_device_init(int device);
+
+/* ===================== matrix level: Q1_0Matrix (weights.rs:83-1208) ===================== */
+
+typedef struct dz_mat dz_mat;
+
+/*
+ * Uploads one Q1_0 matrix given in the reference's AoS block layout
+ * (Q1_0Matrix::bytes, weights.rs:83-102; 18 bytes per 128 weights, row r at r*(cols/128)*18).
+ * cols must be a multiple of 128.  The device copy is repacked into the GEMV's layout;
+ * the bytes themselves are unchanged (dz_q1_0_dequant_rows recovers them bit-exactly).
+ * Replaces Q1_0Matrix::from_gguf (weights.rs:90-102).
+ */
+int dz_q1_0_upload(const uint8_t* aos, size_t rows, size_t cols, dz_mat** out);
+int dz_q1_0_free(dz_mat* m);
+int dz_q1_0_shape(const dz_mat* m, size_t* rows, size_t* cols);
+
+/* y = W x (accumulate = 0) or y += W x (accumulate = 1); host x[cols], y[rows].
+ * Replaces matvec_into_slice (weights.rs:123-325) and matvec_add_into_slice (weights.rs:334-465). */
+int dz_q1_0_matvec(dz_mat* m, const float* x, float* y, int accumulate);
+
+/* Several matrices sharing x and cols, one device pass (n <= 8).
+ * Replaces matvec_multi_into_slice (weights.rs:831-972). */
+int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* const* ys);
+
+/* Same as dz_q1_0_matvec on device pointers, enqueued on `stream` (a hipStream_t, NULL = default),
+ * without a host synchronisation.  The token loop uses the fused kernels instead. */
+int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);
+
+/* Dequantised rows [r0, r0+n) as f32 (w = bit ? +scale : -scale, exact f16->f32).
+ * Replaces dequantize_q1_0_row_into (quant.rs:161-194) / row_into_slice (weights.rs:106). */
+int dz_q1_0_dequant_rows(dz_mat* m, size_t r0, size_t n, float* out);
+
+/* ===================== model level: forward_single_token / forward_batch ===================== */
+
+typedef struct dz_model dz_model;
+typedef struct dz_ctx dz_ctx;
+
+/* One named host tensor, GGUF naming (LoadedWeights::load_all, weights.rs:1308-1379):
+ *   "token_embd.weight" (Q1_0, or F16 when cfg.embd_f16), "output_norm.weight" (F32),
+ *   "output.weight" (Q1_0), "blk.N.<name>" per layer.
+ * type: 0 = F32, 1 = F16, 41 = Q1_0 (GGUF TensorType, gguf/tensor_info.rs:41,66).
+ * ssm_conv1d.weight is given as in GGUF, [qkv_dim][conv_kernel] (the reference transposes at load). */
+typedef struct dz_tensor {
+  const char* name;
+  int32_t type;
+  const void* data;
+  size_t n_bytes;
+} dz_tensor;
+
+int dz_model_create(const dz_config* cfg, const dz_tensor* tensors, int n_tensors, dz_model** out);
+
+/* Synthetic model with the generator of daiza_synth.h (BASELINE.json config 4 when cfg is Bonsai-27B). */
+int dz_model_create_synth(const dz_config* cfg, uint64_t seed, dz_model** out);
+int dz_model_free(dz_model* m);
+int dz_model_weight_bytes(const dz_model* m, uint64_t* q1_bytes);
+
+/* Context = ModelState + ForwardContext (forward.rs:32-131): KV caches, SSM states, position. */
+int dz_ctx_create(dz_model* m, dz_ctx** out);
+int dz_ctx_free(dz_ctx* c);
+int dz_ctx_reset(dz_ctx* c);          /* ModelState::reset (forward.rs:66-76) */
+int dz_ctx_pos(const dz_ctx* c);      /* ModelState::pos */
+
+/*
+ * One token: embed -> 64 blocks -> output norm -> lm_head -> pos += 1.
+ * logits_or_null receives vocab f32 values (ctx.logits_buf); argmax_or_null receives the greedy
+ * token (lowest index among equal maxima, simd_exp.rs:551-598).
+ * Replaces forward_single_token (forward.rs:204-375).
+ */
+int dz_forward_token(dz_ctx* c, uint32_t token, float* logits_or_null, uint32_t* argmax_or_null);
+
+/*
+ * n tokens at positions start_pos.. (start_pos must equal the context position).
+ * Last-position logits to last_logits_or_null; per-position logits [n][vocab] to
+ * per_pos_logits_or_null.  Replaces forward_batch (forward.rs:394-1407).
+ */
+int dz_forward_batch(dz_ctx* c, const uint32_t* ids, int n, int start_pos,
+                     float* last_logits_or_null, float* per_pos_logits_or_null);
+
+/*
+ * Greedy decode of n tokens entirely on the device: the first forward consumes `first_token`,
+ * each next input is the argmax of the previous logits.  out_tokens[i] = argmax after forward i.
+ * Mirrors the greedy loop of Engine::generate_inner (engine.rs:850-871) without the EOS stop.
+ */
+int dz_decode_greedy(dz_ctx* c, uint32_t first_token, int n, uint32_t* out_tokens);
+
+/* Last computed logits (vocab f32) of the context. */
+int dz_ctx_logits(dz_ctx* c, float* logits);
+
+/* ---- state access (ModelState fields; layouts are the reference's) ---- */
+/* SSM layer state S[v_heads][128 (v index i)][128 (k index j)] (cache/ssm_state.rs:10-39) and
+ * the conv ring hist[conv_kernel][qkv_dim] with its head index (oldest row). */
+int dz_ctx_set_ssm_state(dz_ctx* c, int layer, const float* state, const float* conv_hist, int conv_head);
+int dz_ctx_get_ssm_state(dz_ctx* c, int layer, float* state, float* conv_hist, int* conv_head);
+/* KV cache of an attention layer, per-kvh [len][head_dim] (cache/kv_cache.rs:17-130). */
+int dz_ctx_set_kv(dz_ctx* c, int layer, const float* k, const float* v, int len);
+int dz_ctx_get_kv(dz_ctx* c, int layer, float* k, float* v, int len);
+int dz_ctx_kv_len(dz_ctx* c, int layer);
+int dz_kv_truncate(dz_ctx* c, int len);                    /* KvCache::truncate (kv_cache.rs:119-130) */
+int dz_ctx_set_pos(dz_ctx* c, int pos);
+
+/*
+ * One mixer step of one layer on host h[hidden]: h += mixer(rmsnorm(h)), where mixer is the
+ * Gated DeltaNet (ssm_forward_into, ssm.rs:425-616) or gated attention
+ * (attention_forward_into, attention.rs:56-208); uses and advances that layer's state at the
+ * context position (BASELINE configs 2 and 3).
+ */
+int dz_ctx_mixer_step(dz_ctx* c, int layer, float* h);
+
+/* The context's HIP stream (hipStream_t), for callers that time or order work around it. */
+void* dz_ctx_stream(dz_ctx* c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DAIZA_HIP_H */

@@ -1,0 +1,241 @@
+"""Benchmark: batch-1 greedy decode of the synthetic Bonsai-27B-shape Q1_0 model on one MI355X.
+
+Workload: 64-layer hybrid stack (48 Gated DeltaNet + 16 gated GQA
+attention layers), random Q1_0 weights from include/daiza_synth.h, f16 embedding; a 1024-token
+prefill of uniform-random ids, then `--steps` timed greedy decode tokens after `--warmup`
+untimed ones.  One step = one token through the whole stack (forward_single_token).
+
+Prints one JSON line.  `roofline` is the dominant kernel, the Q1_0 LUT GEMV, timed per launch
+with HIP events on its stream at the config-1 shape (17408 x 5120, 32 distinct matrices, more
+than the 256 MB Infinity Cache).  `cpu_baseline` is the CPU oracle (oracle/, a C restatement of
+the reference's multithreaded AVX2 path) on a bounded sample of the same workload.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "batch-1 decode tok/s (27B-shape Q1_0 synth); Q1_0 GEMV HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+SEED = 0xDA1A0004
+PREFILL = 1024
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def hip():
+    h = ctypes.CDLL("libamdhip64.so")
+    h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    h.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    h.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    h.hipDeviceSynchronize.argtypes = []
+    return h
+
+
+class Events:
+    def __init__(self, H, n):
+        self.H = H
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            assert H.hipEventCreate(ctypes.byref(e)) == 0
+            self.ev.append(e)
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        assert self.H.hipEventElapsedTime(ctypes.byref(ms), self.ev[a], self.ev[b]) == 0
+        return ms.value
+
+
+def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
+    """Per-launch HIP-event timing of the LUT GEMV kernel (config 1 shape)."""
+    import oracle  # synthetic bytes only (daiza_synth.h); no oracle arithmetic here
+    aos = oracle.synth_q1_0(SEED, 18, 0, rows, cols)
+    mats = [dz.Q1_0Matrix(aos, rows, cols) for _ in range(nmat)]
+    x = oracle.synth_normal(SEED, 64, 0, cols)
+    L = dz.lib()
+    ld = L.dz_q1_0_partials_ld(mats[0]._h)
+    nt = L.dz_q1_0_ntiles(mats[0]._h)
+    dx, dy = ctypes.c_void_p(), ctypes.c_void_p()
+    H.hipMalloc(ctypes.byref(dx), cols * 4)
+    H.hipMalloc(ctypes.byref(dy), ld * nt * 4)
+    H.hipMemcpy(dx, x.ctypes.data, cols * 4, 1)
+    s = ctypes.c_void_p()
+    H.hipStreamCreate(ctypes.byref(s))
+    for m in mats:  # warm-up
+        assert L.dz_q1_0_gemv_partials(m._h, dx, dy, s) == 0
+    H.hipStreamSynchronize(s)
+    n = nmat * reps
+    ev = Events(H, 2 * n + 2)
+    H.hipEventRecord(ev.ev[-2], s)
+    for i in range(n):
+        H.hipEventRecord(ev.ev[2 * i], s)
+        L.dz_q1_0_gemv_partials(mats[i % nmat]._h, dx, dy, s)
+        H.hipEventRecord(ev.ev[2 * i + 1], s)
+    H.hipEventRecord(ev.ev[-1], s)
+    H.hipEventSynchronize(ev.ev[-1])
+    per = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(n)]
+    total = ev.elapsed_ms(2 * n, 2 * n + 1)
+    algo = rows * (cols // 128) * 18 + cols * 4 + rows * 4  # W + x + y
+    avg_us = 1e3 * float(np.mean(per))
+    for m in mats:
+        m.close()
+    return {
+        "avg_launch_us": avg_us,
+        "median_launch_us": 1e3 * float(np.median(per)),
+        "back_to_back_us": 1e3 * total / n,
+        "algo_bytes": algo,
+        "achieved_gbs": algo / (avg_us * 1e-6) / 1e9,
+    }
+
+
+def cpu_baseline(cfg_cls, budget_s=20.0):
+    """Oracle (C restatement of the reference AVX2 path) decode on the host cores."""
+    import oracle
+    # the GPU box grants 16 host CPUs per GPU
+    threads = min(os.cpu_count() or 1, int(os.environ.get("DZ_CPU_THREADS", 16)))
+    cfg = cfg_cls.bonsai27b(max_ctx=256)
+    t0 = time.time()
+    om = oracle.Model(cfg, SEED, nthreads=threads)
+    gen_s = time.time() - t0
+    rng = np.random.default_rng(1)
+    ids = rng.integers(0, cfg.vocab, 8)
+    for t in ids:  # short prefill (sequential single-token forwards)
+        tok, _ = om.forward(int(t), want_logits=False)
+    n = 0
+    t0 = time.time()
+    while True:
+        tok, _ = om.forward(tok, want_logits=False)
+        n += 1
+        el = time.time() - t0
+        if el > budget_s or n >= 64:
+            break
+    om.close()
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "oracle greedy decode of %d tokens after an 8-token prefill, full 27B shape, %d threads "
+                      "(model generation %.1f s excluded)" % (n, threads, gen_s)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prefill", type=int, default=PREFILL)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build runs the decode loop on a single GPU "
+              "(multi-GPU sharding is design-only, see DESIGN.md); use --gpus 1", file=sys.stderr)
+        return 2
+
+    import daiza_amd as dz
+    H = hip()
+    L = dz.lib()
+    if L.dz_device_init(0) != 0:
+        raise SystemExit("dz_device_init: " + L.dz_last_error().decode())
+
+    max_ctx = args.prefill + args.warmup + args.steps + 8
+    cfg = dz.Config.bonsai27b(max_ctx=max_ctx)
+    t0 = time.time()
+    log("building synthetic 27B-shape model")
+    model = dz.Model.synthetic(cfg, SEED)
+    build_s = time.time() - t0
+    log("model built in %.1f s" % build_s)
+    ctx = dz.Context(model)
+    wbytes = model.q1_bytes()
+
+    rng = np.random.default_rng(SEED & 0xFFFF)
+    prompt = rng.integers(0, cfg.vocab, args.prefill).astype(np.uint32)
+    t0 = time.time()
+    last = ctx.forward_batch(prompt)
+    prefill_s = time.time() - t0
+    log("prefill %d tokens in %.2f s" % (args.prefill, prefill_s))
+    first = int(np.argmax(last))
+
+    stream = ctypes.c_void_p(ctx.stream())
+    ev = Events(H, 2)
+    toks_w = ctx.decode_greedy(first, args.warmup) if args.warmup else np.array([first], np.uint32)
+    nxt = int(toks_w[-1])
+    H.hipDeviceSynchronize()
+    H.hipEventRecord(ev.ev[0], stream)
+    t0 = time.perf_counter()
+    toks = ctx.decode_greedy(nxt, args.steps)
+    H.hipEventRecord(ev.ev[1], stream)
+    H.hipEventSynchronize(ev.ev[1])
+    H.hipDeviceSynchronize()
+    wall = time.perf_counter() - t0
+    ms = ev.elapsed_ms(0, 1)
+    tps = args.steps / (ms / 1e3)
+
+    log("decode %d tokens: %.2f tok/s" % (args.steps, tps))
+    g = bench_gemv(dz, H)
+    log("gemv: %.2f us per launch" % g["avg_launch_us"])
+    out = {
+        "metric": METRIC,
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 4: Bonsai-27B-shape synthetic Q1_0 (64 layers: 48 Gated DeltaNet + 16 gated "
+                        "GQA attention, hidden 5120, FFN 17408, vocab 248320, f16 embedding), %d-token random prefill, "
+                        "then greedy decode" % args.prefill,
+            "prefill_tokens": args.prefill,
+            "decode_tokens": args.steps,
+            "context_at_end": ctx.pos,
+            "q1_weight_bytes_per_token": wbytes,
+            "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
+            "weight_roofline_frac": round(tps * wbytes / (PEAK_GBS * 1e9), 4),
+            "prefill_s": round(prefill_s, 3),
+            "model_build_s": round(build_s, 1),
+            "decode_wall_s": round(wall, 4),
+        },
+        "roofline": {
+            "kernel": "gemv_lut_kernel (Q1_0 LUT GEMV, config 1 17408x5120, split-K partials)",
+            "bound": "hbm",
+            "achieved": round(g["achieved_gbs"], 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["achieved_gbs"] / PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(g["avg_launch_us"], 3),
+            "median_launch_us": round(g["median_launch_us"], 3),
+            "back_to_back_us": round(g["back_to_back_us"], 3),
+            "algo_bytes_per_launch": g["algo_bytes"],
+        },
+        "cpu_baseline": None,
+    }
+    ctx.close()
+    model.close()
+    if not args.no_cpu:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(dz.Config, args.cpu_budget)
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <functional>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <thread>
@@ -112,6 +113,11 @@ static int cfg_check(const dz_config* c) {
   if (c->rope_dim < 2 || c->rope_dim > c->head_dim || c->rope_dim % 2) return set_error(DZ_ERR_MODEL, "rope_dim %d", c->rope_dim);
   if (c->ssm_k_heads < 1 || c->ssm_v_heads % c->ssm_k_heads) return set_error(DZ_ERR_MODEL, "ssm heads");
   if (c->max_ctx < 1) return set_error(DZ_ERR_MODEL, "max_ctx %d", c->max_ctx);
+  const int64_t kout = std::max<int64_t>((int64_t)c->ssm_v_heads * c->ssm_state, (int64_t)c->n_head * c->head_dim);
+  if ((c->hidden + kTileCols - 1) / kTileCols > kMaxTilesH)
+    return set_error(DZ_ERR_UNSUPPORTED, "hidden %d > %d", c->hidden, kMaxTilesH * kTileCols);
+  if ((c->ffn + kTileCols - 1) / kTileCols > kMaxTilesF || (kout + kTileCols - 1) / kTileCols > kMaxTilesF)
+    return set_error(DZ_ERR_UNSUPPORTED, "ffn or mixer width > %d", kMaxTilesF * kTileCols);
   return DZ_OK;
 }
 
@@ -672,12 +678,30 @@ static int ctx_feed(dz_ctx* x, const uint32_t* ids, int n) {
   return DZ_OK;
 }
 
+// DAIZA_GRAPH=0 enqueues each token's kernels directly instead of replaying the captured graph
+// (same kernels and arguments; for tools that do not trace graph launches).
+static bool use_graph() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("DAIZA_GRAPH");
+    v = (e && e[0] == '0') ? 0 : 1;
+  }
+  return v == 1;
+}
+
 static int ctx_run(dz_ctx* x, int n) {
   if (x->pos_host + n > x->m->cfg.max_ctx)
     return set_error(DZ_ERR_TENSOR, "context full: pos %d + %d > max_ctx %d", x->pos_host, n, x->m->cfg.max_ctx);
-  int rc = ctx_build_graph(x);
-  if (rc) return rc;
-  for (int i = 0; i < n; ++i) DZ_HIP_CHECK(hipGraphLaunch(x->gexec, x->s));
+  if (use_graph()) {
+    int rc = ctx_build_graph(x);
+    if (rc) return rc;
+    for (int i = 0; i < n; ++i) DZ_HIP_CHECK(hipGraphLaunch(x->gexec, x->s));
+  } else {
+    for (int i = 0; i < n; ++i) {
+      int rc = enqueue_token(x, x->s);
+      if (rc) return rc;
+    }
+  }
   x->pos_host += n;
   return DZ_OK;
 }

@@ -23,10 +23,24 @@ struct TokState {
   int pad[3];
 };
 
+// Sum over a full wave (all 64 lanes active).  DPP inside each row of 16 lanes (xor 1, xor 2,
+// half-row mirror, row mirror: every lane then holds its row's sum), then the four row sums
+// read with v_readlane; the result is wave-uniform and independent of lane order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -50,10 +64,31 @@ __device__ __forceinline__ float block_sum(float v, float* red, unsigned tid, in
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 
-// inverse RMS of a vector whose per-tile sums of squares are ss[0..nt) (rmsnorm.rs:53-55)
+// Upper bounds on split-K tile counts summed by consumers (checked at model creation):
+// K = hidden (<= 16 tiles of 512) and K = ffn or the out-projection width (<= 48 tiles).
+constexpr int kMaxTilesH = 16;
+constexpr int kMaxTilesF = 48;
+
+// sum_{k<n} p[k*ld + idx] in order k = 0..n-1, with all n loads issued before the first add
+// (one memory round trip instead of n).
+template <int MAXN>
+__device__ __forceinline__ float sum_strided(const float* __restrict__ p, int64_t ld, int n, int64_t idx) {
+  float v[MAXN];
+#pragma unroll
+  for (int k = 0; k < MAXN; ++k)
+    if (k < n) v[k] = p[(size_t)k * ld + idx];
+  float d = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXN; ++k)
+    if (k < n) d += v[k];
+  return d;
+}
+
+// inverse RMS from per-tile sums of squares ss[0..nss), nss <= 64 (rmsnorm.rs:53-55):
+// lane i loads ss[i], a butterfly sums them; every lane of every calling wave gets the value.
 __device__ __forceinline__ float inv_rms_from(const float* ss, int nss, int64_t n, float eps) {
-  float s = 0.f;
-  for (int i = 0; i < nss; ++i) s += ss[i];
+  const unsigned lane = threadIdx.x & 63u;
+  const float s = wave_sum((int)lane < nss ? ss[lane] : 0.f);
   return 1.0f / sqrtf(s / (float)n + eps);
 }
 
@@ -75,8 +110,7 @@ struct ResidSrc {
       const int64_t col = (int64_t)t * kTileCols + i;
       float u = 0.f;
       if (col < H) {
-        float d = 0.f;
-        for (int k = 0; k < np; ++k) d += part[(size_t)k * ldp + col];
+        const float d = sum_strided<kMaxTilesF>(part, ldp, np, col);
         const float v = np ? h_in[col] + d : h_in[col];
         u = v * w[col];
         if (chunk == 0) h_out[col] = v;
@@ -107,11 +141,8 @@ struct SwigluSrc {
       const int64_t col = (int64_t)t * kTileCols + i;
       float u = 0.f;
       if (col < F) {
-        float g = 0.f, up = 0.f;
-        for (int k = 0; k < np; ++k) {
-          g += part[(size_t)k * ldp + col];
-          up += part[(size_t)k * ldp + F + col];
-        }
+        float g = sum_strided<kMaxTilesH>(part, ldp, np, col);
+        float up = sum_strided<kMaxTilesH>(part, ldp, np, F + col);
         g *= inv;
         up *= inv;
         u = siluf_(g) * up;
@@ -186,10 +217,8 @@ struct AttnOutSrc {
           l = __builtin_fmaf(r[1], e, l);
           o = __builtin_fmaf(r[2 + d], e, o);
         }
-        float gate = 0.f;
         const int64_t grow = (int64_t)h * 2 * hd + hd + d;
-        for (int k = 0; k < np; ++k) gate += p_in[(size_t)k * ldp + grow];
-        gate *= inv;
+        const float gate = sum_strided<kMaxTilesH>(p_in, ldp, np, grow) * inv;
         u = (o * (1.0f / l)) * sigmoidf_(gate);
       }
       xs[i] = u;
@@ -383,35 +412,72 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   const unsigned tid = threadIdx.x;
   const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % a.nkh;
   const int i_loc = tid & 31, js = tid >> 5;
+  const int i = quarter * 32 + i_loc;
   const int pos = a.st->pos;
   const int hb = (*a.ring_base_ptr + pos) & 3;  // ring head before this token = slot of the new value
-  const float inv = inv_rms_from(a.ss, a.nss, a.H, a.rms_eps);
   const int64_t kdim = (int64_t)a.nkh * HD;
+  const int64_t qkvd = a.qkvd;
 
-  auto proj = [&](int64_t row) {
-    float d = 0.f;
-    for (int k = 0; k < a.np; ++k) d += a.p_in[(size_t)k * a.ldp + row];
-    return d * inv;
-  };
-  auto conv_silu = [&](int64_t ch, bool write) {
-    const float xn = proj(ch);
-    const float* w = a.conv_w;
-    float o = 0.f;
-    o = __builtin_fmaf(a.conv[(size_t)((hb + 1) & 3) * a.qkvd + ch], w[ch], o);
-    o = __builtin_fmaf(a.conv[(size_t)((hb + 2) & 3) * a.qkvd + ch], w[a.qkvd + ch], o);
-    o = __builtin_fmaf(a.conv[(size_t)((hb + 3) & 3) * a.qkvd + ch], w[2 * a.qkvd + ch], o);
-    o = __builtin_fmaf(xn, w[3 * a.qkvd + ch], o);
-    if (write) a.conv[(size_t)hb * a.qkvd + ch] = xn;
-    return siluf_(o);
-  };
+  // ---- every global load first (one memory round trip) ----
+  // state rows i, k-slice [16*js, 16*js+16)
+  float* S = a.state + (size_t)vh * HD * HD;
+  float s[16];
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  const float inv = inv_rms_from(a.ss, a.nss, a.H, a.rms_eps);
+  // conv channel of this thread: q (tid < 128) or k (tid >= 128) of k-head kh
+  const int64_t ch = tid < HD ? (int64_t)kh * HD + tid : kdim + (int64_t)kh * HD + (tid - HD);
+  const float xq = sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, ch);
+  const float r1 = a.conv[(size_t)((hb + 1) & 3) * qkvd + ch], r2 = a.conv[(size_t)((hb + 2) & 3) * qkvd + ch],
+              r3 = a.conv[(size_t)((hb + 3) & 3) * qkvd + ch];
+  const float w0 = a.conv_w[ch], w1 = a.conv_w[qkvd + ch], w2 = a.conv_w[2 * qkvd + ch], w3 = a.conv_w[3 * qkvd + ch];
+  // second role: v channel (tid < 32), z (32..63), alpha (64), beta (65)
+  int64_t row2 = -1;
+  if (tid < 32) row2 = 2 * kdim + (int64_t)vh * HD + quarter * 32 + tid;
+  else if (tid < 64) row2 = a.off_z + (int64_t)vh * HD + quarter * 32 + (tid - 32);
+  else if (tid == 64) row2 = a.off_a + vh;
+  else if (tid == 65) row2 = a.off_b + vh;
+  float x2 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f, u0 = 0.f, u1 = 0.f, u2 = 0.f, u3 = 0.f;
+  if (row2 >= 0) x2 = sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, row2);
+  if (tid < 32) {
+    v1 = a.conv[(size_t)((hb + 1) & 3) * qkvd + row2];
+    v2 = a.conv[(size_t)((hb + 2) & 3) * qkvd + row2];
+    v3 = a.conv[(size_t)((hb + 3) & 3) * qkvd + row2];
+    u0 = a.conv_w[row2]; u1 = a.conv_w[qkvd + row2]; u2 = a.conv_w[2 * qkvd + row2]; u3 = a.conv_w[3 * qkvd + row2];
+  }
+  float ssm_a = 0.f, dtb = 0.f;
+  if (tid == 64) { ssm_a = a.ssm_a[vh]; dtb = a.dt_bias[vh]; }
 
-  // q (threads 0..127) and k (threads 128..255) of k-head kh; v for this quarter's 32 rows
-  const bool owner = (vh < a.nkh) && quarter == 0;  // writes the shared q/k ring channels
-  float qk;
-  if (tid < HD) qk = conv_silu((int64_t)kh * HD + tid, owner);
-  else qk = conv_silu(kdim + (int64_t)kh * HD + (tid - HD), owner);
-  if (tid < 32) vs[tid] = conv_silu(2 * kdim + (int64_t)vh * HD + quarter * 32 + tid, true);
-  // L2 norms (ssm.rs:523-530): two 128-wide reductions, waves 0-1 for q and 2-3 for k
+  // ---- conv ring + causal conv (fma in tap order, oldest first) + SiLU (ssm.rs:467-518) ----
+  const float xn = xq * inv;
+  float o = 0.f;
+  o = __builtin_fmaf(r1, w0, o);
+  o = __builtin_fmaf(r2, w1, o);
+  o = __builtin_fmaf(r3, w2, o);
+  o = __builtin_fmaf(xn, w3, o);
+  const float qk = siluf_(o);
+  const bool owner = (vh < a.nkh) && quarter == 0;  // one writer per shared q/k ring channel
+  if (owner) a.conv[(size_t)hb * qkvd + ch] = xn;
+  const float x2n = x2 * inv;
+  if (tid < 32) {
+    float ov = 0.f;
+    ov = __builtin_fmaf(v1, u0, ov);
+    ov = __builtin_fmaf(v2, u1, ov);
+    ov = __builtin_fmaf(v3, u2, ov);
+    ov = __builtin_fmaf(x2n, u3, ov);
+    vs[tid] = siluf_(ov);
+    a.conv[(size_t)hb * qkvd + row2] = x2n;
+  } else if (tid < 64) {
+    a.zs[(size_t)vh * HD + quarter * 32 + (tid - 32)] = siluf_(x2n);
+  } else if (tid == 64) {
+    // g = A * softplus(alpha + dt_bias), decay = exp(g)  (ssm.rs:61-67, 163-166)
+    const float x = x2n + dtb;
+    const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
+    sc[0] = expf(ssm_a * sp);
+  } else if (tid == 65) {
+    sc[1] = sigmoidf_(x2n);  // beta = sigmoid(b)
+  }
+  // per-head L2 norms of q and k (ssm.rs:523-530): waves 0-1 hold q, waves 2-3 hold k
   const float s2 = wave_sum(qk * qk);
   if ((tid & 63u) == 0) red[tid >> 6] = s2;
   __syncthreads();
@@ -422,31 +488,15 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
     const float ink = 1.0f / sqrtf((red[2] + red[3]) + 1e-6f);
     ks[tid - HD] = qk * ink;
   }
-  if (tid == 0) {
-    const float al = proj(a.off_a + vh), be = proj(a.off_b + vh);
-    const float x = al + a.dt_bias[vh];
-    const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
-    sc[0] = expf(a.ssm_a[vh] * sp);  // decay
-    sc[1] = sigmoidf_(be);            // beta
-  }
-  if (tid >= 64 && tid < 96) {
-    const int r = tid - 64;
-    const int64_t zi = (int64_t)vh * HD + quarter * 32 + r;
-    a.zs[zi] = siluf_(proj(a.off_z + zi));
-  }
   __syncthreads();
 
-  // recurrence on rows i = 32*quarter + i_loc, k-slice j in [16*js, 16*js+16)
+  // ---- gated delta rule on rows i (ssm.rs:378-418) ----
   const float decay = sc[0], beta = sc[1];
-  const int i = quarter * 32 + i_loc;
-  float* S = a.state + (size_t)vh * HD * HD;
-  float s[16];
   float kvp = 0.f;
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
-    const int j = js * 16 + jj;
-    s[jj] = S[(size_t)j * HD + i] * decay;
-    kvp = __builtin_fmaf(s[jj], ks[j], kvp);
+    s[jj] *= decay;
+    kvp = __builtin_fmaf(s[jj], ks[js * 16 + jj], kvp);
   }
   part[js][i_loc] = kvp;
   __syncthreads();
@@ -466,8 +516,7 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
     S[(size_t)j * HD + i] = s[jj];
     yp = __builtin_fmaf(s[jj], qs[j], yp);
   }
-  __syncthreads();
-  part[js][i_loc] = yp;
+  part[js][i_loc] = yp;  // the kv reads of part finished before the previous barrier
   __syncthreads();
   if (js == 0) {
     float yy = 0.f;
@@ -527,11 +576,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   const int half = a.rope_dim / 2;
   const float* cs = a.rope + (size_t)P * a.rope_dim;
 
-  auto proj = [&](int64_t row) {
-    float d = 0.f;
-    for (int k = 0; k < a.np; ++k) d += a.p_in[(size_t)k * a.ldp + row];
-    return d * inv;
-  };
+  auto proj = [&](int64_t row) { return sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, row) * inv; };
   // raw q of the group's heads, one dim per thread
   float qv[GRP];
 #pragma unroll
@@ -616,8 +661,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   }
   const float* kb = a.kcache + (size_t)kvh * a.max_ctx * HD;
   const float* vb = a.vcache + (size_t)kvh * a.max_ctx * HD;
-  for (int p = p0 + (int)wave; p < p1; p += 4) {
-    float4 k4, v4;
+  auto loadkv = [&](int p, float4& k4, float4& v4) {
     if (p == P) {
       k4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
       v4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
@@ -625,6 +669,20 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
       k4 = *reinterpret_cast<const float4*>(kb + (size_t)p * HD + 4 * lane);
       v4 = *reinterpret_cast<const float4*>(vb + (size_t)p * HD + 4 * lane);
     }
+  };
+  // software pipeline: positions p, p+4 and p+8 of this wave are in flight together
+  int p = p0 + (int)wave;
+  float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka, kb1 = ka, vb1 = ka;
+  if (p < p1) loadkv(p, ka, va);
+  if (p + 4 < p1) loadkv(p + 4, kb1, vb1);
+  for (; p < p1; p += 4) {
+    float4 kc = ka, vc = va;
+    if (p + 8 < p1) loadkv(p + 8, kc, vc);
+    const float4 k4 = ka, v4 = va;
+    ka = kb1;
+    va = vb1;
+    kb1 = kc;
+    vb1 = vc;
 #pragma unroll
     for (int gi = 0; gi < GRP; ++gi) {
       float dp = q4[gi].x * k4.x;
@@ -689,8 +747,7 @@ __global__ __launch_bounds__(512) void final_reduce_kernel(const FinalArgs a) {
   const int64_t col = (int64_t)t * kTileCols + tid;
   float v = 0.f;
   if (col < a.H) {
-    float d = 0.f;
-    for (int k = 0; k < a.np; ++k) d += a.part[(size_t)k * a.ldp + col];
+    const float d = sum_strided<kMaxTilesF>(a.part, a.ldp, a.np, col);
     v = a.h_in[col] + d;
     a.h_out[col] = v;
   }

@@ -341,6 +341,24 @@ int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumula
   return matvec_impl(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
 }
 
+int dz_q1_0_gemv_partials(dz_mat* m, const float* x_dev, float* part_dev, void* stream) {
+  if (!m || !x_dev || !part_dev) return set_error(DZ_ERR_TENSOR, "gemv_partials: null pointer");
+  int rc = ensure_device();
+  if (rc) return rc;
+  if ((rc = prepare_gemv_kernels())) return rc;
+  const Q1Dev* ds[1] = {&m->d};
+  GemvPlan p;
+  if ((rc = plan_gemv(ds, 1, 1, &p))) return rc;
+  PlainSrc src{x_dev, m->d.cols};
+  PartialDst dst{part_dev, p.ld};
+  DZ_HIP_CHECK(launch_gemv(p, src, dst, stream ? (hipStream_t)stream : lib_stream()));
+  return DZ_OK;
+}
+
+size_t dz_q1_0_partials_ld(const dz_mat* m) { return m ? (size_t)(m->d.nrb * kRowBlock) : 0; }
+
+int dz_q1_0_ntiles(const dz_mat* m) { return m ? (int)m->d.ntiles : 0; }
+
 static int matvec_host(dz_mat* const* mats, int n, const float* x, float* const* ys, int accumulate) {
   if (n < 1 || n > 8) return set_error(DZ_ERR_TENSOR, "matvec: %d matrices (1..8 supported)", n);
   if (!x) return set_error(DZ_ERR_TENSOR, "matvec: null x");

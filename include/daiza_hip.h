@@ -91,7 +91,16 @@ int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* cons
  * without a host synchronisation.  The token loop uses the fused kernels instead. */
 int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);
 
-/* Dequantised rows [r0, r0+n) as f32 (w = bit ? +scale : -scale, exact f16->f32).
+/* Split-K form on device pointers: writes part_dev[t][r] for K tiles t = 0..ceil(cols/512)-1 and
+ * rows r < dz_q1_0_partials_ld(m) (row count padded to 64), so that y[r] = sum_t part[t][r] in
+ * tile order.  For callers that fuse the tile sum into their next kernel, as the token loop does
+ * for every projection; y = W x of matvec_into_slice (weights.rs:123-325) without the final sum. */
+int dz_q1_0_gemv_partials(dz_mat* m, const float* x_dev, float* part_dev, void* stream);
+size_t dz_q1_0_partials_ld(const dz_mat* m);
+int dz_q1_0_ntiles(const dz_mat* m);
+
+/* Dequantised rows [r0, r0+n) as f32, w = (bit*2 - 1) * f16_to_f32(scale) with the reference's
+ * f16_to_f32 (quant.rs:39-74) bit for bit, including its handling of subnormal scales.
  * Replaces dequantize_q1_0_row_into (quant.rs:161-194) / row_into_slice (weights.rs:106). */
 int dz_q1_0_dequant_rows(dz_mat* m, size_t r0, size_t n, float* out);
 

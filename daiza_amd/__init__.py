@@ -111,6 +111,7 @@ def lib():
 
 _MODEL_PROTOS = {
     "dz_config_bonsai27b": ([_vp, ctypes.c_int32], None),
+    "dz_model_create": ([_vp, _vp, ctypes.c_int, ctypes.POINTER(_vp)], ctypes.c_int),
     "dz_model_create_synth": ([_vp, ctypes.c_uint64, ctypes.POINTER(_vp)], ctypes.c_int),
     "dz_model_free": ([_vp], ctypes.c_int),
     "dz_model_weight_bytes": ([_vp, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),

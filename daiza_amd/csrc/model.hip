@@ -439,17 +439,20 @@ static int gemv(const Q1Dev& mat, int tpw, const Src& src, const Dst& dst, hipSt
 }
 
 static int launch_attention(int grp, dim3 grid, const AttnArgs& a, hipStream_t s) {
-  switch (grp) {
-    case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(attention_kernel<3>, grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, s, a); break;
-    case 6: hipLaunchKernelGGL(attention_kernel<6>, grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, s, a); break;
-    default: return set_error(DZ_ERR_UNSUPPORTED, "GQA group %d", grp);
-  }
-  DZ_HIP_CHECK(hipGetLastError());
-  return DZ_OK;
+  return with_np_bucket(a.np, [&](auto B) -> int {
+    constexpr int NB = decltype(B)::value;
+    switch (grp) {
+      case 1: hipLaunchKernelGGL((attention_kernel<1, NB>), grid, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((attention_kernel<2, NB>), grid, dim3(256), 0, s, a); break;
+      case 3: hipLaunchKernelGGL((attention_kernel<3, NB>), grid, dim3(256), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((attention_kernel<4, NB>), grid, dim3(256), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((attention_kernel<6, NB>), grid, dim3(256), 0, s, a); break;
+      case 8: hipLaunchKernelGGL((attention_kernel<8, NB>), grid, dim3(256), 0, s, a); break;
+      default: return set_error(DZ_ERR_UNSUPPORTED, "GQA group %d", grp);
+    }
+    DZ_HIP_CHECK(hipGetLastError());
+    return DZ_OK;
+  });
 }
 
 // The mixer of one layer on the residual held in (h_in + parts): norm + in-proj GEMV, then the
@@ -467,11 +470,12 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
   const int64_t kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd, qkvd = 2 * kdim + inner;
   int rc;
   int64_t ld_l = 0;
-  {
-    ResidSrc src{h_in, parts, np, ldp, l.attn_norm, h_mid, ss_mid, H};
+  rc = with_np_bucket(np, [&](auto B) -> int {
+    ResidSrc<decltype(B)::value> src{h_in, parts, np, ldp, l.attn_norm, h_mid, ss_mid, H};
     PartialDst dst{x->p_in, l.in_proj.nrb * kRowBlock};
-    if ((rc = gemv(l.in_proj, 1, src, dst, s, &ld_l))) return rc;
-  }
+    return gemv(l.in_proj, 1, src, dst, s, &ld_l);
+  });
+  if (rc) return rc;
   const int nin = (int)l.in_proj.ntiles;
   if (!l.attn) {
     DeltaArgs a;
@@ -497,8 +501,12 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
     a.off_a = qkvd + inner;
     a.off_b = qkvd + inner + c.ssm_v_heads;
     a.ring_base_ptr = x->ring_base_dev + l.kind_idx;
-    hipLaunchKernelGGL(deltanet_kernel, dim3((unsigned)(c.ssm_v_heads * 4)), dim3(256), 0, s, a);
-    DZ_HIP_CHECK(hipGetLastError());
+    rc = with_np_bucket(nin, [&](auto B) -> int {
+      hipLaunchKernelGGL(deltanet_kernel<decltype(B)::value>, dim3((unsigned)(c.ssm_v_heads * 4)), dim3(256), 0, s, a);
+      DZ_HIP_CHECK(hipGetLastError());
+      return DZ_OK;
+    });
+    if (rc) return rc;
     GatedYSrc src{x->y, x->zs, l.ssm_norm, inner, 1e-6f};
     PartialDst dst{x->p_o, ld_h};
     if ((rc = gemv(l.out_proj, 1, src, dst, s))) return rc;
@@ -525,10 +533,13 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
     a.nq = c.n_head;
     a.nkv = c.n_head_kv;
     if ((rc = launch_attention(c.n_head / c.n_head_kv, dim3((unsigned)(c.n_head_kv * x->gmax)), a, s))) return rc;
-    AttnOutSrc src{x->apart, x->gmax, c.head_dim, (int64_t)c.n_head * c.head_dim, x->st, x->p_in, nin, ld_l,
-                   ss_mid, th, H, c.rms_eps};
-    PartialDst dst{x->p_o, ld_h};
-    if ((rc = gemv(l.out_proj, 1, src, dst, s))) return rc;
+    rc = with_np_bucket(nin, [&](auto B) -> int {
+      AttnOutSrc<decltype(B)::value> src{x->apart, x->gmax, c.head_dim, (int64_t)c.n_head * c.head_dim, x->st,
+                                         x->p_in, nin, ld_l, ss_mid, th, H, c.rms_eps};
+      PartialDst dst{x->p_o, ld_h};
+      return gemv(l.out_proj, 1, src, dst, s);
+    });
+    if (rc) return rc;
   }
   return DZ_OK;
 }
@@ -563,20 +574,26 @@ static int enqueue_token(dz_ctx* x, hipStream_t s) {
     const int np = li == 0 ? 0 : (int)m->L[li - 1].down.ntiles;
     if ((rc = enqueue_mixer(x, li, h_in, x->p_down, np, ld_h, x->h[0], x->ss[0], s))) return rc;
     // post-attention norm + gate/up (block.rs:101-120, mlp.rs:28-47)
-    {
-      ResidSrc src{x->h[0], x->p_o, (int)l.out_proj.ntiles, ld_h, l.post_norm, x->h[1], x->ss[1], H};
+    rc = with_np_bucket((int)l.out_proj.ntiles, [&](auto B) -> int {
+      ResidSrc<decltype(B)::value> src{x->h[0], x->p_o, (int)l.out_proj.ntiles, ld_h, l.post_norm, x->h[1], x->ss[1], H};
       PartialDst dst{x->p_gu, ld_gu};
-      if ((rc = gemv(l.gate_up, 1, src, dst, s))) return rc;
-    }
-    {
-      SwigluSrc src{x->p_gu, (int)l.gate_up.ntiles, ld_gu, F, x->ss[1], th, H, c.rms_eps};
+      return gemv(l.gate_up, 1, src, dst, s);
+    });
+    if (rc) return rc;
+    rc = with_np_bucket((int)l.gate_up.ntiles, [&](auto B) -> int {
+      SwigluSrc<decltype(B)::value> src{x->p_gu, (int)l.gate_up.ntiles, ld_gu, F, x->ss[1], th, H, c.rms_eps};
       PartialDst dst{x->p_down, ld_h};
-      if ((rc = gemv(l.down, 1, src, dst, s))) return rc;
-    }
+      return gemv(l.down, 1, src, dst, s);
+    });
+    if (rc) return rc;
   }
   FinalArgs fa{x->h[1], x->p_down, (int)m->L[c.n_layers - 1].down.ntiles, ld_h, x->h_fin, x->ss_fin, H};
-  hipLaunchKernelGGL(final_reduce_kernel, dim3((unsigned)th), dim3(512), 0, s, fa);
-  DZ_HIP_CHECK(hipGetLastError());
+  rc = with_np_bucket(fa.np, [&](auto B) -> int {
+    hipLaunchKernelGGL(final_reduce_kernel<decltype(B)::value>, dim3((unsigned)th), dim3(512), 0, s, fa);
+    DZ_HIP_CHECK(hipGetLastError());
+    return DZ_OK;
+  });
+  if (rc) return rc;
   NormedSrc src{x->h_fin, m->output_norm, x->ss_fin, th, H, c.rms_eps};
   LogitsDst dst{x->logits, c.vocab, x->am_val, x->am_idx};
   if ((rc = gemv(m->lm_head, (int)m->lm_head.ntiles, src, dst, s))) return rc;
@@ -597,10 +614,17 @@ int dz::prepare_gemv_kernels() {
   static bool done = false;
   if (done) return DZ_OK;
   int rc;
-  if ((rc = set_gemv_attr<ResidSrc, PartialDst>())) return rc;
-  if ((rc = set_gemv_attr<SwigluSrc, PartialDst>())) return rc;
+  for (int np : {2, 4, 8, 12, 16, 24, 36, 48}) {
+    rc = with_np_bucket(np, [&](auto B) -> int {
+      constexpr int NB = decltype(B)::value;
+      int r;
+      if ((r = set_gemv_attr<ResidSrc<NB>, PartialDst>())) return r;
+      if ((r = set_gemv_attr<SwigluSrc<NB>, PartialDst>())) return r;
+      return set_gemv_attr<AttnOutSrc<NB>, PartialDst>();
+    });
+    if (rc) return rc;
+  }
   if ((rc = set_gemv_attr<GatedYSrc, PartialDst>())) return rc;
-  if ((rc = set_gemv_attr<AttnOutSrc, PartialDst>())) return rc;
   if ((rc = set_gemv_attr<NormedSrc, LogitsDst>())) return rc;
   if ((rc = set_gemv_attr<PlainSrc, PartialDst>())) return rc;
   done = true;
@@ -972,8 +996,12 @@ int dz_ctx_mixer_step(dz_ctx* x, int layer, float* h) {
   int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s);
   if (rc) return rc;
   FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden};
-  hipLaunchKernelGGL(final_reduce_kernel, dim3((unsigned)th), dim3(512), 0, x->s, fa);
-  DZ_HIP_CHECK(hipGetLastError());
+  rc = with_np_bucket(fa.np, [&](auto B) -> int {
+    hipLaunchKernelGGL(final_reduce_kernel<decltype(B)::value>, dim3((unsigned)th), dim3(512), 0, x->s, fa);
+    DZ_HIP_CHECK(hipGetLastError());
+    return DZ_OK;
+  });
+  if (rc) return rc;
   DZ_HIP_CHECK(hipMemcpyAsync(h, x->h_fin, (size_t)c.hidden * 4, hipMemcpyDeviceToHost, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
   return ctx_set_pos_dev(x, P + 1);

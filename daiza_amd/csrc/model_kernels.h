@@ -11,6 +11,8 @@
 #pragma once
 #include "q1_gemv.h"
 
+#include <type_traits>
+
 namespace dz {
 
 // Position/token bookkeeping of the token being processed (device resident).
@@ -69,18 +71,42 @@ __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x));
 constexpr int kMaxTilesH = 16;
 constexpr int kMaxTilesF = 48;
 
-// sum_{k<n} p[k*ld + idx] in order k = 0..n-1, with all n loads issued before the first add
-// (one memory round trip instead of n).
+// Calls f(std::integral_constant<int, B>{}) with the smallest partial-count bucket B >= np, so
+// that a consumer's unconditional loads (sum_strided) waste at most a few slots.
+template <class F>
+__host__ inline auto with_np_bucket(int np, F&& f) {
+  if (np <= 2) return f(std::integral_constant<int, 2>{});
+  if (np <= 4) return f(std::integral_constant<int, 4>{});
+  if (np <= 8) return f(std::integral_constant<int, 8>{});
+  if (np <= 12) return f(std::integral_constant<int, 12>{});
+  if (np <= 16) return f(std::integral_constant<int, 16>{});
+  if (np <= 24) return f(std::integral_constant<int, 24>{});
+  if (np <= 36) return f(std::integral_constant<int, 36>{});
+  return f(std::integral_constant<int, 48>{});
+}
+
+// sum_{k<n} p[k*ld + idx] in order k = 0..n-1 (0 when n == 0), n <= MAXN, with every load
+// issued before the first add: one memory round trip instead of n.  The loads are unconditional
+// -- slots k >= n re-read slot n-1 (same cache line, no extra memory traffic) and are masked out
+// of the sum -- and walk one pointer, so no branch, wait or per-slot scalar address sits between
+// them.
 template <int MAXN>
 __device__ __forceinline__ float sum_strided(const float* __restrict__ p, int64_t ld, int n, int64_t idx) {
+  if (n <= 0) return 0.f;
   float v[MAXN];
+  const float* q = p + idx;
+  // keep the stride in vector registers: a wave-uniform stride would be scalarised into MAXN live
+  // 64-bit scalar addresses (spilled to VGPR lanes) before the first load could issue
+  int64_t step = ld;
+  asm volatile("" : "+v"(step));
 #pragma unroll
-  for (int k = 0; k < MAXN; ++k)
-    if (k < n) v[k] = p[(size_t)k * ld + idx];
+  for (int k = 0; k < MAXN; ++k) {
+    v[k] = *q;
+    q += (k + 1 < n) ? step : 0;
+  }
   float d = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXN; ++k)
-    if (k < n) d += v[k];
+  for (int k = 0; k < MAXN; ++k) d += (k < n) ? v[k] : 0.f;
   return d;
 }
 
@@ -95,6 +121,8 @@ __device__ __forceinline__ float inv_rms_from(const float* ss, int nss, int64_t 
 // ---------------------------------------------------------------- GEMV sources
 
 // LUT input (h + sum_k part_k) * w; chunk 0 also writes h_out and the tile's sum of squares.
+// NP bounds the partial count np (a launch picks the smallest instantiation that holds np).
+template <int NP>
 struct ResidSrc {
   const float* h_in;
   const float* part;
@@ -106,11 +134,12 @@ struct ResidSrc {
   int64_t H;
   __device__ __forceinline__ void stage(float* xs, float* red, int t, unsigned tid, int nt, int64_t chunk) const {
     float ssl = 0.f;
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       float u = 0.f;
       if (col < H) {
-        const float d = sum_strided<kMaxTilesF>(part, ldp, np, col);
+        const float d = sum_strided<NP>(part, ldp, np, col);
         const float v = np ? h_in[col] + d : h_in[col];
         u = v * w[col];
         if (chunk == 0) h_out[col] = v;
@@ -126,6 +155,7 @@ struct ResidSrc {
 };
 
 // LUT input silu(g) * u with g, u = inv_rms * sum of gate/up partials (swiglu_inplace_simd, simd_exp.rs:273-296).
+template <int NP>
 struct SwigluSrc {
   const float* part;  // [np][ldp]: gate rows [0, F), up rows [F, 2F)
   int np;
@@ -137,12 +167,13 @@ struct SwigluSrc {
   float eps;
   __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
     const float inv = inv_rms_from(ss, nss, H, eps);
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       float u = 0.f;
       if (col < F) {
-        float g = sum_strided<kMaxTilesH>(part, ldp, np, col);
-        float up = sum_strided<kMaxTilesH>(part, ldp, np, F + col);
+        float g = sum_strided<NP>(part, ldp, np, col);
+        float up = sum_strided<NP>(part, ldp, np, F + col);
         g *= inv;
         up *= inv;
         u = siluf_(g) * up;
@@ -162,7 +193,8 @@ struct GatedYSrc {
   float eps;
   __device__ __forceinline__ void stage(float* xs, float* red, int t, unsigned tid, int nt, int64_t) const {
     // 512 columns = 4 heads of 128; wave h (< 4) reduces head h
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       xs[i] = col < K ? y[col] : 0.f;
     }
@@ -174,7 +206,8 @@ struct GatedYSrc {
       if (l == 0) red[w] = 1.0f / sqrtf(s * (1.0f / 128.0f) + eps);
     }
     __syncthreads();
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       xs[i] = col < K ? ((xs[i] * red[i >> 7]) * nw[i & 127]) * zs[col] : 0.f;
     }
@@ -183,6 +216,7 @@ struct GatedYSrc {
 
 // LUT input of the attention out-projection: combine the split-K softmax partials of the head
 // and gate with sigmoid (attention.rs:189-203).  Partial record: [m, l, o[head_dim]].
+template <int NP>
 struct AttnOutSrc {
   const float* apart;  // [n_head][gmax][2 + hd]
   int gmax;
@@ -202,7 +236,8 @@ struct AttnOutSrc {
     if (chunk < 16) chunk = 16;
     const int geff = (ctx + chunk - 1) / chunk;
     const float inv = inv_rms_from(ss, nss, H, eps);
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       float u = 0.f;
       if (col < K) {
@@ -218,7 +253,7 @@ struct AttnOutSrc {
           o = __builtin_fmaf(r[2 + d], e, o);
         }
         const int64_t grow = (int64_t)h * 2 * hd + hd + d;
-        const float gate = sum_strided<kMaxTilesH>(p_in, ldp, np, grow) * inv;
+        const float gate = sum_strided<NP>(p_in, ldp, np, grow) * inv;
         u = (o * (1.0f / l)) * sigmoidf_(gate);
       }
       xs[i] = u;
@@ -236,7 +271,8 @@ struct NormedSrc {
   float eps;
   __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
     const float inv = inv_rms_from(ss, nss, H, eps);
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       xs[i] = col < H ? (h[col] * inv) * w[col] : 0.f;
     }
@@ -359,9 +395,10 @@ __global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) 
     a.toklog[st->pos] = tok;
   }
   if (a.emb_f16) {
+    // an F16 tensor converts element-wise with the reference's f16_to_f32 (Tensor::load_as_f32,
+    // tensor/tensor.rs:62-76), subnormal handling included
     const uint16_t* row = a.emb_f16 + (size_t)tok * a.H;
-    for (int64_t c = tid; c < a.H; c += blockDim.x)
-      a.emb_out[c] = (float)__builtin_bit_cast(_Float16, row[c]);
+    for (int64_t c = tid; c < a.H; c += blockDim.x) a.emb_out[c] = ref_f16_to_f32_dev(row[c]);
   } else {
     // dequantize_q1_0_row_into (quant.rs:161-194) from the GEMV layout
     const int64_t rb = tok / kRowBlock;
@@ -406,6 +443,7 @@ struct DeltaArgs {
 // per-head L2 norm of q/k, q *= 1/sqrt(128), g = A*softplus(alpha + dt_bias), decay = exp(g),
 // beta = sigmoid(b), then for each state row i: s *= decay; kv = s.k; d = (v_i - kv)*beta;
 // s += d*k; y_i = s.q.  k-head of v-head vh is vh % nkh (ssm.rs:558-561).
+template <int NP>
 __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   constexpr int HD = 128;
   __shared__ float qs[HD], ks[HD], vs[32], red[16], part[8][32], dsh[32], sc[4];
@@ -427,7 +465,7 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   const float inv = inv_rms_from(a.ss, a.nss, a.H, a.rms_eps);
   // conv channel of this thread: q (tid < 128) or k (tid >= 128) of k-head kh
   const int64_t ch = tid < HD ? (int64_t)kh * HD + tid : kdim + (int64_t)kh * HD + (tid - HD);
-  const float xq = sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, ch);
+  const float xq = sum_strided<NP>(a.p_in, a.ldp, a.np, ch);
   const float r1 = a.conv[(size_t)((hb + 1) & 3) * qkvd + ch], r2 = a.conv[(size_t)((hb + 2) & 3) * qkvd + ch],
               r3 = a.conv[(size_t)((hb + 3) & 3) * qkvd + ch];
   const float w0 = a.conv_w[ch], w1 = a.conv_w[qkvd + ch], w2 = a.conv_w[2 * qkvd + ch], w3 = a.conv_w[3 * qkvd + ch];
@@ -438,7 +476,7 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   else if (tid == 64) row2 = a.off_a + vh;
   else if (tid == 65) row2 = a.off_b + vh;
   float x2 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f, u0 = 0.f, u1 = 0.f, u2 = 0.f, u3 = 0.f;
-  if (row2 >= 0) x2 = sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, row2);
+  if (row2 >= 0) x2 = sum_strided<NP>(a.p_in, a.ldp, a.np, row2);
   if (tid < 32) {
     v1 = a.conv[(size_t)((hb + 1) & 3) * qkvd + row2];
     v2 = a.conv[(size_t)((hb + 2) & 3) * qkvd + row2];
@@ -555,7 +593,7 @@ struct AttnArgs {
 // q_norm/k_norm, then the reference's partial RoPE on the first rope_dim dims with both terms
 // added (rope.rs:205-208), and q *= 1/sqrt(hd).  The chunk holding the new position also appends
 // its k/v to the cache.  hd = 256, 256 threads (4 waves).
-template <int GRP>
+template <int GRP, int NP>
 __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   constexpr int HD = 256;
   __shared__ float qs[GRP][HD];
@@ -576,7 +614,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   const int half = a.rope_dim / 2;
   const float* cs = a.rope + (size_t)P * a.rope_dim;
 
-  auto proj = [&](int64_t row) { return sum_strided<kMaxTilesH>(a.p_in, a.ldp, a.np, row) * inv; };
+  auto proj = [&](int64_t row) { return sum_strided<NP>(a.p_in, a.ldp, a.np, row) * inv; };
   // raw q of the group's heads, one dim per thread
   float qv[GRP];
 #pragma unroll
@@ -740,6 +778,7 @@ struct FinalArgs {
   int64_t H;
 };
 
+template <int NP>
 __global__ __launch_bounds__(512) void final_reduce_kernel(const FinalArgs a) {
   __shared__ float red[16];
   const int t = blockIdx.x;
@@ -747,7 +786,7 @@ __global__ __launch_bounds__(512) void final_reduce_kernel(const FinalArgs a) {
   const int64_t col = (int64_t)t * kTileCols + tid;
   float v = 0.f;
   if (col < a.H) {
-    const float d = sum_strided<kMaxTilesF>(a.part, a.ldp, a.np, col);
+    const float d = sum_strided<NP>(a.part, a.ldp, a.np, col);
     v = a.h_in[col] + d;
     a.h_out[col] = v;
   }

@@ -132,7 +132,8 @@ __device__ __forceinline__ const uint8_t* unit_ptr(const GemvGrid& g, int64_t rb
   return g.seg[s].data + ((size_t)lrb * g.ntiles + t) * kUnitBytes;
 }
 
-// Src: stage(xs, red, tile, tid, nthreads, chunk) writes the 512 LUT inputs of `tile` into LDS xs;
+// Src: stage(xs, red, tile, tid, nthreads, chunk) writes the 512 LUT inputs of `tile` into LDS xs,
+//      one column per thread (nthreads == kTileCols);
 //      `red` is 16 floats of LDS scratch for reductions; chunk is the workgroup's row-block chunk
 //      (sources that also publish per-tile values do so from chunk 0 only).
 // Dst: store(tg, rb, lane, acc) consumes the row result (a partial when ntiles > tpw).
@@ -143,6 +144,7 @@ __global__ __launch_bounds__(NWAVES * 64) void gemv_lut_kernel(const GemvGrid g,
   float* red = reinterpret_cast<float*>(smem + kLutBytes);
   float* xs = red + 16;
   constexpr int NT = NWAVES * 64;
+  static_assert(NT == kTileCols, "staging runs one thread per tile column");
   const unsigned tid = threadIdx.x, lane = tid & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar row-block math
   const int tg = (int)(blockIdx.x % (unsigned)g.n_tg);
@@ -194,7 +196,8 @@ struct PlainSrc {  // x[K] in device memory, zero beyond K
   const float* x;
   int64_t K;
   __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
-    for (int i = tid; i < kTileCols; i += nt) {
+    {  // one thread per tile column (nt == kTileCols)
+      const int i = (int)tid;
       const int64_t col = (int64_t)t * kTileCols + i;
       xs[i] = col < K ? x[col] : 0.f;
     }

@@ -31,6 +31,8 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         L.or_f16_to_f32.restype = ctypes.c_float
         L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f16_to_f32_bits.restype = ctypes.c_uint32
+        L.or_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
         L.or_f16_to_f32_fast.restype = ctypes.c_float
         L.or_f16_to_f32_fast.argtypes = [ctypes.c_uint16]
         L.or_dequant_row.argtypes = [u8p, ctypes.c_size_t, ctypes.c_size_t, f32p]
@@ -70,6 +72,7 @@ def lib():
         L.or_ctx_pos.restype = ctypes.c_int
         L.or_ctx_pos.argtypes = [ctypes.c_void_p]
         L.or_ctx_set_pos.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.or_model_embd_row.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
         L.or_forward_token.restype = ctypes.c_int
         L.or_forward_token.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
         L.or_mixer_step.argtypes = [ctypes.c_void_p, ctypes.c_int, f32p]
@@ -83,6 +86,8 @@ def lib():
                                          ctypes.c_uint64, ctypes.c_uint64, u8p]
         L.or_synth_normal_f32.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
                                           ctypes.c_uint64, ctypes.c_double, ctypes.c_double, f32p]
+        L.or_synth_embd_row_f16.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
+                                            ctypes.POINTER(ctypes.c_uint16)]
         L.or_f32_to_f16.restype = ctypes.c_uint16
         L.or_f32_to_f16.argtypes = [ctypes.c_float]
         _lib = L
@@ -98,6 +103,12 @@ def synth_q1_0(seed, kind, layer, rows, cols, r0=0):
 def synth_normal(seed, kind, layer, n, mean=0.0, sigma=1.0, i0=0):
     out = np.empty(n, np.float32)
     lib().or_synth_normal_f32(seed, kind, layer, i0, n, mean, sigma, _f(out))
+    return out
+
+
+def synth_embd_row_f16(seed, token, hidden):
+    out = np.empty(hidden, np.uint16)
+    lib().or_synth_embd_row_f16(seed, int(token), hidden, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)))
     return out
 
 
@@ -179,6 +190,11 @@ class Model:
         logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
         am = lib().or_forward_token(self._c, int(token), _f(logits) if want_logits else None)
         return am, logits
+
+    def embd_row(self, token):
+        out = np.empty(self.cfg.hidden, np.float32)
+        lib().or_model_embd_row(self._m, int(token), _f(out))
+        return out
 
     def mixer_step(self, layer, h):
         h = np.ascontiguousarray(h, np.float32).copy()

@@ -7,6 +7,12 @@
  * (Rust never contracts a*b+c) and the vector code issues the reference's intrinsics in its order.
  *
  * Citations are to /root/reference/Daiza-engine/src/... unless the path says otherwise.
+ *
+ * Pinning (tests/test_oracle_cpu.py): every function is checked against known answers, closed
+ * forms, float64 brute force or the independent float64 restatement tests/npref.py.  Parity
+ * unpinned (matched within tolerance only; only running the reference could fix the bits):
+ * sigmoid_ps / silu_ps (vendor-specific _mm256_rcp_ps) and libm expf/logf/powf/sinf/cosf, which
+ * the reference takes from its platform's libm and this file from glibc.
  */
 #include "oracle.h"
 #include "daiza_synth.h"
@@ -43,6 +49,14 @@ float or_f16_to_f32(uint16_t bits) {
   float f;
   memcpy(&f, &out, 4);
   return f;
+}
+
+/* the same conversion returned as bits (a float return through ctypes would quiet a signalling NaN) */
+uint32_t or_f16_to_f32_bits(uint16_t bits) {
+  float f = or_f16_to_f32(bits);
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
 }
 
 /* tensor/quant.rs:86-108 — branch-free variant that flushes subnormal scales to zero */
@@ -151,7 +165,8 @@ float or_dot_row_scalar(const uint8_t* aos, size_t row, size_t cols, const float
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (size_t g = 0; g < gpr; ++g) {
     const uint8_t* blk = rb + g * Q1_BLOCK;
-    float s = or_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    /* every AVX2 row kernel converts the scale with vcvtph2ps (exact IEEE, subnormals included) */
+    float s = _cvtsh_ss((unsigned short)(blk[0] | (blk[1] << 8)));
     const float* xp = x + g * Q1_GROUP;
     for (int l = 0; l < 8; ++l) {
       float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -900,19 +915,26 @@ void or_mixer_step(or_ctx* x, int li, float* h) {
   x->pos += 1; /* the step consumed one position (its KV entry / conv slot) */
 }
 
+/* forward.rs:212 token embedding row.  An F16 token_embd converts element-wise with f16_to_f32
+ * (Tensor::to_f32, tensor/tensor.rs:68-80); a Q1_0 one is dequantize_q1_0_row_into. */
+void or_model_embd_row(or_model* m, uint32_t token, float* out) {
+  size_t H = (size_t)m->cfg.hidden;
+  if (m->cfg.embd_f16) {
+    uint16_t* row = (uint16_t*)malloc(H * 2);
+    dz_synth_embd_row_f16(m->embd_key, token, H, row);
+    for (size_t i = 0; i < H; ++i) out[i] = or_f16_to_f32(row[i]);
+    free(row);
+  } else {
+    or_dequant_row(m->embd_q.q, token, H, out);
+  }
+}
+
 /* model/forward.rs:204-375 forward_single_token */
 int or_forward_token(or_ctx* x, uint32_t token, float* logits) {
   or_model* m = x->m;
   const dz_config* c = &m->cfg;
   size_t H = (size_t)c->hidden;
-  if (c->embd_f16) {
-    uint16_t* row = (uint16_t*)malloc(H * 2);
-    dz_synth_embd_row_f16(m->embd_key, token, H, row);
-    for (size_t i = 0; i < H; ++i) x->h[i] = or_f16_to_f32(row[i]);
-    free(row);
-  } else {
-    or_dequant_row(m->embd_q.q, token, H, x->h);
-  }
+  or_model_embd_row(m, token, x->h);
   or_rope_cos_sin(x->pos, m->freqs, c->rope_dim, x->co, x->si);
   for (int li = 0; li < c->n_layers; ++li) {
     if (m->L[li].is_attn) attn_forward(x, li, x->h);
@@ -975,3 +997,6 @@ void or_synth_normal_f32(uint64_t seed, int kind, int layer, uint64_t i0, uint64
   dz_synth_normal_f32(dz_key(seed, (uint32_t)kind, (uint32_t)layer), i0, n, mean, sigma, out);
 }
 uint16_t or_f32_to_f16(float v) { return dz_f32_to_f16(v); }
+void or_synth_embd_row_f16(uint64_t seed, uint32_t token, uint64_t hidden, uint16_t* out) {
+  dz_synth_embd_row_f16(dz_key(seed, DZ_K_EMBD, (uint32_t)-1), token, hidden, out);
+}

@@ -20,6 +20,7 @@ extern "C" {
 
 /* quant.rs:39-74 */
 float or_f16_to_f32(uint16_t bits);
+uint32_t or_f16_to_f32_bits(uint16_t bits);
 /* quant.rs:86-108 (scalar fallback only; flushes subnormals) */
 float or_f16_to_f32_fast(uint16_t bits);
 /* quant.rs:161-194 */
@@ -59,6 +60,7 @@ float or_lcg_next(uint64_t* state);
 void or_synth_q1_0_rows(uint64_t seed, int kind, int layer, uint64_t cols, uint64_t r0, uint64_t r1, uint8_t* out);
 void or_synth_normal_f32(uint64_t seed, int kind, int layer, uint64_t i0, uint64_t n, double mean, double sigma, float* out);
 uint16_t or_f32_to_f16(float v);
+void or_synth_embd_row_f16(uint64_t seed, uint32_t token, uint64_t hidden, uint16_t* out);
 
 /* ------------------------------ model ------------------------------ */
 typedef struct or_model or_model;
@@ -76,6 +78,7 @@ void or_ctx_free(or_ctx* c);
 int or_ctx_pos(or_ctx* c);
 void or_ctx_set_pos(or_ctx* c, int pos);
 /* forward_single_token (forward.rs:204-375); logits may be NULL; returns argmax */
+void or_model_embd_row(or_model* m, uint32_t token, float* out);
 int or_forward_token(or_ctx* c, uint32_t token, float* logits);
 /* h += mixer(rmsnorm(h)) of one layer (ssm_forward_into / attention_forward_into); pos += 1 */
 void or_mixer_step(or_ctx* c, int layer, float* h);

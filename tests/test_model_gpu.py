@@ -36,6 +36,25 @@ def test_small_forward_logits_and_argmax(dz, oracle):
     assert ctx.pos == om.pos == len(toks)
 
 
+def test_f16_embedding_subnormal_rows(dz, oracle):
+    """Tokens whose f16 embedding row holds subnormal halves: the row converts with the
+    reference's f16_to_f32 (tensor/tensor.rs:62-76, quant.rs:39-74) on the GPU as in the oracle."""
+    cfg = dz.Config.small(n_layers=1, max_ctx=16)
+    toks = []
+    for t in range(cfg.vocab):
+        row = oracle.synth_embd_row_f16(SEED, t, cfg.hidden)
+        if np.any(((row & 0x7C00) == 0) & ((row & 0x3FF) != 0)):
+            toks.append(t)
+        if len(toks) == 3:
+            break
+    assert toks, "no token with a subnormal embedding element in this vocabulary"
+    for t in toks:
+        m, ctx, om = _pair(dz, oracle, cfg)
+        _, lg = ctx.forward_single_token(t)
+        _, olg = om.forward(t)
+        assert normwise_rel(lg, olg) < 1e-4, t
+
+
 def test_small_decode_greedy_tokens(dz, oracle):
     cfg = dz.Config.small(n_layers=8, max_ctx=128)
     m, ctx, om = _pair(dz, oracle, cfg, seed=SEED + 1)

@@ -132,6 +132,7 @@ _MODEL_PROTOS = {
     "dz_ctx_set_pos": ([_vp, ctypes.c_int], ctypes.c_int),
     "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
     "dz_ctx_stream": ([_vp], _vp),
+    "dz_ctx_token_kernel": ([_vp], ctypes.c_int),
 }
 
 EXPORTED_SYMBOLS = [
@@ -270,6 +271,11 @@ class Context:
     @property
     def pos(self):
         return lib().dz_ctx_pos(self._h)
+
+    @property
+    def token_kernel(self):
+        """True when forwards run in the persistent token kernel (see dz_ctx_token_kernel)."""
+        return bool(lib().dz_ctx_token_kernel(self._h))
 
     def reset(self):
         _check(lib().dz_ctx_reset(self._h))

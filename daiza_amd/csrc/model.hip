@@ -3,9 +3,11 @@
 // (forward_single_token / forward_batch / ModelState, Daiza-engine/src/model/forward.rs).
 #include "runtime.h"
 #include "model_kernels.h"
+#include "ptk_kernel.h"
 #include "daiza_synth.h"
 
 #include <cmath>
+#include <cstdio>
 #include <functional>
 #include <cstdlib>
 #include <cstring>
@@ -71,6 +73,17 @@ struct dz_ctx {
   int pos_host = 0;            // mirror of TokState::pos_next
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
+  // persistent token kernel (used by forward_token / forward_batch / decode_greedy when enabled)
+  struct {
+    bool on = false;
+    dz::PtkPlan plan{};
+    dz::PtkLayer* layers_d = nullptr;
+    int* err = nullptr;           // [4]
+    float* logits_all = nullptr;  // [chunk][vocab]
+    int chunk = 32;
+    uint64_t gti = 0;             // index of the next token for tags and parity
+    const void* kfn = nullptr;
+  } ptk;
   std::vector<void*> allocs;
 };
 
@@ -756,6 +769,291 @@ static int ctx_set_pos_dev(dz_ctx* x, int pos) {
   return DZ_OK;
 }
 
+// ---------------------------------------------------------------- persistent token kernel (host)
+
+// Kernel instantiation for a model shape: partial-count buckets (K tiles of hidden, of the mixer
+// output width, of ffn) and the GQA group.  Other shapes run on the graph path.
+struct PtkShape {
+  int th, to, tf, grp, u_in, u_out, u_gu, u_dn, u_lm;
+};
+static const void* ptk_pick(const PtkShape& s) {
+  if (s.th <= 12 && s.to <= 12 && s.tf <= 36 && s.grp == 6 && s.u_in <= 2 && s.u_out <= 1 && s.u_gu <= 3 && s.u_dn <= 2 &&
+      s.u_lm <= 2)
+    return reinterpret_cast<const void*>(ptk_kernel<12, 12, 36, 6, 2, 1, 3, 2, 2>);
+  if (s.th <= 2 && s.to <= 2 && s.tf <= 2 && s.grp == 2 && s.u_in <= 1 && s.u_out <= 1 && s.u_gu <= 1 && s.u_dn <= 1 &&
+      s.u_lm <= 1)
+    return reinterpret_cast<const void*>(ptk_kernel<2, 2, 2, 2, 1, 1, 1, 1, 1>);
+  return nullptr;
+}
+
+// DAIZA_PTK=0 selects the graph path for new contexts.
+static bool ptk_wanted() {
+  const char* e = getenv("DAIZA_PTK");
+  return !(e && e[0] == '0');
+}
+
+// Builds the plan of a context; leaves ptk.on false when the shape or the device does not fit.
+static int ptk_prepare(dz_ctx* x) {
+  dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  int dev = 0;
+  DZ_HIP_CHECK(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  DZ_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+  int coop = 0;
+  DZ_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+  const int G = prop.multiProcessorCount;
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int grp = c.n_head / c.n_head_kv;
+  if (!coop || c.head_dim != 256 || c.ssm_state != 128 || G < 8 || G > kPtkThreads || c.n_layers > kPtkMaxLayers)
+    return DZ_OK;
+  // shape limits of the static work split: row-block slots per wave of each matrix kind
+  const int nrb_h = (int)(ld_h / kRowBlock), nrb_gu = (int)(ld_gu / kRowBlock), nrb_v = (int)m->lm_head.nrb;
+  auto slots = [&](int T, int nrb) {
+    if (T > G) return 1 << 20;
+    int mx = 0;
+    for (int t = 0; t < T; ++t) {
+      const int nw = tile_first_wg(t + 1, T, G) - tile_first_wg(t, T, G);
+      mx = std::max(mx, (nrb + nw - 1) / nw);
+    }
+    return (mx + kPtkWaves - 1) / kPtkWaves;
+  };
+  PtkShape sh{th, to, tf, grp, 0, 0, slots(th, nrb_gu), slots(tf, nrb_h), ((nrb_v + G - 1) / G + kPtkWaves - 1) / kPtkWaves};
+  for (auto& l : m->L) {
+    sh.u_in = std::max(sh.u_in, slots(th, (int)l.in_proj.nrb));
+    sh.u_out = std::max(sh.u_out, slots((int)l.out_proj.ntiles, nrb_h));
+  }
+  const void* kfn = ptk_pick(sh);
+  if (!kfn) return DZ_OK;
+  int occ = 0;
+  DZ_HIP_CHECK(hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
+  DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kPtkThreads, kPtkLds));
+  if (occ < 1) return DZ_OK;
+  const int gmax = std::min(64, G / std::max(1, c.n_head_kv));
+  bool ok = 4 * c.ssm_v_heads <= G && c.n_head_kv * gmax <= G && gmax >= 1 && c.rope_dim / 2 <= 256;
+  // column sums (ll_colsum): nc columns of K terms per workgroup
+  auto colq = [&](int n_items, int cols_per_item, int K) {
+    const int nc = (n_items + G - 1) / G * cols_per_item;
+    if (nc > kPtkThreads) return false;
+    const int nq = std::max(1, std::min(kPtkThreads / std::max(1, nc), K));
+    return (K + nq - 1) / nq <= kPtkColQ;
+  };
+  auto colq1 = [&](int n_items, int cols_per_item, int K) {  // one extra column of K terms
+    const int nc = (n_items + G - 1) / G * cols_per_item + 1;
+    if (nc > kPtkThreads) return false;
+    const int nq = std::max(1, std::min(kPtkThreads / nc, K));
+    return (K + nq - 1) / nq <= kPtkColQ;
+  };
+  ok = ok && colq(c.hidden, 1, to + 1) && colq(c.hidden, 1, tf + 1) && colq1(c.ffn, 2, th) &&
+       colq1(2 * c.n_head * c.head_dim + 2 * c.n_head_kv * c.head_dim, 1, th) && th <= 64;
+  if (!ok) return DZ_OK;
+  PtkPlan& P = x->ptk.plan;
+  memset(&P, 0, sizeof P);
+  P.G = G;
+  P.n_layers = c.n_layers;
+  P.H = c.hidden;
+  P.F = c.ffn;
+  P.vocab = c.vocab;
+  P.nT_h = th;
+  P.nrb_h = nrb_h;
+  P.nT_f = tf;
+  P.nrb_gu = nrb_gu;
+  P.nrb_v = nrb_v;
+  const int hd = c.ssm_state;
+  P.nkh = c.ssm_k_heads;
+  P.nvh = c.ssm_v_heads;
+  P.inner = c.ssm_v_heads * hd;
+  P.qkvd = 2 * c.ssm_k_heads * hd + P.inner;
+  P.off_z = P.qkvd;
+  P.off_a = P.qkvd + P.inner;
+  P.off_b = P.qkvd + P.inner + c.ssm_v_heads;
+  P.nq = c.n_head;
+  P.nkv = c.n_head_kv;
+  P.hd = c.head_dim;
+  P.rope_dim = c.rope_dim;
+  P.grp = grp;
+  P.gmax = gmax;
+  P.max_ctx = c.max_ctx;
+  P.eps = c.rms_eps;
+  P.embd_f16 = c.embd_f16;
+  // LL layout of one layer region (64-word aligned sub-buffers)
+  auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
+  int64_t o = 0;
+  auto take = [&](int64_t n) { const int64_t r = o; o += al(n); return r; };
+  const int64_t qdim = (int64_t)c.n_head * c.head_dim;
+  const int64_t attn_rows = 2 * qdim + 2 * (int64_t)c.n_head_kv * c.head_dim;
+  P.off.pin = take((int64_t)th * ld_in);
+  P.off.sst_in = take(th);
+  P.off.po = take((int64_t)to * ld_h);
+  P.off.hmid = take(ld_h);
+  P.off.sst_mid = take(th);
+  P.off.pgu = take((int64_t)th * ld_gu);
+  P.off.sw = take((int64_t)tf * kTileCols);
+  P.off.pd = take((int64_t)tf * ld_h);
+  P.off.h = take(ld_h);
+  P.off.y = take(P.inner);
+  P.off.zs = take(P.inner);
+  P.off.yss = take(4 * (int64_t)P.nvh);
+  P.off.qkv = take(attn_rows);
+  P.off.rec = take((int64_t)c.n_head * gmax * (2 + c.head_dim));
+  P.off.ao = take(qdim);
+  P.off.words = std::max<int64_t>(o, al(ld_h + 2 * (int64_t)G));
+  // phases: S, then 8 per DeltaNet layer / 10 per attention layer, then L
+  std::vector<PtkLayer> Ls((size_t)c.n_layers);
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
+  const int64_t hd2 = hd;
+  const int64_t qkvd = P.qkvd;
+  int ph = 1;
+  for (int i = 0; i < c.n_layers; ++i) {
+    LayerDev& l = m->L[i];
+    PtkLayer& y = Ls[(size_t)i];
+    memset(&y, 0, sizeof y);
+    y.attn = l.attn ? 1 : 0;
+    y.rows_in = (int)l.in_proj.rows;
+    y.nrb_in = (int)l.in_proj.nrb;
+    y.nt_out = (int)l.out_proj.ntiles;
+    y.w_in = l.in_proj.data;
+    y.w_out = l.out_proj.data;
+    y.w_gu = l.gate_up.data;
+    y.w_dn = l.down.data;
+    y.attn_norm = l.attn_norm;
+    y.post_norm = l.post_norm;
+    if (!l.attn) {
+      y.conv_w = l.conv_w;
+      y.ssm_a = l.ssm_a;
+      y.dt_bias = l.dt_bias;
+      y.ssm_norm = l.ssm_norm;
+      y.conv = x->conv + (size_t)l.kind_idx * 4 * qkvd;
+      y.state = x->ssm_state + (size_t)l.kind_idx * c.ssm_v_heads * hd2 * hd2;
+      y.ring_base = x->ring_base_dev + l.kind_idx;
+    } else {
+      y.q_norm = l.q_norm;
+      y.k_norm = l.k_norm;
+      y.kc = x->kv + (size_t)l.kind_idx * 2 * kvsz;
+      y.vc = y.kc + kvsz;
+    }
+    y.ph0 = ph;
+    ph += l.attn ? 10 : 8;
+  }
+  // the kernel assigns GEMV work per matrix kind: every layer of a kind has the same shapes
+  P.nrb_in_k[0] = P.nrb_in_k[1] = P.nt_out_k[0] = P.nt_out_k[1] = -1;
+  for (const PtkLayer& y : Ls) {
+    int& nrb = P.nrb_in_k[y.attn];
+    int& nto = P.nt_out_k[y.attn];
+    if ((nrb >= 0 && nrb != y.nrb_in) || (nto >= 0 && nto != y.nt_out)) return DZ_OK;
+    nrb = y.nrb_in;
+    nto = y.nt_out;
+  }
+  for (int k = 0; k < 2; ++k)
+    if (P.nrb_in_k[k] < 0) P.nrb_in_k[k] = P.nt_out_k[k] = 1;
+  P.ph_l = ph;
+  P.ppt = ph + 1;
+  P.w_lm = m->lm_head.data;
+  P.output_norm = m->output_norm;
+  P.emb_f16 = m->emb_f16;
+  P.emb_q1 = m->emb_q1.data;
+  P.emb_ntiles = (int)m->emb_q1.ntiles;
+  P.rope = x->rope;
+  P.st = x->st;
+  P.toklog = x->toklog;
+  P.logits = x->logits;
+  auto& A = x->allocs;
+  int rc;
+  const size_t ll_words = (size_t)2 * (c.n_layers + 1) * (size_t)P.off.words;
+  if ((rc = alloc_t(A, &P.ll, ll_words)) || (rc = alloc_t(A, &x->ptk.layers_d, Ls.size())) ||
+      (rc = alloc_t(A, &x->ptk.err, 4)) ||
+      (rc = alloc_t(A, &x->ptk.logits_all, (size_t)x->ptk.chunk * c.vocab)))
+    return rc;
+  DZ_HIP_CHECK(hipMemset(P.ll, 0, ll_words * sizeof(u64)));
+  DZ_HIP_CHECK(hipMemset(x->ptk.err, 0, 16));
+  DZ_HIP_CHECK(hipMemcpy(x->ptk.layers_d, Ls.data(), Ls.size() * sizeof(PtkLayer), hipMemcpyHostToDevice));
+  P.L = x->ptk.layers_d;
+  x->ptk.kfn = kfn;
+  x->ptk.gti = 0;
+  x->ptk.on = true;
+  return DZ_OK;
+}
+
+// Runs n tokens at positions pos_host.. in one cooperative launch: tokens [0, n_feed) take the fed
+// ids (already in x->feed), the rest the greedy pick.  toklog[pos + i] receives token i and
+// toklog[pos + n] the greedy pick after the last one; logits of the last token land in x->logits,
+// and with per_pos every token's logits in ptk.logits_all[i] (n <= ptk.chunk).
+static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0) {
+  const PtkPlan& P = x->ptk.plan;
+  if (x->pos_host + n > x->m->cfg.max_ctx)
+    return set_error(DZ_ERR_TENSOR, "context full: pos %d + %d > max_ctx %d", x->pos_host, n, x->m->cfg.max_ctx);
+  if (per_pos && n > x->ptk.chunk) return set_error(DZ_ERR_TENSOR, "per-position logits: %d tokens per launch", n);
+  // tags stay below 2^31: restart them (and clear every LL word) before they would pass it
+  if ((x->ptk.gti + (uint64_t)n + 2) * (uint64_t)P.ppt + 1 >= (1ull << 31)) {
+    const size_t ll_words = (size_t)2 * (P.n_layers + 1) * (size_t)P.off.words;
+    DZ_HIP_CHECK(hipMemsetAsync(P.ll, 0, ll_words * sizeof(u64), x->s));
+    x->ptk.gti = 0;
+  }
+  PtkRun r;
+  r.plan = x->ptk.plan;
+  r.plan.logits_all = per_pos ? x->ptk.logits_all : nullptr;
+  r.feed = x->feed + feed_off;
+  r.n_feed = n_feed;
+  r.n_tok = n;
+  r.pos0 = x->pos_host;
+  r.tag0 = (unsigned)(1 + x->ptk.gti * (uint64_t)P.ppt);
+  r.want_logits = 1;
+  r.err.flag = x->ptk.err;
+  r.err.spin_limit = 1 << 21;
+  // DAIZA_PTK_TRACE=<file>: append per-phase completion times of every workgroup to <file>
+  // (binary: int32 n_tok, ppt, G, then n_tok*ppt*G uint64 s_memrealtime ticks of 10 ns)
+  const char* trace_path = getenv("DAIZA_PTK_TRACE");
+  u64* trace = nullptr;
+  r.trace = nullptr;
+  const size_t trace_n = (size_t)n * P.ppt * P.G;
+  if (trace_path && trace_path[0]) {
+    DZ_HIP_CHECK(hipMalloc(&trace, trace_n * sizeof(u64)));
+    DZ_HIP_CHECK(hipMemset(trace, 0, trace_n * sizeof(u64)));
+    r.trace = trace;
+  }
+  void* args[] = {&r};
+  DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  int err[4];
+  DZ_HIP_CHECK(hipMemcpyAsync(err, x->ptk.err, 16, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  x->ptk.gti += (uint64_t)n;
+  if (trace) {
+    std::vector<u64> h(trace_n);
+    DZ_HIP_CHECK(hipMemcpy(h.data(), trace, trace_n * sizeof(u64), hipMemcpyDeviceToHost));
+    DZ_HIP_CHECK(hipFree(trace));
+    FILE* f = fopen(trace_path, "ab");
+    if (f) {
+      const int32_t hdr[3] = {n, P.ppt, P.G};
+      fwrite(hdr, sizeof hdr, 1, f);
+      fwrite(h.data(), sizeof(u64), h.size(), f);
+      fclose(f);
+    }
+  }
+  if (err[0]) {
+    DZ_HIP_CHECK(hipMemset(x->ptk.err, 0, 16));
+    return set_error(DZ_ERR_DEVICE, "token kernel: wait timed out (code %d, phase tag %u, workgroup %d)", err[0],
+                     (unsigned)err[1], err[2]);
+  }
+  x->pos_host += n;
+  // keep TokState consistent for the graph-path kernels (mixer steps)
+  int pp[2] = {x->pos_host - 1, x->pos_host};
+  DZ_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos), &pp[0], 4, hipMemcpyHostToDevice));
+  DZ_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos_next), &pp[1], 4, hipMemcpyHostToDevice));
+  return DZ_OK;
+}
+
+// Copies ids into the device feed array (synchronously: `ids` may be reused after the call).
+static int ptk_feed(dz_ctx* x, const uint32_t* ids, int n) {
+  if (n > x->feed_cap) return set_error(DZ_ERR_TENSOR, "feed of %d ids exceeds capacity %d", n, x->feed_cap);
+  for (int i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)x->m->cfg.vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", ids[i], x->m->cfg.vocab);
+  DZ_HIP_CHECK(hipMemcpyAsync(x->feed, ids, (size_t)n * 4, hipMemcpyHostToDevice, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
 }  // namespace dz
 
 extern "C" {
@@ -802,6 +1100,7 @@ int dz_ctx_create(dz_model* m, dz_ctx** out) {
   if ((rc = upload_f32(A, &x->rope, rope.data(), rope.size()))) return fail(rc);
   // argmax partials of "no logits yet": value -inf everywhere, selects token 0 if ever read
   if ((rc = ctx_zero_state(x))) return fail(rc);
+  if (ptk_wanted() && (rc = ptk_prepare(x))) return fail(rc);
   *out = x;
   return DZ_OK;
 }
@@ -820,8 +1119,21 @@ int dz_ctx_pos(const dz_ctx* x) { return x ? x->pos_host : -1; }
 
 void* dz_ctx_stream(dz_ctx* x) { return x ? (void*)x->s : nullptr; }
 
+int dz_ctx_token_kernel(const dz_ctx* x) { return x && x->ptk.on ? 1 : 0; }
+
 int dz_forward_token(dz_ctx* x, uint32_t token, float* logits, uint32_t* argmax) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (x->ptk.on) {
+    int rc = ptk_feed(x, &token, 1);
+    if (rc || (rc = ptk_run(x, 1, 1, false))) return rc;
+    if (argmax) {
+      int t;
+      DZ_HIP_CHECK(hipMemcpy(&t, x->toklog + x->pos_host, 4, hipMemcpyDeviceToHost));
+      *argmax = (uint32_t)t;
+    }
+    if (logits) DZ_HIP_CHECK(hipMemcpy(logits, x->logits, (size_t)x->m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    return DZ_OK;
+  }
   int rc = ctx_feed(x, &token, 1);
   if (rc) return rc;
   if ((rc = ctx_run(x, 1))) return rc;
@@ -843,9 +1155,24 @@ int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float
   if (start_pos != x->pos_host)
     return set_error(DZ_ERR_TENSOR, "forward_batch: start_pos %d != context position %d", start_pos, x->pos_host);
   if (x->pos_host + n > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "forward_batch: context full");
+  const size_t V = (size_t)x->m->cfg.vocab;
+  if (x->ptk.on) {
+    int rc = ptk_feed(x, ids, n);
+    if (rc) return rc;
+    if (per_pos) {
+      for (int i0 = 0; i0 < n; i0 += x->ptk.chunk) {
+        const int k = std::min(x->ptk.chunk, n - i0);
+        if ((rc = ptk_run(x, k, k, true, i0))) return rc;
+        DZ_HIP_CHECK(hipMemcpy(per_pos + (size_t)i0 * V, x->ptk.logits_all, (size_t)k * V * 4, hipMemcpyDeviceToHost));
+      }
+    } else if ((rc = ptk_run(x, n, n, false))) {
+      return rc;
+    }
+    if (last_logits) DZ_HIP_CHECK(hipMemcpy(last_logits, x->logits, V * 4, hipMemcpyDeviceToHost));
+    return DZ_OK;
+  }
   int rc = ctx_feed(x, ids, n);
   if (rc) return rc;
-  const size_t V = (size_t)x->m->cfg.vocab;
   for (int i = 0; i < n; ++i) {
     if ((rc = ctx_run(x, 1))) return rc;
     if (per_pos) DZ_HIP_CHECK(hipMemcpyAsync(per_pos + (size_t)i * V, x->logits, V * 4, hipMemcpyDeviceToHost, x->s));
@@ -859,6 +1186,12 @@ int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_token
   if (!x || !out_tokens) return set_error(DZ_ERR_MODEL, "null argument");
   if (n < 1) return DZ_OK;
   const int p0 = x->pos_host;
+  if (x->ptk.on) {
+    int rc = ptk_feed(x, &first_token, 1);
+    if (rc || (rc = ptk_run(x, n, 1, false))) return rc;
+    DZ_HIP_CHECK(hipMemcpy(out_tokens, x->toklog + p0 + 1, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return DZ_OK;
+  }
   int rc = ctx_feed(x, &first_token, 1);
   if (rc) return rc;
   if ((rc = ctx_run(x, n))) return rc;

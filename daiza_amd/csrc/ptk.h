@@ -1,0 +1,301 @@
+// ptk.h — the persistent token kernel: one cooperative launch runs whole tokens of the decode loop
+// (forward_single_token, Daiza-engine/src/model/forward.rs:204-375, and the greedy selection of
+// engine.rs:850-871) with every phase of every layer inside it.
+//
+// One workgroup per CU (512 threads, >80 KiB of LDS so that no CU takes two).  A token is a fixed
+// sequence of phases; every workgroup walks the same sequence and knows statically which work of
+// each phase is its own.  Phases hand their results over in "LL words": 64-bit {f32 value, 32-bit
+// tag} stored and loaded with agent-scope relaxed atomics (write-through to the device coherence
+// point, no fences).  A consumer polls the words it needs until each carries the producing phase's
+// tag, so readiness and data travel together and no counter or barrier is involved.  Weights of
+// the next matrix phase are loaded into registers before the workgroup starts waiting for that
+// phase's input, so the weight stream overlaps the hand-over latency.
+//
+// Per DeltaNet layer: A in-proj GEMV -> B DeltaNet -> C out-proj GEMV -> R1 (h_mid = h + sum of
+// out-proj partials) -> D gate/up GEMV -> R2 (SwiGLU of the gate/up partials) -> E down GEMV ->
+// R3 (h = h_mid + sum of down partials).  An attention layer replaces B, C by R0 (q/k/v/gate
+// partial sums) -> B' (split-K attention chunks) -> R'' (chunk merge and output gate) -> C'.
+// A token starts with S (greedy pick or fed id, embedding) and ends with L (lm_head, full K per
+// workgroup, per-workgroup argmax).
+#pragma once
+#include "model_kernels.h"
+
+namespace dz {
+
+typedef unsigned long long u64;
+
+// ------------------------------------------------------------------ address spaces
+
+// The plan and the layer table are read through the constant address space (scalar loads through
+// the scalar cache), and every data pointer taken from them is re-marked global.  A pointer loaded
+// from memory is otherwise generic, and generic (flat) accesses count on both the vector-memory and
+// the LDS counters: every LDS wait would also wait for outstanding HBM loads and LL stores, and
+// every field read would wait for the weight prefetch in flight.
+#define DZ_AS_GLOBAL __attribute__((address_space(1)))
+#define DZ_AS_CONST __attribute__((address_space(4)))
+
+template <class T>
+__device__ __forceinline__ T* glb(T* p) {
+  return (T*)(DZ_AS_GLOBAL T*)p;
+}
+
+// ------------------------------------------------------------------ LL words
+
+__device__ __forceinline__ u64 ll_ld(const u64* p) {
+  return __hip_atomic_load((const DZ_AS_GLOBAL u64*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_st(u64* p, float v, unsigned tag) {
+  __hip_atomic_store((DZ_AS_GLOBAL u64*)p, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
+__device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
+
+// Plain f32 in memory that other workgroups read in a later token (conv ring, KV cache):
+// written through and read past the non-coherent caches.
+__device__ __forceinline__ float co_ld(const float* p) {
+  return __hip_atomic_load((const DZ_AS_GLOBAL float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void co_st(float* p, float v) {
+  __hip_atomic_store((DZ_AS_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int flag_ld(const int* p) {
+  return __hip_atomic_load((const DZ_AS_GLOBAL int*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct PtkErr {
+  int* flag;  // first failure: code, phase tag, workgroup (0 = none)
+  int spin_limit;
+};
+
+__device__ __forceinline__ void ptk_fail(const PtkErr& e, int code, unsigned tag) {
+  DZ_AS_GLOBAL int* f = (DZ_AS_GLOBAL int*)e.flag;
+  int expected = 0;
+  if (__hip_atomic_compare_exchange_strong(f, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT)) {
+    __hip_atomic_store(f + 1, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(f + 2, (int)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Waits until the N words this thread needs carry `tag`, re-polling only the stale ones.
+// Bounded: past spin_limit rounds, or once another workgroup has failed, it records a failure and
+// returns false.  Every word must be a valid address.
+template <int N>
+__device__ __forceinline__ bool ll_wait(const u64* const (&p)[N], u64 (&w)[N], unsigned tag, const PtkErr& e) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = ll_ld(p[i]);
+  for (int spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ok &= ll_tag(w[i]) == tag;
+    if (ok) return true;
+    if (spin >= e.spin_limit) {
+      ptk_fail(e, 1, tag);
+      return false;
+    }
+    if ((spin & 31) == 31 && flag_ld(e.flag)) return false;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (ll_tag(w[i]) != tag) w[i] = ll_ld(p[i]);
+  }
+}
+
+__device__ __forceinline__ bool ll_wait1(const u64* p, float& v, unsigned tag, const PtkErr& e) {
+  const u64* a[1] = {p};
+  u64 w[1];
+  const bool ok = ll_wait<1>(a, w, tag, e);
+  v = ll_val(w[0]);
+  return ok;
+}
+
+// Sum of n (1 <= n <= MAXN) LL words p[k*ld] in order k = 0..n-1, all polled together.  Slots
+// k >= n are neither loaded nor waited for (their words count as ready).
+template <int MAXN>
+__device__ __forceinline__ bool ll_sum(const u64* p, int64_t ld, int n, unsigned tag, const PtkErr& e, float& out) {
+  u64 w[MAXN];
+  const u64 ready = (u64)tag << 32;
+#pragma unroll
+  for (int k = 0; k < MAXN; ++k) w[k] = k < n ? ll_ld(p + (size_t)k * ld) : ready;
+  for (int spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < MAXN; ++k) ok &= ll_tag(w[k]) == tag;
+    if (ok) break;
+    if (spin >= e.spin_limit) {
+      ptk_fail(e, 2, tag);
+      return false;
+    }
+    if ((spin & 31) == 31 && flag_ld(e.flag)) return false;
+#pragma unroll
+    for (int k = 0; k < MAXN; ++k)
+      if (ll_tag(w[k]) != tag) w[k] = ll_ld(p + (size_t)k * ld);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXN; ++k) s += k < n ? ll_val(w[k]) : 0.f;
+  out = s;
+  return true;
+}
+
+// ------------------------------------------------------------------ work assignment
+
+// Split-K GEMV over G workgroups: tile t owns workgroups [t*G/T, (t+1)*G/T); the n_t workgroups of a
+// tile split its nrb row-blocks evenly.  Requires T <= G.
+struct Assign {
+  int t, rb0, rb1;
+};
+__host__ __device__ inline int tile_first_wg(int t, int T, int G) { return (int)(((int64_t)t * G) / T); }
+__host__ __device__ inline Assign gemv_assign(int w, int G, int T, int nrb) {
+  Assign a;
+  a.t = (int)((((int64_t)w + 1) * T - 1) / G);
+  const int w0 = tile_first_wg(a.t, T, G), w1 = tile_first_wg(a.t + 1, T, G);
+  const int nw = w1 - w0, j = w - w0;
+  a.rb0 = (int)(((int64_t)j * nrb) / nw);
+  a.rb1 = (int)(((int64_t)(j + 1) * nrb) / nw);
+  return a;
+}
+// Even split of n items over G workgroups: [w*n/G, (w+1)*n/G).
+__host__ __device__ inline void even_split(int w, int G, int n, int* a, int* b) {
+  *a = (int)(((int64_t)w * n) / G);
+  *b = (int)(((int64_t)(w + 1) * n) / G);
+}
+
+constexpr int kPtkThreads = 512;
+constexpr int kPtkWaves = kPtkThreads / 64;
+constexpr int kPtkMaxU = 3;  // row-blocks per wave per GEMV phase (checked on the host)
+
+// ------------------------------------------------------------------ plan (device memory)
+
+struct PtkLayer {
+  int attn;
+  int rows_in;                 // in-proj rows; its partials have leading dimension nrb_in*64
+  int nrb_in;
+  int nt_out;                  // out-proj K tiles
+  const uint8_t* w_in;
+  const uint8_t* w_out;
+  const uint8_t* w_gu;
+  const uint8_t* w_dn;
+  const float* attn_norm;
+  const float* post_norm;
+  const float* conv_w;         // [4][qkvd]
+  const float* ssm_a;
+  const float* dt_bias;
+  const float* ssm_norm;
+  float* conv;                 // ring [4][qkvd]
+  float* state;                // [nvh][128 j][128 i]
+  const int* ring_base;
+  const float* q_norm;
+  const float* k_norm;
+  float* kc;                   // [nkv][max_ctx][hd]
+  float* vc;
+  int ph0;                     // index of this layer's first phase within a token
+};
+
+// Word offsets of the per-layer LL buffers inside one layer region.
+struct PtkOffsets {
+  int64_t pin, sst_in, po, hmid, sst_mid, pgu, sw, pd, h, y, zs, yss, qkv, rec, ao, words;
+};
+
+struct PtkPlan {
+  // dimensions
+  int G;
+  int n_layers;
+  int H, F, vocab;
+  int nT_h, nrb_h, nT_f, nrb_gu, nrb_v;
+  int nkh, nvh, qkvd, inner, off_z, off_a, off_b;
+  int nq, nkv, hd, rope_dim, grp;
+  int nrb_in_k[2];             // in-proj row-blocks of a DeltaNet [0] / attention [1] layer
+  int nt_out_k[2];             // out-proj K tiles of a DeltaNet [0] / attention [1] layer
+  int gmax;                    // attention chunks per kv-head at most (G / nkv)
+  int max_ctx;
+  float eps;
+  int embd_f16;
+  int ppt;                     // phases per token
+  int ph_l;                    // index of the lm_head phase
+  PtkOffsets off;
+  // weights
+  const uint8_t* w_lm;
+  const float* output_norm;
+  const uint16_t* emb_f16;
+  const uint8_t* emb_q1;
+  int emb_ntiles;
+  const float* rope;           // [max_ctx][rope_dim]
+  const PtkLayer* L;
+  // LL memory: [2 parities][n_layers + 1 regions][off.words]; region n_layers holds the token-level
+  // words: hemb (nrb_h*64), candv (G), candi (G)
+  u64* ll;
+  // state / outputs
+  TokState* st;
+  int* toklog;
+  float* logits;               // logits of the last token (vocab)
+  float* logits_all;           // per-token logits [n][vocab] when requested, else null
+};
+
+constexpr int kPtkMaxLayers = 128;
+
+struct PtkRun {
+  PtkPlan plan;                // by value: kernel arguments are read with scalar loads
+  const int* feed;             // fed ids for tokens [0, n_feed)
+  int n_feed;
+  int n_tok;
+  int pos0;                    // position of the first token
+  unsigned tag0;               // tag base of the first token (token i: tag0 + i*ppt)
+  int want_logits;             // 1: write logits (last token; all tokens when logits_all is set)
+  PtkErr err;
+  u64* trace;                  // optional [n_tok][ppt][G] completion times (s_memrealtime), else null
+};
+
+static_assert(sizeof(PtkRun) <= 4096, "kernel arguments are limited to 4 KiB");
+
+__device__ __forceinline__ u64* ll_region(const PtkPlan& P, int parity, int layer) {
+  return P.ll + ((size_t)parity * (P.n_layers + 1) + (size_t)layer) * (size_t)P.off.words;
+}
+
+// The kernel's view of the plan: its data pointers marked global.
+__device__ __forceinline__ PtkPlan plan_view(const PtkPlan& p) {
+  PtkPlan v = p;
+  v.w_lm = glb(v.w_lm);
+  v.output_norm = glb(v.output_norm);
+  v.emb_f16 = glb(v.emb_f16);
+  v.emb_q1 = glb(v.emb_q1);
+  v.rope = glb(v.rope);
+  v.ll = glb(v.ll);
+  v.st = glb(v.st);
+  v.toklog = glb(v.toklog);
+  v.logits = glb(v.logits);
+  v.logits_all = v.logits_all ? glb(v.logits_all) : nullptr;
+  return v;
+}
+
+// Layer l of the table, read through the constant address space (l is uniform), data pointers
+// marked global.
+__device__ __forceinline__ PtkLayer layer_at(const PtkPlan& P, int l) {
+  const DZ_AS_CONST PtkLayer* t = (const DZ_AS_CONST PtkLayer*)P.L + l;
+  PtkLayer y;
+  y.attn = t->attn;
+  y.rows_in = t->rows_in;
+  y.nrb_in = t->nrb_in;
+  y.nt_out = t->nt_out;
+  y.w_in = glb(t->w_in);
+  y.w_out = glb(t->w_out);
+  y.w_gu = glb(t->w_gu);
+  y.w_dn = glb(t->w_dn);
+  y.attn_norm = glb(t->attn_norm);
+  y.post_norm = glb(t->post_norm);
+  y.conv_w = glb(t->conv_w);
+  y.ssm_a = glb(t->ssm_a);
+  y.dt_bias = glb(t->dt_bias);
+  y.ssm_norm = glb(t->ssm_norm);
+  y.conv = glb(t->conv);
+  y.state = glb(t->state);
+  y.ring_base = glb(t->ring_base);
+  y.q_norm = glb(t->q_norm);
+  y.k_norm = glb(t->k_norm);
+  y.kc = glb(t->kc);
+  y.vc = glb(t->vc);
+  y.ph0 = t->ph0;
+  return y;
+}
+
+}  // namespace dz

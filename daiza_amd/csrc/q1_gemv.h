@@ -44,32 +44,81 @@ __device__ __forceinline__ void load_unit(const uint8_t* __restrict__ unit, unsi
 __device__ __forceinline__ float half_lo(unsigned v) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(v & 0xFFFFu)); }
 __device__ __forceinline__ float half_hi(unsigned v) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(v >> 16)); }
 
-typedef __attribute__((address_space(3))) const float lds_cfloat;
+// Dot product of one lane's 512-weight row slice with the tile whose table sits at LDS address 0
+// (kernels using it allocate no static LDS, so their dynamic LDS, the table, starts at address 0
+// and a v_perm result is the LDS address itself):
+//   a_k = +0;  for m = 0..15:  a_k = fma(scale[m >> 2], LUT[byte k of word m][position], a_k)
+//   result = (a0 + a1) + (a2 + a3)
+// where word m holds stored bytes 4m..4m+3, byte k's LDS address is v_perm(word, c[m]) (byte0 =
+// c[m].byte k, the position offset; byte1 = the sign byte; bytes 2,3 = 0) and scale slot m >> 2
+// is the f16 group scale of those positions, converted exactly to f32.
+// It is one software-pipelined block: the table reads of word m are issued three words ahead of
+// their FMAs (12 reads in flight, within the 4-bit LDS counter), so LDS latency is hidden by the
+// wave itself rather than by the compiler's scheduling, which serializes the reads (one in
+// flight) when the surrounding kernel is short of registers.  Per sign byte: one v_perm_b32, one
+// ds_read_b32, one v_fmac_f32.
+#define DZ_Q1_ISSUE(M, T)                                   \
+  "v_perm_b32 %[" #T "0], %[w" #M "], %[c" #M "], %[k0]\n" \
+  "v_perm_b32 %[" #T "1], %[w" #M "], %[c" #M "], %[k1]\n" \
+  "v_perm_b32 %[" #T "2], %[w" #M "], %[c" #M "], %[k2]\n" \
+  "v_perm_b32 %[" #T "3], %[w" #M "], %[c" #M "], %[k3]\n" \
+  "ds_read_b32 %[" #T "0], %[" #T "0]\n"                   \
+  "ds_read_b32 %[" #T "1], %[" #T "1]\n"                   \
+  "ds_read_b32 %[" #T "2], %[" #T "2]\n"                   \
+  "ds_read_b32 %[" #T "3], %[" #T "3]\n"
+#define DZ_Q1_ACC(T, F)                        \
+  "v_fmac_f32 %[a0], %[" #F "], %[" #T "0]\n" \
+  "v_fmac_f32 %[a1], %[" #F "], %[" #T "1]\n" \
+  "v_fmac_f32 %[a2], %[" #F "], %[" #T "2]\n" \
+  "v_fmac_f32 %[a3], %[" #F "], %[" #T "3]\n"
+#define DZ_Q1_STEP(MA, TA, F, MI, TI) "s_waitcnt lgkmcnt(8)\n" DZ_Q1_ACC(TA, F) DZ_Q1_ISSUE(MI, TI)
 
-// LDS load at an absolute LDS byte address.  The GEMV kernel allocates no static LDS, so its
-// dynamic LDS (the table) starts at address 0 and the v_perm result is the address itself.
-__device__ __forceinline__ float lds_at(unsigned byte_addr) { return *(lds_cfloat*)(uintptr_t)byte_addr; }
-
-// Dot product of one lane's 512-weight row slice with the tile whose table sits at LDS address 0.
 __device__ __forceinline__ float unit_dot(const UnitRegs& r, const unsigned c[16]) {
-  const float sc[4] = {half_lo(r.sc.x), half_hi(r.sc.x), half_lo(r.sc.y), half_hi(r.sc.y)};
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const unsigned w = r.s[m >> 2][m & 3];  // stored bytes 4m..4m+3
-    const float s = sc[m >> 2];             // slot (4m+k) >> 4
-    // byte0 <- c[m].byte k (position offset), byte1 <- w.byte k (sign byte), bytes 2,3 <- 0
-    const unsigned ad0 = __builtin_amdgcn_perm(w, c[m], 0x0C0C0400u);
-    const unsigned ad1 = __builtin_amdgcn_perm(w, c[m], 0x0C0C0501u);
-    const unsigned ad2 = __builtin_amdgcn_perm(w, c[m], 0x0C0C0602u);
-    const unsigned ad3 = __builtin_amdgcn_perm(w, c[m], 0x0C0C0703u);
-    a0 = __builtin_fmaf(s, lds_at(ad0), a0);
-    a1 = __builtin_fmaf(s, lds_at(ad1), a1);
-    a2 = __builtin_fmaf(s, lds_at(ad2), a2);
-    a3 = __builtin_fmaf(s, lds_at(ad3), a3);
-  }
+  const float f0 = half_lo(r.sc.x), f1 = half_hi(r.sc.x), f2 = half_lo(r.sc.y), f3 = half_hi(r.sc.y);
+  float a0, a1, a2, a3;
+  unsigned p0, p1, p2, p3, q0, q1, q2, q3, u0, u1, u2, u3, v0, v1, v2, v3;
+  asm volatile(
+      "v_mov_b32 %[a0], 0\n"
+      "v_mov_b32 %[a1], 0\n"
+      "v_mov_b32 %[a2], 0\n"
+      "v_mov_b32 %[a3], 0\n"
+      DZ_Q1_ISSUE(0, p) DZ_Q1_ISSUE(1, q) DZ_Q1_ISSUE(2, u)
+      DZ_Q1_STEP(0, p, f0, 3, v)
+      DZ_Q1_STEP(1, q, f0, 4, p)
+      DZ_Q1_STEP(2, u, f0, 5, q)
+      DZ_Q1_STEP(3, v, f0, 6, u)
+      DZ_Q1_STEP(4, p, f1, 7, v)
+      DZ_Q1_STEP(5, q, f1, 8, p)
+      DZ_Q1_STEP(6, u, f1, 9, q)
+      DZ_Q1_STEP(7, v, f1, 10, u)
+      DZ_Q1_STEP(8, p, f2, 11, v)
+      DZ_Q1_STEP(9, q, f2, 12, p)
+      DZ_Q1_STEP(10, u, f2, 13, q)
+      DZ_Q1_STEP(11, v, f2, 14, u)
+      DZ_Q1_STEP(12, p, f3, 15, v)
+      "s_waitcnt lgkmcnt(8)\n" DZ_Q1_ACC(q, f3)
+      "s_waitcnt lgkmcnt(4)\n" DZ_Q1_ACC(u, f3)
+      "s_waitcnt lgkmcnt(0)\n" DZ_Q1_ACC(v, f3)
+      : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3),
+        [p0] "=&v"(p0), [p1] "=&v"(p1), [p2] "=&v"(p2), [p3] "=&v"(p3),
+        [q0] "=&v"(q0), [q1] "=&v"(q1), [q2] "=&v"(q2), [q3] "=&v"(q3),
+        [u0] "=&v"(u0), [u1] "=&v"(u1), [u2] "=&v"(u2), [u3] "=&v"(u3),
+        [v0] "=&v"(v0), [v1] "=&v"(v1), [v2] "=&v"(v2), [v3] "=&v"(v3)
+      : [w0] "v"(r.s[0].x), [w1] "v"(r.s[0].y), [w2] "v"(r.s[0].z), [w3] "v"(r.s[0].w),
+        [w4] "v"(r.s[1].x), [w5] "v"(r.s[1].y), [w6] "v"(r.s[1].z), [w7] "v"(r.s[1].w),
+        [w8] "v"(r.s[2].x), [w9] "v"(r.s[2].y), [w10] "v"(r.s[2].z), [w11] "v"(r.s[2].w),
+        [w12] "v"(r.s[3].x), [w13] "v"(r.s[3].y), [w14] "v"(r.s[3].z), [w15] "v"(r.s[3].w),
+        [c0] "v"(c[0]), [c1] "v"(c[1]), [c2] "v"(c[2]), [c3] "v"(c[3]), [c4] "v"(c[4]), [c5] "v"(c[5]),
+        [c6] "v"(c[6]), [c7] "v"(c[7]), [c8] "v"(c[8]), [c9] "v"(c[9]), [c10] "v"(c[10]), [c11] "v"(c[11]),
+        [c12] "v"(c[12]), [c13] "v"(c[13]), [c14] "v"(c[14]), [c15] "v"(c[15]),
+        [f0] "v"(f0), [f1] "v"(f1), [f2] "v"(f2), [f3] "v"(f3),
+        [k0] "s"(0x0C0C0400u), [k1] "s"(0x0C0C0501u), [k2] "s"(0x0C0C0602u), [k3] "s"(0x0C0C0703u)
+      : "memory");
   return (a0 + a1) + (a2 + a3);
 }
+#undef DZ_Q1_STEP
+#undef DZ_Q1_ACC
+#undef DZ_Q1_ISSUE
 
 // Builds LUT[v][p] from xs[0..511] (LDS).  NT threads; NT/64 threads share one position.
 template <int NT>

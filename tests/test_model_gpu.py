@@ -137,3 +137,56 @@ def test_attention_step(dz, oracle, ctxlen):
     assert ko.shape[1] == ctxlen + 1
     assert normwise_rel(kg[:, -2:], ko[:, -2:]) < 1e-3
     assert normwise_rel(vg[:, -2:], vo[:, -2:]) < 1e-3
+
+
+@pytest.fixture
+def graph_path(monkeypatch):
+    """Contexts created while this fixture is active replay the per-kernel token graph."""
+    monkeypatch.setenv("DAIZA_PTK", "0")
+
+
+def test_token_kernel_is_default_for_supported_shapes(dz):
+    for cfg in (dz.Config.small(n_layers=4, max_ctx=64), dz.Config.bonsai27b(max_ctx=64)):
+        if cfg.n_layers == 64:
+            cfg.n_layers = 4  # a 4-layer stack of the 27B shapes: same kernel instance, less memory
+        m = dz.Model.synthetic(cfg, SEED)
+        ctx = dz.Context(m)
+        assert ctx.token_kernel, cfg.hidden
+        ctx.close()
+        m.close()
+
+
+def test_graph_path_matches_oracle(dz, oracle, graph_path):
+    cfg = dz.Config.small(n_layers=4, max_ctx=64)
+    m, ctx, om = _pair(dz, oracle, cfg, seed=SEED + 7)
+    assert not ctx.token_kernel
+    for t in [5, 17, 2047, 0, 999, 1234]:
+        am, lg = ctx.forward_single_token(t)
+        oam, olg = om.forward(t)
+        assert normwise_rel(lg, olg) < 1e-3
+        assert am == oam
+    got = ctx.decode_greedy(am, 24)
+    want, tok = [], am
+    for _ in range(24):
+        tok, _ = om.forward(tok, want_logits=False)
+        want.append(tok)
+    assert list(got) == want
+
+
+def test_token_kernel_and_graph_agree(dz, monkeypatch):
+    """The two launch paths compute the same per-position logits (small stack, 20 tokens)."""
+    cfg = dz.Config.small(n_layers=8, max_ctx=64)
+    ids = np.random.default_rng(3).integers(0, cfg.vocab, 20).astype(np.uint32)
+    out = {}
+    for path in ("1", "0"):
+        monkeypatch.setenv("DAIZA_PTK", path)
+        m = dz.Model.synthetic(cfg, SEED + 9)
+        ctx = dz.Context(m)
+        assert ctx.token_kernel == (path == "1")
+        out[path] = ctx.forward_batch(ids, per_pos_logits=True)
+        out[path + "g"] = ctx.decode_greedy(int(np.argmax(out[path][-1])), 16)
+        ctx.close()
+        m.close()
+    for i in range(len(ids)):
+        assert normwise_rel(out["1"][i], out["0"][i]) < 1e-5, i
+    assert list(out["1g"]) == list(out["0g"])

@@ -771,18 +771,22 @@ static int ctx_set_pos_dev(dz_ctx* x, int pos) {
 
 // ---------------------------------------------------------------- persistent token kernel (host)
 
-// Kernel instantiation for a model shape: partial-count buckets (K tiles of hidden, of the mixer
-// output width, of ffn) and the GQA group.  Other shapes run on the graph path.
+// Kernel instantiation for a model shape (the template bounds of ptk_kernel): K tiles of hidden (exact), GQA
+// group, row-block slots per compute wave of each GEMV kind, terms per lane of the residual sums,
+// ffn channels per lane of the SwiGLU sums, rows per lane of the in-projection sums and outputs per
+// workgroup of the attention merge.  Other shapes run on the graph path.
 struct PtkShape {
-  int th, to, tf, grp, u_in, u_out, u_gu, u_dn, u_lm;
+  int th, grp, u_in, u_out, u_gu, u_dn, u_lm, qr, mf, mr, mo;
 };
+static bool ptk_fits(const PtkShape& s, const PtkShape& b) {
+  return s.th == b.th && s.grp == b.grp && s.u_in <= b.u_in && s.u_out <= b.u_out && s.u_gu <= b.u_gu &&
+         s.u_dn <= b.u_dn && s.u_lm <= b.u_lm && s.qr <= b.qr && s.mf <= b.mf && s.mr <= b.mr && s.mo <= b.mo;
+}
 static const void* ptk_pick(const PtkShape& s) {
-  if (s.th <= 12 && s.to <= 12 && s.tf <= 36 && s.grp == 6 && s.u_in <= 2 && s.u_out <= 1 && s.u_gu <= 3 && s.u_dn <= 2 &&
-      s.u_lm <= 2)
-    return reinterpret_cast<const void*>(ptk_kernel<12, 12, 36, 6, 2, 1, 3, 2, 2>);
-  if (s.th <= 2 && s.to <= 2 && s.tf <= 2 && s.grp == 2 && s.u_in <= 1 && s.u_out <= 1 && s.u_gu <= 1 && s.u_dn <= 1 &&
-      s.u_lm <= 1)
-    return reinterpret_cast<const void*>(ptk_kernel<2, 2, 2, 2, 1, 1, 1, 1, 1>);
+  if (ptk_fits(s, PtkShape{10, 6, 2, 1, 4, 2, 3, 12, 2, 2, 24}))
+    return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 2, 2, 24>);
+  if (ptk_fits(s, PtkShape{1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8}))
+    return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8>);
   return nullptr;
 }
 
@@ -807,9 +811,10 @@ static int ptk_prepare(dz_ctx* x) {
   int th, to, tf;
   ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
   const int grp = c.n_head / c.n_head_kv;
-  if (!coop || c.head_dim != 256 || c.ssm_state != 128 || G < 8 || G > kPtkThreads || c.n_layers > kPtkMaxLayers)
+  if (!coop || c.head_dim != 256 || c.rope_dim != 64 || c.ssm_state != 128 || G < 8 || G > kPtkThreads ||
+      c.n_layers > kPtkMaxLayers || th > kMaxTilesH || c.hidden < G)
     return DZ_OK;
-  // shape limits of the static work split: row-block slots per wave of each matrix kind
+  // shape limits of the static work split: row-block slots per compute wave of each matrix kind
   const int nrb_h = (int)(ld_h / kRowBlock), nrb_gu = (int)(ld_gu / kRowBlock), nrb_v = (int)m->lm_head.nrb;
   auto slots = [&](int T, int nrb) {
     if (T > G) return 1 << 20;
@@ -818,13 +823,26 @@ static int ptk_prepare(dz_ctx* x) {
       const int nw = tile_first_wg(t + 1, T, G) - tile_first_wg(t, T, G);
       mx = std::max(mx, (nrb + nw - 1) / nw);
     }
-    return (mx + kPtkWaves - 1) / kPtkWaves;
+    return (mx + kCW - 1) / kCW;
   };
-  PtkShape sh{th, to, tf, grp, 0, 0, slots(th, nrb_gu), slots(tf, nrb_h), ((nrb_v + G - 1) / G + kPtkWaves - 1) / kPtkWaves};
+  auto per_wg = [&](int n) { return (n + G - 1) / G; };  // items per workgroup of an even split
+  const int nc = per_wg(c.hidden);                       // residual columns per workgroup
+  auto resid_q = [&](int np) {                           // terms per lane of a residual sum
+    const int K = np + 1, nq = std::min(64 / nc, K);
+    return (K + nq - 1) / nq;
+  };
+  PtkShape sh{th, grp, 0, 0, slots(th, nrb_gu), slots(tf, nrb_h), (per_wg(nrb_v) + kCW - 1) / kCW, 0,
+              (per_wg(c.ffn) + 63) / 64, 0, per_wg(c.n_head * c.head_dim)};
+  int max_rows_in = 0;
   for (auto& l : m->L) {
     sh.u_in = std::max(sh.u_in, slots(th, (int)l.in_proj.nrb));
     sh.u_out = std::max(sh.u_out, slots((int)l.out_proj.ntiles, nrb_h));
+    sh.qr = std::max(sh.qr, resid_q((int)l.out_proj.ntiles));
+    max_rows_in = std::max(max_rows_in, (int)l.in_proj.rows);
   }
+  sh.qr = std::max(sh.qr, resid_q(tf));
+  sh.mr = (per_wg(max_rows_in) + 63) / 64;
+  if (nc > 64 || sh.mo > 64 || sh.mo > c.head_dim) return DZ_OK;
   const void* kfn = ptk_pick(sh);
   if (!kfn) return DZ_OK;
   int occ = 0;
@@ -832,23 +850,7 @@ static int ptk_prepare(dz_ctx* x) {
   DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kPtkThreads, kPtkLds));
   if (occ < 1) return DZ_OK;
   const int gmax = std::min(64, G / std::max(1, c.n_head_kv));
-  bool ok = 4 * c.ssm_v_heads <= G && c.n_head_kv * gmax <= G && gmax >= 1 && c.rope_dim / 2 <= 256;
-  // column sums (ll_colsum): nc columns of K terms per workgroup
-  auto colq = [&](int n_items, int cols_per_item, int K) {
-    const int nc = (n_items + G - 1) / G * cols_per_item;
-    if (nc > kPtkThreads) return false;
-    const int nq = std::max(1, std::min(kPtkThreads / std::max(1, nc), K));
-    return (K + nq - 1) / nq <= kPtkColQ;
-  };
-  auto colq1 = [&](int n_items, int cols_per_item, int K) {  // one extra column of K terms
-    const int nc = (n_items + G - 1) / G * cols_per_item + 1;
-    if (nc > kPtkThreads) return false;
-    const int nq = std::max(1, std::min(kPtkThreads / nc, K));
-    return (K + nq - 1) / nq <= kPtkColQ;
-  };
-  ok = ok && colq(c.hidden, 1, to + 1) && colq(c.hidden, 1, tf + 1) && colq1(c.ffn, 2, th) &&
-       colq1(2 * c.n_head * c.head_dim + 2 * c.n_head_kv * c.head_dim, 1, th) && th <= 64;
-  if (!ok) return DZ_OK;
+  if (4 * c.ssm_v_heads > G || c.n_head_kv * gmax > G || gmax < 1) return DZ_OK;
   PtkPlan& P = x->ptk.plan;
   memset(&P, 0, sizeof P);
   P.G = G;
@@ -895,12 +897,12 @@ static int ptk_prepare(dz_ctx* x) {
   P.off.h = take(ld_h);
   P.off.y = take(P.inner);
   P.off.zs = take(P.inner);
-  P.off.yss = take(4 * (int64_t)P.nvh);
-  P.off.qkv = take(attn_rows);
+  P.off.yss = take(16 * (int64_t)P.nvh);
+  P.off.qkv = take(std::max<int64_t>(attn_rows, max_rows_in));
   P.off.rec = take((int64_t)c.n_head * gmax * (2 + c.head_dim));
   P.off.ao = take(qdim);
   P.off.words = std::max<int64_t>(o, al(ld_h + 2 * (int64_t)G));
-  // phases: S, then 8 per DeltaNet layer / 10 per attention layer, then L
+  // phases: S, then 9 per DeltaNet layer / 10 per attention layer, then L
   std::vector<PtkLayer> Ls((size_t)c.n_layers);
   const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
   const int64_t hd2 = hd;
@@ -935,7 +937,7 @@ static int ptk_prepare(dz_ctx* x) {
       y.vc = y.kc + kvsz;
     }
     y.ph0 = ph;
-    ph += l.attn ? 10 : 8;
+    ph += l.attn ? 10 : 9;
   }
   // the kernel assigns GEMV work per matrix kind: every layer of a kind has the same shapes
   P.nrb_in_k[0] = P.nrb_in_k[1] = P.nt_out_k[0] = P.nt_out_k[1] = -1;
@@ -1002,12 +1004,12 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0)
   r.want_logits = 1;
   r.err.flag = x->ptk.err;
   r.err.spin_limit = 1 << 21;
-  // DAIZA_PTK_TRACE=<file>: append per-phase completion times of every workgroup to <file>
-  // (binary: int32 n_tok, ppt, G, then n_tok*ppt*G uint64 s_memrealtime ticks of 10 ns)
+  // DAIZA_PTK_TRACE=<file>: append per-phase times of every workgroup to <file> (binary: int32
+  // n_tok, ppt, G, slots, then n_tok*ppt*G*slots uint64 s_memrealtime ticks of 10 ns)
   const char* trace_path = getenv("DAIZA_PTK_TRACE");
   u64* trace = nullptr;
   r.trace = nullptr;
-  const size_t trace_n = (size_t)n * P.ppt * P.G;
+  const size_t trace_n = (size_t)n * P.ppt * P.G * kPtkTraceSlots;
   if (trace_path && trace_path[0]) {
     DZ_HIP_CHECK(hipMalloc(&trace, trace_n * sizeof(u64)));
     DZ_HIP_CHECK(hipMemset(trace, 0, trace_n * sizeof(u64)));
@@ -1025,7 +1027,7 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0)
     DZ_HIP_CHECK(hipFree(trace));
     FILE* f = fopen(trace_path, "ab");
     if (f) {
-      const int32_t hdr[3] = {n, P.ppt, P.G};
+      const int32_t hdr[4] = {n, P.ppt, P.G, kPtkTraceSlots};
       fwrite(hdr, sizeof hdr, 1, f);
       fwrite(h.data(), sizeof(u64), h.size(), f);
       fclose(f);

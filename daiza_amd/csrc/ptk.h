@@ -7,16 +7,16 @@
 // each phase is its own.  Phases hand their results over in "LL words": 64-bit {f32 value, 32-bit
 // tag} stored and loaded with agent-scope relaxed atomics (write-through to the device coherence
 // point, no fences).  A consumer polls the words it needs until each carries the producing phase's
-// tag, so readiness and data travel together and no counter or barrier is involved.  Weights of
-// the next matrix phase are loaded into registers before the workgroup starts waiting for that
-// phase's input, so the weight stream overlaps the hand-over latency.
+// tag, so readiness and data travel together and no counter or barrier is involved.  Wave 0 of a
+// workgroup does all polling; waves 1..7 hold the GEMV weights, requested as soon as the previous
+// GEMV's weights are consumed, so the weight stream overlaps the hand-overs (ptk_kernel.h).
 //
-// Per DeltaNet layer: A in-proj GEMV -> B DeltaNet -> C out-proj GEMV -> R1 (h_mid = h + sum of
-// out-proj partials) -> D gate/up GEMV -> R2 (SwiGLU of the gate/up partials) -> E down GEMV ->
-// R3 (h = h_mid + sum of down partials).  An attention layer replaces B, C by R0 (q/k/v/gate
-// partial sums) -> B' (split-K attention chunks) -> R'' (chunk merge and output gate) -> C'.
-// A token starts with S (greedy pick or fed id, embedding) and ends with L (lm_head, full K per
-// workgroup, per-workgroup argmax).
+// Per DeltaNet layer: A in-proj GEMV -> R0 (in-proj partial sums) -> B DeltaNet -> C out-proj GEMV
+// -> R1 (h_mid = h + sum of out-proj partials) -> D gate/up GEMV -> R2 (SwiGLU of the gate/up
+// partials) -> E down GEMV -> R3 (h = h_mid + sum of down partials).  An attention layer replaces
+// B, C by B' (split-K attention chunks) -> R'' (chunk merge and output gate) -> C'.  A token starts
+// with S (greedy pick or fed id, embedding) and ends with L (lm_head, full K per workgroup,
+// per-workgroup argmax).
 #pragma once
 #include "model_kernels.h"
 
@@ -78,66 +78,6 @@ __device__ __forceinline__ void ptk_fail(const PtkErr& e, int code, unsigned tag
   }
 }
 
-// Waits until the N words this thread needs carry `tag`, re-polling only the stale ones.
-// Bounded: past spin_limit rounds, or once another workgroup has failed, it records a failure and
-// returns false.  Every word must be a valid address.
-template <int N>
-__device__ __forceinline__ bool ll_wait(const u64* const (&p)[N], u64 (&w)[N], unsigned tag, const PtkErr& e) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) w[i] = ll_ld(p[i]);
-  for (int spin = 0;; ++spin) {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < N; ++i) ok &= ll_tag(w[i]) == tag;
-    if (ok) return true;
-    if (spin >= e.spin_limit) {
-      ptk_fail(e, 1, tag);
-      return false;
-    }
-    if ((spin & 31) == 31 && flag_ld(e.flag)) return false;
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (ll_tag(w[i]) != tag) w[i] = ll_ld(p[i]);
-  }
-}
-
-__device__ __forceinline__ bool ll_wait1(const u64* p, float& v, unsigned tag, const PtkErr& e) {
-  const u64* a[1] = {p};
-  u64 w[1];
-  const bool ok = ll_wait<1>(a, w, tag, e);
-  v = ll_val(w[0]);
-  return ok;
-}
-
-// Sum of n (1 <= n <= MAXN) LL words p[k*ld] in order k = 0..n-1, all polled together.  Slots
-// k >= n are neither loaded nor waited for (their words count as ready).
-template <int MAXN>
-__device__ __forceinline__ bool ll_sum(const u64* p, int64_t ld, int n, unsigned tag, const PtkErr& e, float& out) {
-  u64 w[MAXN];
-  const u64 ready = (u64)tag << 32;
-#pragma unroll
-  for (int k = 0; k < MAXN; ++k) w[k] = k < n ? ll_ld(p + (size_t)k * ld) : ready;
-  for (int spin = 0;; ++spin) {
-    bool ok = true;
-#pragma unroll
-    for (int k = 0; k < MAXN; ++k) ok &= ll_tag(w[k]) == tag;
-    if (ok) break;
-    if (spin >= e.spin_limit) {
-      ptk_fail(e, 2, tag);
-      return false;
-    }
-    if ((spin & 31) == 31 && flag_ld(e.flag)) return false;
-#pragma unroll
-    for (int k = 0; k < MAXN; ++k)
-      if (ll_tag(w[k]) != tag) w[k] = ll_ld(p + (size_t)k * ld);
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < MAXN; ++k) s += k < n ? ll_val(w[k]) : 0.f;
-  out = s;
-  return true;
-}
-
 // ------------------------------------------------------------------ work assignment
 
 // Split-K GEMV over G workgroups: tile t owns workgroups [t*G/T, (t+1)*G/T); the n_t workgroups of a
@@ -163,7 +103,6 @@ __host__ __device__ inline void even_split(int w, int G, int n, int* a, int* b) 
 
 constexpr int kPtkThreads = 512;
 constexpr int kPtkWaves = kPtkThreads / 64;
-constexpr int kPtkMaxU = 3;  // row-blocks per wave per GEMV phase (checked on the host)
 
 // ------------------------------------------------------------------ plan (device memory)
 
@@ -233,6 +172,9 @@ struct PtkPlan {
 };
 
 constexpr int kPtkMaxLayers = 128;
+// Trace stamps per (token, phase, workgroup): 0 = phase done; in a GEMV phase 1 = first compute
+// wave at the staging barrier, 2 = table built (lookups start), 3 = sync wave done staging.
+constexpr int kPtkTraceSlots = 4;
 
 struct PtkRun {
   PtkPlan plan;                // by value: kernel arguments are read with scalar loads
@@ -243,7 +185,7 @@ struct PtkRun {
   unsigned tag0;               // tag base of the first token (token i: tag0 + i*ppt)
   int want_logits;             // 1: write logits (last token; all tokens when logits_all is set)
   PtkErr err;
-  u64* trace;                  // optional [n_tok][ppt][G] completion times (s_memrealtime), else null
+  u64* trace;                  // optional [n_tok][ppt][G][kPtkTraceSlots] times (s_memrealtime), else null
 };
 
 static_assert(sizeof(PtkRun) <= 4096, "kernel arguments are limited to 4 KiB");
@@ -253,8 +195,7 @@ __device__ __forceinline__ u64* ll_region(const PtkPlan& P, int parity, int laye
 }
 
 // The kernel's view of the plan: its data pointers marked global.
-__device__ __forceinline__ PtkPlan plan_view(const PtkPlan& p) {
-  PtkPlan v = p;
+__device__ __forceinline__ PtkPlan plan_globals(PtkPlan v) {
   v.w_lm = glb(v.w_lm);
   v.output_norm = glb(v.output_norm);
   v.emb_f16 = glb(v.emb_f16);
@@ -267,6 +208,9 @@ __device__ __forceinline__ PtkPlan plan_view(const PtkPlan& p) {
   v.logits_all = v.logits_all ? glb(v.logits_all) : nullptr;
   return v;
 }
+
+__device__ __forceinline__ PtkPlan plan_view(const PtkPlan& p) { return plan_globals(p); }
+
 
 // Layer l of the table, read through the constant address space (l is uniform), data pointers
 // marked global.

@@ -1,17 +1,30 @@
 // ptk_kernel.h — device code of the persistent token kernel (declarations in ptk.h).
+//
+// Wave roles.  Wave 0 of every workgroup is the sync wave: it does every LL poll of the kernel, the
+// small per-column phases (residual sums, SwiGLU, q/k/v sums, attention chunk merge, token
+// selection), the per-head prologues of the DeltaNet and attention phases, and it stages every GEMV
+// input into LDS.  Waves 1..7 are compute waves: they hold GEMV weights in registers, build the
+// lookup table together with the sync wave, run the table lookups and publish the split-K partials;
+// they never poll.  A wave's vector memory operations complete in issue order (gfx9 counts loads
+// and stores on one vmcnt), so a poll issued behind a weight load waits for that load.  With the
+// roles split, a compute wave requests the next GEMV's weights as soon as the current ones are
+// consumed, and the weight stream overlaps every hand-over, while the sync wave's polls cost one
+// round trip.
 #pragma once
 #include "ptk.h"
 
 namespace dz {
 
-// LDS map of the kernel (dynamic LDS only, so that the LUT sits at LDS address 0 as unit_dot needs).
-constexpr int kLdsXs = kLutBytes;                          // 512 floats: staged LUT input
-constexpr int kLdsRed = kLdsXs + kTileCols * 4;            // 64 floats: reductions
-constexpr int kLdsFlag = kLdsRed + 64 * 4;                 // 4 ints: abort flag
-constexpr int kLdsAsg = kLdsFlag + 16;                     // 8 x {t, rb0, rb1, lead}: GEMV assignments
-constexpr int kLdsRing = kLdsAsg + 8 * 16;                 // kPtkMaxLayers ints: conv ring bases
-constexpr int kLdsScratch = kLdsRing + kPtkMaxLayers * 4;  // phase scratch
-constexpr int kLdsScratchBytes = 28 * 1024;
+constexpr int kCW = kPtkWaves - 1;  // compute waves per workgroup
+
+// LDS map (dynamic LDS only, so that the lookup table sits at LDS address 0 as unit_dot needs).
+constexpr int kLdsXs = kLutBytes;                                // staged LUT inputs: up to 16 tiles (lm_head)
+constexpr int kLdsRed = kLdsXs + kMaxTilesH * kTileCols * 4;     // 64 floats: reductions
+constexpr int kLdsFlag = kLdsRed + 64 * 4;                       // abort flag, trace, hand-off, arrival counts
+constexpr int kLdsAsg = kLdsFlag + 16;                           // 8 x {t, rb0, rb1, lead}: GEMV assignments
+constexpr int kLdsRing = kLdsAsg + 8 * 16;                       // kPtkMaxLayers ints: conv ring bases
+constexpr int kLdsScratch = kLdsRing + kPtkMaxLayers * 4;        // phase scratch
+constexpr int kLdsScratchBytes = 16 * 1024;
 // > 80 KiB so that a CU never holds two workgroups of this kernel
 constexpr size_t kPtkLds = (size_t)kLdsScratch + kLdsScratchBytes;
 
@@ -28,155 +41,159 @@ __device__ __forceinline__ bool wg_ok(unsigned char* smem, bool ok) {
 
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Deterministic block sum over 512 threads; every thread gets the result.
-__device__ __forceinline__ float block_sum512(float v, float* red, unsigned tid) {
-  v = wave_sum(v);
-  if ((tid & 63u) == 0) red[tid >> 6] = v;
-  lds_barrier();
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < kPtkWaves; ++w) s += red[w];
-  lds_barrier();
-  return s;
+// Sum over each row of 16 lanes (DPP); every lane gets its row's sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_add<0xB1>(v);
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x141>(v);
+  v = dpp_add<0x140>(v);
+  return v;
 }
 
-// 1 / rms of a length-n vector from its per-tile sums of squares sst[0..nt) (nt <= 64), read by
-// wave 0 only and shared through LDS.
-__device__ __forceinline__ bool inv_rms_tiles(unsigned char* smem, const u64* sst, unsigned tag, int nt, int n,
-                                              float eps, unsigned tid, const PtkErr& e, float& inv) {
-  float* red = lds_ptr<float>(smem, kLdsRed);
-  bool ok = true;
-  if (tid < 64) {
-    float v = 0.f;
-    if ((int)tid < nt) ok = ll_wait1(sst + tid, v, tag, e);
-    const float s = wave_sum(v);
-    if (tid == 0) red[32] = 1.0f / sqrtf(s / (float)n + eps);
-  }
-  if (!wg_ok(smem, ok)) return false;
-  inv = red[32];
-  return true;
+// Coherent 16-byte row read of memory written earlier in the launch by another workgroup.
+__device__ __forceinline__ float4 co_ld4(const float* p) {
+  const u64* q = reinterpret_cast<const u64*>(p);
+  const u64 a = __hip_atomic_load((const DZ_AS_GLOBAL u64*)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const u64 b = __hip_atomic_load((const DZ_AS_GLOBAL u64*)(q + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((unsigned)a), __uint_as_float((unsigned)(a >> 32)), __uint_as_float((unsigned)b),
+                     __uint_as_float((unsigned)(b >> 32)));
 }
 
-constexpr int kPtkColQ = 4;  // terms per thread in ll_colsum (checked on the host)
+// A uniform value the compiler cannot see through: anything derived from it is recomputed where it
+// is used instead of being hoisted out of the enclosing loop.
+__device__ __forceinline__ int opaque_s(int v) {
+  v = __builtin_amdgcn_readfirstlane(v);
+  asm volatile("" : "+s"(v));
+  return v;
+}
 
-// Column sums of LL words spread over the workgroup: for each of nc columns j, the terms
-// k = 0..K-1 at ptr(j, k), each carrying tag tagf(k), are summed.  Thread (j, q) sums terms
-// [q*Q, (q+1)*Q) in order (Q <= QMAX, checked on the host) into LDS, then thread j adds the slices
-// in order: deterministic, and at most QMAX words in flight per thread.  Thread j < nc receives its
-// column's sum in `out`.
-template <int QMAX, class Ptr, class Tag>
-__device__ __forceinline__ bool ll_colsum(unsigned char* smem, int nc, int K, const Ptr& ptr, const Tag& tagf,
-                                          unsigned tid, const PtkErr& e, float& out) {
-  float* slice = lds_ptr<float>(smem, kLdsScratch + 16 * 1024);  // up to 512 floats
-  bool ok = true;
-  int nq = 1, Q = K;
-  if (nc > 0) {
-    nq = min(kPtkThreads / nc, K);
-    if (nq < 1) nq = 1;
-    Q = (K + nq - 1) / nq;
-    if ((int)tid < nq * nc) {
-      const int j = (int)tid % nc, q = (int)tid / nc;
-      const int k0 = q * Q, k1 = min(K, k0 + Q);
-      u64 w[QMAX];
-      unsigned tg[QMAX];
+// ------------------------------------------------------------------ polling (sync wave)
+
+// Waits until every valid slot i < N of this lane (word addr(i, lane), expected tag tagf(i)) carries
+// its tag, re-polling only the stale slots; invalid slots count as ready and are never loaded.
+// Bounded: past spin_limit rounds, or once another workgroup has failed, it records a failure and
+// returns false.  Each round passes addr an opaque copy of the lane index, so that slot addresses
+// are recomputed per round instead of being kept live (two registers per slot) across the loop.
+template <int N, class A, class V, class T>
+__device__ __forceinline__ bool poll(const A& addr, const V& valid, const T& tagf, u64 (&w)[N], const PtkErr& e) {
+  const unsigned lane0 = threadIdx.x & 63u;
 #pragma unroll
-      for (int i = 0; i < QMAX; ++i) {
-        tg[i] = tagf(k0 + i);
-        w[i] = k0 + i < k1 ? ll_ld(ptr(j, k0 + i)) : ((u64)tg[i] << 32);
-      }
-      for (int spin = 0;; ++spin) {
-        bool all = true;
+  for (int i = 0; i < N; ++i) w[i] = valid(i) ? ll_ld(addr(i, lane0)) : ((u64)tagf(i) << 32);
+  for (int spin = 0;; ++spin) {
+    bool all = true;
 #pragma unroll
-        for (int i = 0; i < QMAX; ++i) all &= ll_tag(w[i]) == tg[i];
-        if (all) break;
-        if (spin >= e.spin_limit) {
-          ptk_fail(e, 3, tg[0]);
-          ok = false;
-          break;
-        }
-        if ((spin & 31) == 31 && flag_ld(e.flag)) {
-          ok = false;
-          break;
-        }
-#pragma unroll
-        for (int i = 0; i < QMAX; ++i)
-          if (ll_tag(w[i]) != tg[i]) w[i] = ll_ld(ptr(j, k0 + i));
-      }
-      float sv = 0.f;
-#pragma unroll
-      for (int i = 0; i < QMAX; ++i) sv += k0 + i < k1 ? ll_val(w[i]) : 0.f;
-      slice[q * nc + j] = sv;
+    for (int i = 0; i < N; ++i) all &= ll_tag(w[i]) == tagf(i);
+    if (all) return true;
+    if (spin >= e.spin_limit) {
+      ptk_fail(e, 1, tagf(0));
+      return false;
     }
+    if ((spin & 31) == 31 && flag_ld(e.flag)) return false;
+    unsigned ln = threadIdx.x & 63u;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (ll_tag(w[i]) != tagf(i)) w[i] = ll_ld(addr(i, ln));
   }
-  if (!wg_ok(smem, ok)) return false;
-  if ((int)tid < nc) {
-    float sv = 0.f;
-    for (int q = 0; q < nq; ++q) sv += slice[q * nc + (int)tid];
-    out = sv;
-  }
-  lds_barrier();  // slices are reused by the next call
-  return true;
 }
 
-struct NoPrefetch {
-  __device__ __forceinline__ void operator()() const {}
+// Hand-offs from the sync wave to the compute waves inside a workgroup.  A CU's vector memory
+// pipeline returns data in issue order across all its waves, so a poll issued behind a phase's
+// weight prefetch waits for the whole prefetch to arrive.  The compute waves therefore request a
+// GEMV's weights only once the sync wave has finished the polls of the phase before it (a residual
+// or SwiGLU sum, which needs no weights), and the weights then overlap the GEMV's own input
+// hand-over.  Both roles count the hand-off points in the same order: the sync wave publishes its
+// count in LDS (sync_bump), a compute wave waits until the count reaches its own (sync_wait,
+// bounded; the sync wave bumps even after a failed poll).
+__device__ __forceinline__ void sync_bump(unsigned char* smem, int seq) {
+  if ((threadIdx.x & 63u) == 0)
+    __hip_atomic_store(reinterpret_cast<int*>(smem + kLdsFlag + 8), seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void sync_wait(unsigned char* smem, int seq) {
+  const int* c = reinterpret_cast<const int*>(smem + kLdsFlag + 8);
+  for (int spin = 0; spin < (1 << 22); ++spin) {
+    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) - seq >= 0) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+template <bool SYNC>
+__device__ __forceinline__ void sync_point(unsigned char* smem, int& seq) {
+  ++seq;
+  if constexpr (SYNC) sync_bump(smem, seq);
+}
+
+struct TagC {
+  unsigned t;
+  __device__ __forceinline__ unsigned operator()(int) const { return t; }
 };
 
 // ------------------------------------------------------------------ GEMV phase pieces
 
-// Weights of one GEMV phase held by a wave: U row-blocks of the phase's tile (a kernel instance
-// sizes U per matrix kind, so that only the next phase's weights stay live across a wait).
+// Weights of one GEMV phase held by a compute wave: up to U row-blocks of the phase's tile.
 template <int U>
 struct WRegs {
   UnitRegs u[U];
 };
 
-template <int U>
-__device__ __forceinline__ void gemv_prefetch(const uint8_t* W, int ntiles, const Assign& a, unsigned wave, unsigned lane,
+// Compute wave cw (0..kCW-1) loads its row-blocks rb0 + cw + kCW*m of tile t into slots m < UN
+// (slots >= UN are left alone: the phase that uses these registers reads only its UN slots).  Every
+// slot m < UN is loaded: one without a row-block reads 16 bytes of the matrix's first cache line, at
+// an offset of its own, in every lane, and its registers are never used.  A slot that were either
+// loaded or left as it was would become a phi, and the register allocator resolves phis (as it does
+// identical, merged loads) with copies next to the loads -- each copy waits for its load and turns
+// the prefetch into a stall.
+template <int UN, int U>
+__device__ __forceinline__ void gemv_prefetch(const uint8_t* W, int ntiles, int t, int rb0, int rb1, unsigned tid,
                                               WRegs<U>& r) {
+  static_assert(UN <= U, "prefetch slots exceed the register set");
+  const unsigned lane = tid & 63u, cw = (tid >> 6) - 1;
 #pragma unroll
-  for (int m = 0; m < U; ++m) {
-    const int rb = a.rb0 + (int)wave + kPtkWaves * m;
-    if (rb < a.rb1) {
-      load_unit(W + ((size_t)rb * ntiles + a.t) * kUnitBytes, lane, r.u[m]);
-    } else {  // define every slot, so that the previous phase's registers are dead from here on
-      r.u[m].s[0] = r.u[m].s[1] = r.u[m].s[2] = r.u[m].s[3] = u32x4{0u, 0u, 0u, 0u};
-      r.u[m].sc = u32x2{0u, 0u};
-    }
+  for (int m = 0; m < UN; ++m) {
+    const int rb = rb0 + (int)cw + kCW * m;
+    const bool v = rb < rb1;
+    const uint8_t* unit = W + ((size_t)(v ? rb : 0) * ntiles + t) * kUnitBytes;
+    const u32x4* sp = reinterpret_cast<const u32x4*>(v ? unit + (size_t)lane * 16 : W + (size_t)m * 80);
+    const int cs = v ? 64 : 1;  // chunk stride in 16-byte words
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.u[m].s[c] = __builtin_nontemporal_load(sp + c * cs);
+    const u32x2* scp = reinterpret_cast<const u32x2*>(v ? unit + kUnitSignBytes + (size_t)lane * 8 : W + (size_t)m * 80 + 64);
+    r.u[m].sc = __builtin_nontemporal_load(scp);
   }
 }
 
-template <int U>
-__device__ __forceinline__ void gemv_compute_ll(const Assign& a, const WRegs<U>& r, const unsigned c[16], u64* out,
-                                                int64_t ld, unsigned tag, unsigned wave, unsigned lane) {
-#pragma unroll
-  for (int m = 0; m < U; ++m) {
-    const int rb = a.rb0 + (int)wave + kPtkWaves * m;
-    if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, unit_dot(r.u[m], c), tag);
-  }
-}
-
-// LUT input sources: write xs[tid] for tile t (one column per thread) after waiting for their words.
-// The tile's sum of v^2 goes to sq (the GEMV phase publishes it from one workgroup per tile when
-// sst is set: the RMSNorm statistics of v, applied to the GEMV result by the consumer).
+// LUT input sources: the sync wave (lane = 0..63) writes xs[lane + 64*m] (m < 8) for tile t after
+// waiting for their words.  sq receives this lane's share of the tile's sum of v^2 when the source
+// is normed (the GEMV publishes the tile sum from one workgroup per tile when sst is set: the
+// RMSNorm statistics of v, applied to the GEMV result by its consumers).
 struct SrcNormedLL {  // v[col] * w[col]
   const u64* v;
   unsigned tag;
   const float* w;
   int K;
   u64* sst;
-  __device__ __forceinline__ bool stage(float* xs, int t, unsigned tid, const PtkErr& e, float& sq) const {
-    const int col = t * kTileCols + (int)tid;
-    float x = 0.f;
-    bool ok = true;
-    sq = 0.f;
-    if (col < K) {
-      float hv;
-      ok = ll_wait1(v + col, hv, tag, e);
-      x = hv * w[col];
-      sq = hv * hv;
+  __device__ __forceinline__ bool stage(float* xs, int t, unsigned lane, const PtkErr& e, float& sq) const {
+    // an opaque lane index: the loads below stay in this stage (when the stages of several tiles are
+    // unrolled one after another they would otherwise all be hoisted to the first)
+    asm volatile("" : "+v"(lane));
+    const int base = t * kTileCols + (int)lane;
+    float wv[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) wv[m] = base + 64 * m < K ? w[base + 64 * m] : 0.f;
+    u64 x[8];
+    const bool ok = poll<8>([&](int m, unsigned ln) { return v + t * kTileCols + ln + 64 * m; },
+                            [&](int m) { return base + 64 * m < K; }, TagC{tag}, x, e);
+    float s = 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      float o = 0.f;
+      if (base + 64 * m < K) {
+        const float hv = ll_val(x[m]);
+        o = hv * wv[m];
+        s += hv * hv;
+      }
+      xs[lane + 64 * m] = o;
     }
-    xs[tid] = x;
+    sq = s;
     return ok;
   }
 };
@@ -186,121 +203,183 @@ struct SrcPlainLL {
   unsigned tag;
   int K;
   static constexpr u64* sst = nullptr;
-  __device__ __forceinline__ bool stage(float* xs, int t, unsigned tid, const PtkErr& e, float& sq) const {
+  __device__ __forceinline__ bool stage(float* xs, int t, unsigned lane, const PtkErr& e, float& sq) const {
+    const int base = t * kTileCols + (int)lane;
+    u64 x[8];
+    const bool ok = poll<8>([&](int m, unsigned ln) { return v + t * kTileCols + ln + 64 * m; },
+                            [&](int m) { return base + 64 * m < K; }, TagC{tag}, x, e);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) xs[lane + 64 * m] = base + 64 * m < K ? ll_val(x[m]) : 0.f;
     sq = 0.f;
-    const int col = t * kTileCols + (int)tid;
-    float x = 0.f;
-    bool ok = true;
-    if (col < K) ok = ll_wait1(v + col, x, tag, e);
-    xs[tid] = x;
     return ok;
   }
 };
 
-// DeltaNet out-projection input: per v-head RMSNorm of y (from the quarters' sums of squares) times
-// ssm_norm times silu(z) (ssm_output_gate_avx2, model/ssm.rs:246-286).
+// DeltaNet out-projection input: per v-head RMSNorm of y (from 16 per-wave sums of squares per head)
+// times ssm_norm times silu(z) (ssm_output_gate_avx2, model/ssm.rs:246-286).  A tile holds 4 heads.
 struct SrcGatedYLL {
   const u64* y;
   const u64* zs;
-  const u64* yss;  // [nvh][4]
+  const u64* yss;  // [nvh][16]
   unsigned tag;
   const float* nw;
   int K;
   static constexpr u64* sst = nullptr;
-  __device__ __forceinline__ bool stage(float* xs, int t, unsigned tid, const PtkErr& e, float& sq) const {
-    sq = 0.f;
-    const int col = t * kTileCols + (int)tid;
-    float x = 0.f;
-    bool ok = true;
-    if (col < K) {
-      const int head = col >> 7;
-      const u64* a[6] = {y + col, zs + col, yss + head * 4, yss + head * 4 + 1, yss + head * 4 + 2, yss + head * 4 + 3};
-      u64 w[6];
-      ok = ll_wait<6>(a, w, tag, e);
-      const float s = (ll_val(w[2]) + ll_val(w[3])) + (ll_val(w[4]) + ll_val(w[5]));
+  __device__ __forceinline__ bool stage(float* xs, int t, unsigned lane, const PtkErr& e, float& sq) const {
+    const int base = t * kTileCols + (int)lane;
+    const int nh = K / 128, h0 = t * (kTileCols / 128);
+    float nwv[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) nwv[m] = base + 64 * m < K ? nw[(base + 64 * m) & 127] : 0.f;
+    u64 x[17];
+    auto addr = [&](int s, unsigned ln) -> const u64* {
+      const int b = t * kTileCols + (int)ln;
+      if (s < 8) return y + b + 64 * s;
+      if (s < 16) return zs + b + 64 * (s - 8);
+      return yss + (size_t)(h0 + (int)(ln >> 4)) * 16 + (ln & 15u);
+    };
+    auto valid = [&](int s) { return s < 16 ? base + 64 * (s & 7) < K : h0 + (int)(lane >> 4) < nh; };
+    const bool ok = poll<17>(addr, valid, TagC{tag}, x, e);
+    // lanes 16h..16h+15 hold the 16 partial sums of head h0 + h
+    const float hs = row16_sum(valid(16) ? ll_val(x[16]) : 0.f);
+    const int hb = __builtin_bit_cast(int, hs);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      // columns lane + 64m of the tile belong to head m / 2 of the tile
+      const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(hb, 16 * (m >> 1)));
       const float inv = 1.0f / sqrtf(s * (1.0f / 128.0f) + 1e-6f);
-      x = ((ll_val(w[0]) * inv) * nw[col & 127]) * ll_val(w[1]);
+      xs[lane + 64 * m] = base + 64 * m < K ? ((ll_val(x[m]) * inv) * nwv[m]) * ll_val(x[8 + m]) : 0.f;
     }
-    xs[tid] = x;
+    sq = 0.f;
     return ok;
   }
 };
 
-// One split-K GEMV phase on weights already requested (by the previous phase, right after its own
-// polls: vector loads complete in issue order, so weights in flight delay any later poll): stage +
-// LUT + units -> LL partials [t][row].  The first workgroup of each tile publishes the tile's sum
-// of squares when the source provides one.
-template <int U, class Src>
-__device__ __forceinline__ bool gemv_phase(unsigned char* smem, const Src& src, const WRegs<U>& r, const Assign& a,
+// Trace stamp `slot` of phase `ph` of token i, written by thread `by` (tracing runs only).
+__device__ __forceinline__ void ptk_mark(const PtkRun& r, const PtkPlan& P, int i, int ph, int w, unsigned tid,
+                                         unsigned by, int slot = 0) {
+  if (r.trace && tid == by)
+    glb(r.trace)[(((size_t)i * P.ppt + ph) * P.G + w) * kPtkTraceSlots + slot] = __builtin_amdgcn_s_memrealtime();
+}
+struct TraceAt;
+__device__ __forceinline__ bool r_trace_wait(const TraceAt& tr);
+struct TraceAt {  // where a GEMV phase stamps its sub-points
+  const PtkRun* r;
+  const PtkPlan* P;
+  int i, ph, w;
+  __device__ __forceinline__ void operator()(unsigned tid, unsigned by, int slot) const {
+    ptk_mark(*r, *P, i, ph, w, tid, by, slot);
+  }
+  // slot 0 from the last compute wave to finish its stores (an LDS arrival count, tracing runs only)
+  __device__ __forceinline__ void last_wave(unsigned char* smem, unsigned tid) const {
+    if (!r->trace) return;
+    if ((tid & 63u) == 0) {
+      int* cnt = reinterpret_cast<int*>(smem + kLdsFlag + 4);
+      const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if ((old + 1) % kCW == 0) ptk_mark(*r, *P, i, ph, w, tid, tid, 0);
+    }
+  }
+};
+__device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->trace != nullptr; }
+
+// One split-K GEMV phase, run by both roles (SYNC: the sync wave, else a compute wave) with the same
+// barriers.  The sync wave stages the tile's inputs (prior: its previous phases succeeded) and the
+// first workgroup of each tile publishes the tile's sum of squares when the source provides one;
+// all waves build the table; the compute waves run their row-blocks on weights already in
+// registers (requested by an earlier phase), publish LL partials [t][row] and call pf() (the next
+// GEMV's weight prefetch into the same registers).  The sync wave leaves once the table is built
+// and goes on to its next phase while the compute waves finish.
+template <bool SYNC, int UN, int U, class Src, class Pf>
+__device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, const Src& src, WRegs<U>& r, const Assign& a,
                                            bool lead, u64* out, int64_t ld, unsigned tag, unsigned tid,
-                                           const PtkErr& e) {
+                                           const PtkErr& e, const Pf& pf, const TraceAt& tr) {
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
-  float sq;
-  const bool ok = src.stage(xs, a.t, tid, e, sq);
-  if (!wg_ok(smem, ok)) return false;
-  if (src.sst != nullptr && lead) {
-    const float s = block_sum512(sq, lds_ptr<float>(smem, kLdsRed), tid);
-    if (tid == 0) ll_st(src.sst + a.t, s, tag);
+  bool ok = true;
+  if constexpr (SYNC) {
+    ok = prior;
+    if (ok) {
+      float sq = 0.f;
+      ok = src.stage(xs, a.t, tid, e, sq);
+      if (src.sst != nullptr && lead) {
+        const float s = wave_sum(sq);
+        if (tid == 0 && ok) ll_st(src.sst + a.t, s, tag);
+      }
+    }
+    tr(tid, 0, 3);
+  } else {
+    tr(tid, 64, 1);
   }
+  if (!wg_ok(smem, ok)) return false;  // inputs staged; every compute wave is done with the previous table
   build_lut<kPtkThreads>(lut, xs, tid);
   lds_barrier();
-  unsigned c[16];
-  make_pos_consts(tid & 63u, c);
-  gemv_compute_ll(a, r, c, out, ld, tag, tid >> 6, tid & 63u);
-  lds_barrier();  // every wave is done with the LUT before anyone rebuilds it
+  if constexpr (!SYNC) {
+    tr(tid, 64, 2);
+    const unsigned cw = (tid >> 6) - 1, lane = tid & 63u;
+    unsigned c[16];
+    make_pos_consts(lane, c);
+    // every dot product before the first store: gfx9 counts loads and stores on one vmcnt, and with
+    // a store pending the wait for the next row-block's weights becomes a wait for everything
+    float y[UN];
+#pragma unroll
+    for (int m = 0; m < UN; ++m) y[m] = a.rb0 + (int)cw + kCW * m < a.rb1 ? unit_dot(r.u[m], c) : 0.f;
+#pragma unroll
+    for (int m = 0; m < UN; ++m) {
+      const int rb = a.rb0 + (int)cw + kCW * m;
+      if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, y[m], tag);
+    }
+    tr.last_wave(smem, tid);
+    pf();
+  }
   return true;
 }
 
-// ------------------------------------------------------------------ phase S: token + embedding
+// ------------------------------------------------------------------ sync-wave phases
 
-template <class Pf>
-__device__ __forceinline__ bool phase_select(unsigned char* smem, const PtkPlan& P, const PtkRun& r, int i, int w,
-                                             unsigned tid, u64* tokreg, const u64* prev_cand_v, const u64* prev_cand_i,
-                                             unsigned tag_prev_l, unsigned tag, int pos, int& tok_out, const Pf& pf) {
-  const PtkErr& e = r.err;
-  int* tok_s = lds_ptr<int>(smem, kLdsScratch);
+// S: token of step i -- a fed id, or the greedy pick over the previous lm_head's per-workgroup
+// candidates (first maximum, simd_exp.rs:551-598) -- and this workgroup's embedding columns
+// (forward.rs:212-213), published as LL words.
+__device__ __forceinline__ int s_pick(const PtkPlan& P, unsigned lane, const u64* cand_v, const u64* cand_i,
+                                      unsigned tag_prev, const PtkErr& e, bool& ok) {
+  u64 x[16];
+  auto addr = [&](int s, unsigned ln) {
+    const int c = (int)ln + 64 * (s >> 1);
+    return (s & 1) ? cand_i + c : cand_v + c;
+  };
+  auto valid = [&](int s) { return (int)lane + 64 * (s >> 1) < P.G; };
+  ok = poll<16>(addr, valid, TagC{tag_prev}, x, e);
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    if (valid(2 * s)) {
+      const float v = ll_val(x[2 * s]);
+      const int id = __float_as_int(ll_val(x[2 * s + 1]));
+      if (am_better(v, id, bv, bi)) {
+        bv = v;
+        bi = id;
+      }
+    }
+  wave_argmax(bv, bi);
+  int tok = __builtin_amdgcn_readfirstlane(bi);
+  if (tok < 0 || tok >= P.vocab) tok = 0;  // no candidate (or a failed wait): token 0
+  return tok;
+}
+
+__device__ __forceinline__ bool s_select(const PtkPlan& P, const PtkRun& r, int i, int w, unsigned lane, u64* hemb,
+                                         const u64* cand_v, const u64* cand_i, unsigned tag_prev, unsigned tag,
+                                         int pos) {
+  bool ok = true;
+  int tok;
   if (i < r.n_feed) {
-    if (tid == 0) *tok_s = glb(r.feed)[i];
+    tok = __builtin_amdgcn_readfirstlane(glb(r.feed)[i]);
   } else {
-    // greedy: first maximum over the previous lm_head's per-workgroup candidates (simd_exp.rs:551-598)
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    bool ok = true;
-    if ((int)tid < P.G) {
-      const u64* a[2] = {prev_cand_v + tid, prev_cand_i + tid};
-      u64 wv[2];
-      ok = ll_wait<2>(a, wv, tag_prev_l, e);
-      bv = ll_val(wv[0]);
-      bi = __float_as_int(ll_val(wv[1]));
-    }
-    if (!wg_ok(smem, ok)) return false;
-    wave_argmax(bv, bi);
-    float* sv = lds_ptr<float>(smem, kLdsScratch + 64);
-    int* si = lds_ptr<int>(smem, kLdsScratch + 128);
-    if ((tid & 63u) == 0) {
-      sv[tid >> 6] = bv;
-      si[tid >> 6] = bi;
-    }
-    lds_barrier();
-    if (tid == 0) {
-      for (int wv = 1; wv < kPtkWaves; ++wv)
-        if (am_better(sv[wv], si[wv], bv, bi)) {
-          bv = sv[wv];
-          bi = si[wv];
-        }
-      *tok_s = bi == 0x7FFFFFFF ? 0 : bi;
-    }
+    tok = s_pick(P, lane, cand_v, cand_i, tag_prev, r.err, ok);
   }
-  lds_barrier();
-  const int tok = *tok_s;
-  tok_out = tok;
-  if (w == 0 && tid == 0) P.toklog[pos] = tok;
-  // embedding columns [c0, c1) of this workgroup (forward.rs:212-213)
+  if (w == 0 && lane == 0) P.toklog[pos] = tok;
   int c0, c1;
   even_split(w, P.G, P.H, &c0, &c1);
-  u64* hemb = tokreg;
-  for (int col = c0 + (int)tid; col < c1; col += kPtkThreads) {
+  for (int col = c0 + (int)lane; col < c1; col += 64) {
     float v;
     if (P.embd_f16) {
       v = ref_f16_to_f32_dev(P.emb_f16[(size_t)tok * P.H + col]);
@@ -317,254 +396,121 @@ __device__ __forceinline__ bool phase_select(unsigned char* smem, const PtkPlan&
     }
     ll_st(hemb + col, v, tag);
   }
-  pf();
-  return true;
+  return ok;
 }
 
-// ------------------------------------------------------------------ R phases (tile sums)
-
-// h_out = h_in + sum_t part[t][col] for this workgroup's columns (term 0 is h_in, then the tiles in
-// order), all polled together; pf() runs after the result is stored.  Columns per workgroup <= 512.
-template <int NT, class Pf>
-__device__ __forceinline__ bool phase_resid(unsigned char* smem, const PtkPlan& P, int w, unsigned tid, const u64* h_in,
-                                            unsigned tag_h, const u64* part, int np, int64_t ldp, unsigned tag_p,
-                                            u64* h_out, unsigned tag, const PtkErr& e, const Pf& pf) {
+// R1 / R3: h_out[c] = h_in[c] + sum_t part[t][c] for this workgroup's columns c (term 0 is h_in,
+// then the tiles in order).  Lane (j, q) sums terms [q*Q, q*Q+Q) of column j; lane j then adds the
+// nq slices in order.
+template <int QMAX>
+__device__ __forceinline__ bool s_resid(const PtkPlan& P, int w, unsigned lane, const u64* h_in, unsigned tag_h,
+                                        const u64* part, int np, int64_t ldp, unsigned tag_p, u64* h_out, unsigned tag,
+                                        const PtkErr& e) {
   int c0, c1;
   even_split(w, P.G, P.H, &c0, &c1);
   const int nc = c1 - c0;
-  auto ptr = [&](int j, int k) { return k == 0 ? h_in + c0 + j : part + (size_t)(k - 1) * ldp + c0 + j; };
-  auto tagf = [&](int k) { return k == 0 ? tag_h : tag_p; };
-  float v = 0.f;
-  if (!ll_colsum<kPtkColQ>(smem, nc, np + 1, ptr, tagf, tid, e, v)) return false;
-  if ((int)tid < nc) ll_st(h_out + c0 + tid, v, tag);
-  pf();  // after the store: issuing a whole phase of weights can stall until part of it has landed
-  return true;
+  if (nc <= 0) return true;
+  const int K = np + 1;
+  const int nq = min(64 / nc, K);
+  const int Q = (K + nq - 1) / nq;
+  const int j = (int)lane % nc, q = (int)lane / nc;
+  const int k0 = q * Q;
+  const bool act = q < nq;
+  u64 x[QMAX];
+  auto addr = [&](int s, unsigned ln) {
+    const int jl = (int)ln % nc, k = ((int)ln / nc) * Q + s;
+    return k == 0 ? h_in + c0 + jl : part + (size_t)(k - 1) * ldp + c0 + jl;
+  };
+  auto valid = [&](int s) { return act && s < Q && k0 + s < K; };
+  auto tagf = [&](int s) { return k0 + s == 0 ? tag_h : tag_p; };
+  const bool ok = poll<QMAX>(addr, valid, tagf, x, e);
+  float sl = 0.f;
+#pragma unroll
+  for (int s = 0; s < QMAX; ++s)
+    if (valid(s)) sl += ll_val(x[s]);
+  float tot = 0.f;
+  for (int qq = 0; qq < nq; ++qq) tot += __shfl(sl, j + qq * nc, 64);
+  if ((int)lane < nc && ok) ll_st(h_out + c0 + lane, tot, tag);
+  return ok;
 }
 
-// sw[f] = silu(inv * sum_t g) * (inv * sum_t u) for this workgroup's ffn channels (mlp.rs:28-47):
-// columns 0..nf-1 are the gate rows, nf..2nf-1 the up rows, column 2nf the tile sums of squares of
-// h_mid (all written by the gate/up phase); pf() runs after the results are stored.
-template <int NT, class Pf>
-__device__ __forceinline__ bool phase_swiglu(unsigned char* smem, const PtkPlan& P, int w, unsigned tid, const u64* sstm,
-                                             const u64* pgu, unsigned tag_p, u64* sw, unsigned tag, const PtkErr& e,
-                                             const Pf& pf) {
+// R2: sw[f] = silu(inv * sum_t g[t][f]) * (inv * sum_t u[t][f]) for this workgroup's ffn channels f
+// (lane handles f0 + lane + 64m), inv from h_mid's tile sums of squares (mlp.rs:28-47).
+template <int NTH, int MF>
+__device__ __forceinline__ bool s_swiglu(const PtkPlan& P, int w, unsigned lane, const u64* sstm, const u64* pgu,
+                                         unsigned tag_p, u64* sw, unsigned tag, const PtkErr& e) {
   int f0, f1;
   even_split(w, P.G, P.F, &f0, &f1);
   const int nf = f1 - f0;
   const int64_t ldp = (int64_t)P.nrb_gu * kRowBlock;
-  auto ptr = [&](int j, int k) {
-    return j == 2 * nf ? sstm + k : pgu + (size_t)k * ldp + (j < nf ? f0 + j : P.F + f0 + (j - nf));
+  const int T = P.nT_h;
+  constexpr int N = MF * 2 * NTH + 1;
+  u64 x[N];
+  auto addr = [&](int s, unsigned ln) -> const u64* {
+    if (s == N - 1) return sstm + ln;
+    const int m = s / (2 * NTH), g = (s / NTH) & 1, k = s % NTH;
+    const int f = f0 + (int)ln + 64 * m;
+    return pgu + (size_t)k * ldp + (g ? P.F + f : f);
   };
-  auto tagf = [&](int) { return tag_p; };
-  float v = 0.f;
-  if (!ll_colsum<kPtkColQ>(smem, 2 * nf + 1, P.nT_h, ptr, tagf, tid, e, v)) return false;
-  float* gu = lds_ptr<float>(smem, kLdsScratch);
-  if ((int)tid <= 2 * nf) gu[tid] = v;
-  lds_barrier();
-  const float inv = 1.0f / sqrtf(gu[2 * nf] / (float)P.H + P.eps);
-  if ((int)tid < nf) ll_st(sw + f0 + tid, siluf_(gu[tid] * inv) * (gu[nf + tid] * inv), tag);
-  pf();
-  lds_barrier();
-  return true;
+  auto valid = [&](int s) {
+    if (s == N - 1) return (int)lane < T;
+    const int m = s / (2 * NTH), k = s % NTH;
+    return k < T && (int)lane + 64 * m < nf;
+  };
+  const bool ok = poll<N>(addr, valid, TagC{tag_p}, x, e);
+  const float ss = wave_sum((int)lane < T ? ll_val(x[N - 1]) : 0.f);
+  const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+#pragma unroll
+  for (int m = 0; m < MF; ++m) {
+    const int f = (int)lane + 64 * m;
+    if (f < nf && ok) {
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int k = 0; k < NTH; ++k)
+        if (k < T) {
+          g += ll_val(x[m * 2 * NTH + k]);
+          u += ll_val(x[m * 2 * NTH + NTH + k]);
+        }
+      ll_st(sw + f0 + f, siluf_(g * inv) * (u * inv), tag);
+    }
+  }
+  return ok;
 }
 
-// ------------------------------------------------------------------ phase B: Gated DeltaNet step
-
-// Workgroup w < 4*nvh: v-head w/4, state rows (w%4)*32 .. +32; threads 0..255 as in deltanet_kernel.
-template <int NTH, class Pf>
-__device__ __forceinline__ bool phase_deltanet(unsigned char* smem, const PtkPlan& P, const PtkLayer& Ly, int ring_base,
-                                               int w, unsigned tid, int pos, const u64* sst_in, const u64* pin,
-                                               unsigned tag_in, u64* y, u64* zs, u64* yss, unsigned tag,
-                                               const PtkErr& e, const Pf& pf) {
-  constexpr int HD = 128;
-  if (w >= 4 * P.nvh) {
-    pf();
-    return true;
-  }
-  float* qs = lds_ptr<float>(smem, kLdsScratch);
-  float* ks = qs + HD;
-  float* vs = ks + HD;
-  float* red = vs + 32;  // [0..3] q/k norms, [24] inv rms
-  float* part = red + 16;  // [8][32]
-  float* dsh = part + 8 * 32;
-  float* sc = dsh + 32;
-  const int vh = w >> 2, quarter = w & 3, kh = vh % P.nkh;
-  const int i_loc = tid & 31, js = (tid >> 5) & 7;
-  const int i = quarter * 32 + i_loc;
-  const int hb = (ring_base + pos) & 3;
-  const int64_t kdim = (int64_t)P.nkh * HD, qkvd = P.qkvd;
-  const int64_t ldp = (int64_t)Ly.nrb_in * kRowBlock;
-  const bool act = tid < 256;
-  float s[16];
-  float xq = 0.f, x2 = 0.f;
-  float r1 = 0.f, r2 = 0.f, r3 = 0.f, w0 = 0.f, w1 = 0.f, w2 = 0.f, w3 = 0.f;
-  float v1 = 0.f, v2 = 0.f, v3 = 0.f, u0 = 0.f, u1 = 0.f, u2 = 0.f, u3 = 0.f, ssm_a = 0.f, dtb = 0.f;
-  int64_t ch = 0, row2 = -1;
-  bool ok = true;
-  if (act) {
-    float* S = Ly.state + (size_t)vh * HD * HD;
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
-    ch = tid < HD ? (int64_t)kh * HD + tid : kdim + (int64_t)kh * HD + (tid - HD);
-    r1 = co_ld(Ly.conv + (size_t)((hb + 1) & 3) * qkvd + ch);
-    r2 = co_ld(Ly.conv + (size_t)((hb + 2) & 3) * qkvd + ch);
-    r3 = co_ld(Ly.conv + (size_t)((hb + 3) & 3) * qkvd + ch);
-    w0 = Ly.conv_w[ch];
-    w1 = Ly.conv_w[qkvd + ch];
-    w2 = Ly.conv_w[2 * qkvd + ch];
-    w3 = Ly.conv_w[3 * qkvd + ch];
-    if (tid < 32) row2 = 2 * kdim + (int64_t)vh * HD + quarter * 32 + tid;
-    else if (tid < 64) row2 = P.off_z + (int64_t)vh * HD + quarter * 32 + (tid - 32);
-    else if (tid == 64) row2 = P.off_a + vh;
-    else if (tid == 65) row2 = P.off_b + vh;
-    if (tid < 32) {
-      v1 = co_ld(Ly.conv + (size_t)((hb + 1) & 3) * qkvd + row2);
-      v2 = co_ld(Ly.conv + (size_t)((hb + 2) & 3) * qkvd + row2);
-      v3 = co_ld(Ly.conv + (size_t)((hb + 3) & 3) * qkvd + row2);
-      u0 = Ly.conv_w[row2];
-      u1 = Ly.conv_w[qkvd + row2];
-      u2 = Ly.conv_w[2 * qkvd + row2];
-      u3 = Ly.conv_w[3 * qkvd + row2];
-    }
-    if (tid == 64) {
-      ssm_a = Ly.ssm_a[vh];
-      dtb = Ly.dt_bias[vh];
-    }
-  }
-  // the layer input's tile sums of squares (inv rms), polled alongside the projections
-  u64 sw = (u64)tag_in << 32;
-  if ((int)tid < P.nT_h) sw = ll_ld(sst_in + tid);
-  if (act) {
-    ok = ll_sum<NTH>(pin + ch, ldp, P.nT_h, tag_in, e, xq);
-    if (ok && row2 >= 0) ok = ll_sum<NTH>(pin + row2, ldp, P.nT_h, tag_in, e, x2);
-  }
-  if ((int)tid < P.nT_h && ok) {
-    for (int spin = 0; ll_tag(sw) != tag_in; ++spin) {
-      if (spin >= e.spin_limit) {
-        ptk_fail(e, 4, tag_in);
-        ok = false;
-        break;
-      }
-      sw = ll_ld(sst_in + tid);
-    }
-  }
-  if (tid < 64) {
-    const float sst = wave_sum((int)tid < P.nT_h ? ll_val(sw) : 0.f);
-    if (tid == 0) red[24] = 1.0f / sqrtf(sst / (float)P.H + P.eps);
-  }
-  if (!wg_ok(smem, ok)) return false;
-  const float inv = red[24];
-  // conv ring + causal conv + SiLU (ssm.rs:467-518)
-  float qk = 0.f;
-  if (act) {
-    const float xn = xq * inv;
-    float o = 0.f;
-    o = __builtin_fmaf(r1, w0, o);
-    o = __builtin_fmaf(r2, w1, o);
-    o = __builtin_fmaf(r3, w2, o);
-    o = __builtin_fmaf(xn, w3, o);
-    qk = siluf_(o);
-    if (vh < P.nkh && quarter == 0) co_st(Ly.conv + (size_t)hb * qkvd + ch, xn);
-    const float x2n = x2 * inv;
-    if (tid < 32) {
-      float ov = 0.f;
-      ov = __builtin_fmaf(v1, u0, ov);
-      ov = __builtin_fmaf(v2, u1, ov);
-      ov = __builtin_fmaf(v3, u2, ov);
-      ov = __builtin_fmaf(x2n, u3, ov);
-      vs[tid] = siluf_(ov);
-      co_st(Ly.conv + (size_t)hb * qkvd + row2, x2n);
-    } else if (tid < 64) {
-      ll_st(zs + (size_t)vh * HD + quarter * 32 + (tid - 32), siluf_(x2n), tag);
-    } else if (tid == 64) {
-      const float x = x2n + dtb;
-      const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
-      sc[0] = expf(ssm_a * sp);
-    } else if (tid == 65) {
-      sc[1] = sigmoidf_(x2n);
-    }
-  }
-  const float s2 = wave_sum(qk * qk);
-  if ((tid & 63u) == 0 && tid < 256) red[tid >> 6] = s2;
-  lds_barrier();
-  if (tid < HD) {
-    const float inq = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
-    qs[tid] = (qk * inq) * (1.0f / sqrtf((float)HD));
-  } else if (tid < 256) {
-    const float ink = 1.0f / sqrtf((red[2] + red[3]) + 1e-6f);
-    ks[tid - HD] = qk * ink;
-  }
-  lds_barrier();
-  const float decay = sc[0], beta = sc[1];
-  if (act) {
-    float kvp = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      s[jj] *= decay;
-      kvp = __builtin_fmaf(s[jj], ks[js * 16 + jj], kvp);
-    }
-    part[js * 32 + i_loc] = kvp;
-  }
-  lds_barrier();
-  if (tid < 32) {
-    float kv = 0.f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) kv += part[q * 32 + i_loc];
-    dsh[i_loc] = (vs[i_loc] - kv) * beta;
-  }
-  lds_barrier();
-  if (act) {
-    const float d = dsh[i_loc];
-    float* S = Ly.state + (size_t)vh * HD * HD;
-    float yp = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int j = js * 16 + jj;
-      s[jj] = __builtin_fmaf(d, ks[j], s[jj]);
-      S[(size_t)j * HD + i] = s[jj];
-      yp = __builtin_fmaf(s[jj], qs[j], yp);
-    }
-    part[js * 32 + i_loc] = yp;
-  }
-  lds_barrier();
-  // the ring stores above are complete before this step's outputs become visible
-  wait_stores();
-  if (tid < 64) {
-    float yy = 0.f;
-    if (tid < 32) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) yy += part[q * 32 + i_loc];
-      ll_st(y + (size_t)vh * HD + i, yy, tag);
-    }
-    const float ys = wave_sum(yy * yy);
-    if (tid == 0) ll_st(yss + vh * 4 + quarter, ys, tag);
-  }
-  pf();  // the next matrix phase's weights (issued last: fewer registers live during the math)
-  return true;
-}
-
-// ------------------------------------------------------------------ attention phases
-
-// R0: q|gate|k|v projections = inv * sum of in-proj partials, for this workgroup's rows (the last
-// column sums the layer input's tile sums of squares).
-template <int NTH>
-__device__ __forceinline__ bool phase_qkv(unsigned char* smem, const PtkPlan& P, const PtkLayer& Ly, int w, unsigned tid,
-                                          const u64* sst_in, const u64* pin, unsigned tag_in, u64* qkv, unsigned tag,
-                                          const PtkErr& e) {
+// R0: q|gate|k|v projections = inv * sum of in-proj partials for this workgroup's rows.
+template <int NTH, int MR>
+__device__ __forceinline__ bool s_qkv(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned lane, const u64* sst_in,
+                                      const u64* pin, unsigned tag_in, u64* qkv, unsigned tag, const PtkErr& e) {
   int r0, r1;
   even_split(w, P.G, Ly.rows_in, &r0, &r1);
   const int nr = r1 - r0;
   const int64_t ldp = (int64_t)Ly.nrb_in * kRowBlock;
-  auto ptr = [&](int j, int k) { return j == nr ? sst_in + k : pin + (size_t)k * ldp + r0 + j; };
-  auto tagf = [&](int) { return tag_in; };
-  float v = 0.f;
-  if (!ll_colsum<kPtkColQ>(smem, nr + 1, P.nT_h, ptr, tagf, tid, e, v)) return false;
-  float* red = lds_ptr<float>(smem, kLdsRed);
-  if ((int)tid == nr) red[32] = 1.0f / sqrtf(v / (float)P.H + P.eps);
-  lds_barrier();
-  if ((int)tid < nr) ll_st(qkv + r0 + tid, v * red[32], tag);
-  lds_barrier();
-  return true;
+  const int T = P.nT_h;
+  constexpr int N = MR * NTH + 1;
+  u64 x[N];
+  auto addr = [&](int s, unsigned ln) -> const u64* {
+    if (s == N - 1) return sst_in + ln;
+    return pin + (size_t)(s % NTH) * ldp + r0 + (int)ln + 64 * (s / NTH);
+  };
+  auto valid = [&](int s) {
+    if (s == N - 1) return (int)lane < T;
+    return s % NTH < T && (int)lane + 64 * (s / NTH) < nr;
+  };
+  const bool ok = poll<N>(addr, valid, TagC{tag_in}, x, e);
+  const float ss = wave_sum((int)lane < T ? ll_val(x[N - 1]) : 0.f);
+  const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int row = (int)lane + 64 * m;
+    if (row < nr && ok) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < NTH; ++k)
+        if (k < T) v += ll_val(x[m * NTH + k]);
+      ll_st(qkv + r0 + row, v * inv, tag);
+    }
+  }
+  return ok;
 }
 
 __device__ __forceinline__ void attn_chunks(const PtkPlan& P, int pos, int* chunk, int* gc) {
@@ -575,112 +521,343 @@ __device__ __forceinline__ void attn_chunks(const PtkPlan& P, int pos, int* chun
   *gc = (ctx + ch - 1) / ch;
 }
 
-// B': workgroup (kv-head, chunk g) -- online softmax of attention.rs:124-199 over its positions
-// for the kv-head's GRP query heads; q/k RMSNorm, the reference's +/+ partial RoPE, q *= 1/sqrt(hd);
-// the chunk holding the new position appends its k/v.  Writes rec = (m, l, o[hd]) per q-head.
-template <int GRP>
-__device__ __forceinline__ bool phase_attn(unsigned char* smem, const PtkPlan& P, const PtkLayer& Ly, int w,
+// R'': merge the chunk records of each query head and apply the output gate (attention.rs:189-203):
+// ao[h*hd + d] = (O/L) * sigmoid(gate).  Lane g holds chunk g; this workgroup's outputs [j0, j1)
+// span at most two heads.
+template <int MO, class Tr>
+__device__ __forceinline__ bool s_merge(const PtkPlan& P, int w, unsigned lane, int pos, const u64* rec,
+                                        unsigned tag_r, const u64* qkv, unsigned tag_q, u64* ao, unsigned tag,
+                                        const PtkErr& e, const Tr& tr) {
+  constexpr int HD = 256;
+  int chunk, gc;
+  attn_chunks(P, pos, &chunk, &gc);
+  int j0, j1;
+  even_split(w, P.G, P.nq * HD, &j0, &j1);
+  const int no = j1 - j0;
+  if (no <= 0) return true;
+  const int hf = j0 / HD, hl = (j1 - 1) / HD;
+  const bool lg = (int)lane < gc;
+  // slots: 0..3 = m, l of heads hf, hf+1; 4..4+MO-1 = o of output jj; last = gate of output `lane`
+  constexpr int N = 4 + MO + 1;
+  u64 x[N];
+  auto addr = [&](int s, unsigned ln) -> const u64* {
+    auto recp = [&](int h) { return rec + ((size_t)h * P.gmax + ln) * (2 + HD); };
+    if (s < 4) return recp(hf + (s >> 1)) + (s & 1);
+    if (s < 4 + MO) {
+      const int j = j0 + (s - 4);
+      return recp(j / HD) + 2 + (j % HD);
+    }
+    const int j = j0 + (int)ln;
+    return qkv + (int64_t)((j / HD) * 2 + 1) * HD + (j % HD);
+  };
+  auto valid = [&](int s) {
+    if (s < 4) return lg && hf + (s >> 1) <= hl;
+    if (s < 4 + MO) return lg && s - 4 < no;
+    return (int)lane < no;
+  };
+  auto tagf = [&](int s) { return s < 4 + MO ? tag_r : tag_q; };
+  const bool ok = poll<N>(addr, valid, tagf, x, e);
+  tr(lane, 0, 2);
+  float ex[2], L[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const float mv = valid(2 * hh) ? ll_val(x[2 * hh]) : -INFINITY;
+    const float M = wave_max(mv);
+    ex[hh] = valid(2 * hh) ? __expf(mv - M) : 0.f;
+    L[hh] = wave_sum((valid(2 * hh) ? ll_val(x[2 * hh + 1]) : 0.f) * ex[hh]);
+  }
+  const int gb = __float_as_int((int)lane < no ? ll_val(x[N - 1]) : 0.f);
+  float mine = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < MO; ++jj) {
+    if (jj < no) {
+      const int hh = (j0 + jj) / HD - hf;
+      const float ov = valid(4 + jj) ? ll_val(x[4 + jj]) : 0.f;
+      const float O = wave_sum(ov * (hh ? ex[1] : ex[0]));
+      const float gate = __int_as_float(__builtin_amdgcn_readlane(gb, jj));
+      const float v = (O * (1.0f / (hh ? L[1] : L[0]))) * sigmoidf_(gate);
+      if ((int)lane == jj) mine = v;
+    }
+  }
+  if ((int)lane < no && ok) ll_st(ao + j0 + lane, mine, tag);
+  return ok;
+}
+
+// ------------------------------------------------------------------ phase B: Gated DeltaNet step
+
+// State rows of a compute thread in the DeltaNet phase: waves 4..7 hold rows quarter*32 + (wave-4)*8
+// + (lane >> 3), columns (lane & 7)*16 .. +16 of the v-head's 128x128 state S[j][i].
+__device__ __forceinline__ void dn_state_load(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned tid,
+                                              float (&s)[16]) {
+  // every thread loads: a thread without rows reads 16 distinct words of one cache line, so that no
+  // phi forms and no identical loads merge (the register copies either needs would wait for the loads)
+  const bool v = !Ly.attn && w < 4 * P.nvh && tid >= 256;
+  const int vh = w >> 2, quarter = w & 3;
+  const unsigned lane = tid & 63u, w4 = (tid >> 6) - 4, il = lane >> 3, js = lane & 7u;
+  const int i = quarter * 32 + (int)(w4 * 8 + il);
+  const float* S = v ? Ly.state + (size_t)vh * 128 * 128 + (size_t)js * 16 * 128 + i : P.output_norm;
+  const int st = v ? 128 : 1;
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) s[jj] = co_ld(S + (size_t)jj * st);
+}
+
+// Workgroup w < 4*nvh: v-head w/4, state rows (w%4)*32 .. +32 (ssm.rs:425-616).  The sync wave takes
+// its 322 in-projection channels (q and k of the tiled k-head kh = vh % nkh, this quarter's v and z
+// channels, alpha, beta; summed and scaled by 1/rms in phase R0), runs the conv ring + causal conv +
+// SiLU, the q/k L2 norms and the gates, and publishes silu(z); waves 4..7 then run the delta rule on
+// the state rows held in registers and publish y and per-wave sums of y^2.
+// Sum over the 8 lanes of each aligned group of 8 (DPP: xor 1, xor 2, then the half-row mirror
+// adds the two quads); every lane of the group gets bitwise the same value.
+__device__ __forceinline__ float group8_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  return v;
+}
+
+// LDS layout of the DeltaNet phase (scratch): q[128] k[128] v[32] | decay, beta | conv inputs of the
+// 288 convolved channels (q 0..127, k 128..255, this quarter's v 256..287): ring history [3][288]
+// (t = 0 oldest) and conv weights [4][288] | ssm_a, dt_bias.
+constexpr int kDnCh = 288;
+constexpr int kDnRing = 128 + 128 + 32 + 4;           // float offset of the ring history
+constexpr int kDnConvW = kDnRing + 3 * kDnCh;         // conv weights
+constexpr int kDnGate = kDnConvW + 4 * kDnCh;         // ssm_a, dt_bias
+static_assert((kDnGate + 2) * 4 <= kLdsScratchBytes, "DeltaNet scratch exceeds the LDS scratch area");
+
+// In-projection row of convolved channel c (0..287) of v-head vh, quarter `quarter`.
+__device__ __forceinline__ int64_t dn_conv_row(const PtkPlan& P, int kh, int vh, int quarter, int c) {
+  const int64_t kdim = (int64_t)P.nkh * 128;
+  return c < 128 ? (int64_t)kh * 128 + c : c < 256 ? kdim + (int64_t)kh * 128 + (c - 128)
+                                                   : 2 * kdim + (int64_t)vh * 128 + quarter * 32 + (c - 256);
+}
+
+// Workgroup w < 4*nvh: v-head w/4, state rows (w%4)*32 .. +32 (ssm.rs:425-616).  Compute waves 1..3
+// bring the conv ring history, conv weights and gate constants into LDS (memory traffic kept off the
+// sync wave's pipeline position, ahead of its polls) and count themselves in; the sync wave takes
+// its in-projection channels (q and k of the tiled k-head kh = vh % nkh, this quarter's v and z
+// channels, alpha, beta; summed and scaled by 1/rms in phase R0), runs the conv ring + causal conv +
+// SiLU, the q/k L2 norms and the gates, and publishes silu(z); waves 4..7 then run the delta rule on
+// the state rows held in registers and publish y and per-wave sums of y^2.  dn_seq counts DeltaNet
+// phases (both roles), for the compute waves' LDS arrival count.
+template <bool SYNC>
+__device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const PtkPlan& P, const PtkLayer& Ly,
+                                         int ring_base, int w, unsigned tid, int pos, const u64* qkvz, unsigned tag_in,
+                                         u64* y, u64* zs, u64* yss, unsigned tag, const PtkErr& e, float (&s)[16],
+                                         int dn_seq, const TraceAt& tr) {
+  constexpr int HD = 128;
+  if (w >= 4 * P.nvh) return wg_ok(smem, SYNC ? prior : true);
+  float* qs = lds_ptr<float>(smem, kLdsScratch);
+  float* ks = qs + HD;
+  float* vs = ks + HD;
+  float* sc = vs + 32;  // decay, beta
+  float* rl = qs + kDnRing;
+  float* cwl = qs + kDnConvW;
+  float* gl = qs + kDnGate;
+  int* arrivals = reinterpret_cast<int*>(smem + kLdsFlag + 12);
+  const int vh = w >> 2, quarter = w & 3, kh = vh % P.nkh;
+  const int hb = (ring_base + pos) & 3;
+  const int64_t qkvd = P.qkvd;
+  bool ok = SYNC ? prior : true;
+  if (!SYNC && tid < 256) {
+    // waves 1..3: conv inputs of channels c = tid-64 and tid-64+192
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = (int)tid - 64 + 192 * k;
+      if (c < kDnCh) {
+        const int64_t row = dn_conv_row(P, kh, vh, quarter, c);
+#pragma unroll
+        for (int t = 0; t < 3; ++t) rl[t * kDnCh + c] = co_ld(Ly.conv + (size_t)((hb + 1 + t) & 3) * qkvd + row);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) cwl[t * kDnCh + c] = Ly.conv_w[(size_t)t * qkvd + row];
+      }
+    }
+    if (tid == 64) {
+      gl[0] = Ly.ssm_a[vh];
+      gl[1] = Ly.dt_bias[vh];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are done (lgkmcnt(0))
+    if ((tid & 63u) == 0) __hip_atomic_fetch_add(arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  if (SYNC && ok) {
+    const unsigned lane = tid;
+    const bool vlane = lane < 32;  // slot 4: a v channel (convolved) below lane 32, a z channel above
+    int64_t row[6];
+    row[0] = dn_conv_row(P, kh, vh, quarter, (int)lane);
+    row[1] = dn_conv_row(P, kh, vh, quarter, (int)lane + 64);
+    row[2] = dn_conv_row(P, kh, vh, quarter, (int)lane + 128);
+    row[3] = dn_conv_row(P, kh, vh, quarter, (int)lane + 192);
+    row[4] = vlane ? dn_conv_row(P, kh, vh, quarter, 256 + (int)lane) : P.off_z + (int64_t)vh * HD + quarter * 32 + (lane - 32);
+    row[5] = lane == 0 ? P.off_a + vh : P.off_b + vh;
+    u64 x[6];
+    ok = poll<6>([&](int sl, unsigned) { return qkvz + row[sl]; }, [&](int sl) { return sl < 5 || lane < 2; },
+                 TagC{tag_in}, x, e);
+    float xn[6];
+#pragma unroll
+    for (int sl = 0; sl < 6; ++sl) xn[sl] = sl < 5 || lane < 2 ? ll_val(x[sl]) : 0.f;
+    // the compute waves' conv inputs (bounded wait; they always arrive)
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      if (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) - 3 * dn_seq >= 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // conv ring + causal conv + SiLU (ssm.rs:467-518): tap 3 is this token
+    float c[5];
+#pragma unroll
+    for (int sl = 0; sl < 5; ++sl) {
+      const int ch = sl < 4 ? (int)lane + 64 * sl : 256 + (int)(lane & 31u);
+      float o = 0.f;
+      o = __builtin_fmaf(rl[0 * kDnCh + ch], cwl[0 * kDnCh + ch], o);
+      o = __builtin_fmaf(rl[1 * kDnCh + ch], cwl[1 * kDnCh + ch], o);
+      o = __builtin_fmaf(rl[2 * kDnCh + ch], cwl[2 * kDnCh + ch], o);
+      o = __builtin_fmaf(xn[sl], cwl[3 * kDnCh + ch], o);
+      c[sl] = siluf_(o);
+    }
+    if (ok) {
+      if (vh < P.nkh && quarter == 0) {
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) co_st(Ly.conv + (size_t)hb * qkvd + row[sl], xn[sl]);
+      }
+      if (vlane) co_st(Ly.conv + (size_t)hb * qkvd + row[4], xn[4]);
+      else ll_st(zs + (size_t)vh * HD + quarter * 32 + (lane - 32), siluf_(xn[4]), tag);
+    }
+    if (lane == 0) {
+      const float xa = xn[5] + gl[1];
+      const float sp = xa > 20.0f ? xa : logf(1.0f + expf(xa));
+      sc[0] = expf(gl[0] * sp);
+    } else if (lane == 1) {
+      sc[1] = sigmoidf_(xn[5]);
+    }
+    // L2 norms of q and k (ssm.rs:76-135), q *= 1/sqrt(128) (ssm.rs:532-533)
+    const float inq = 1.0f / sqrtf(wave_sum(c[0] * c[0] + c[1] * c[1]) + 1e-6f);
+    const float ink = 1.0f / sqrtf(wave_sum(c[2] * c[2] + c[3] * c[3]) + 1e-6f);
+    const float qsc = 1.0f / sqrtf((float)HD);
+    qs[lane] = (c[0] * inq) * qsc;
+    qs[lane + 64] = (c[1] * inq) * qsc;
+    ks[lane] = c[2] * ink;
+    ks[lane + 64] = c[3] * ink;
+    if (vlane) vs[lane] = c[4];
+    tr(tid, 0, 3);
+  }
+  if (!wg_ok(smem, ok)) return false;
+  tr(tid, 256, 1);
+  if (!SYNC && tid >= 256) {
+    // gated delta rule (ssm_scan_fused_avx2, ssm.rs:378-418) on row i (lane >> 3 within the wave's
+    // 8 rows), columns j = js*16 + jj (js = lane & 7); a row's 8 column slices are adjacent lanes
+    const unsigned lane = tid & 63u, w4 = (tid >> 6) - 4, il = lane >> 3, js = lane & 7u;
+    const int i32 = (int)(w4 * 8 + il), i = quarter * 32 + i32;
+    const float decay = sc[0], beta = sc[1];
+    float kk[16], qq[16];
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float4 a4 = *reinterpret_cast<const float4*>(&ks[js * 16 + 4 * v4]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&qs[js * 16 + 4 * v4]);
+      kk[4 * v4] = a4.x; kk[4 * v4 + 1] = a4.y; kk[4 * v4 + 2] = a4.z; kk[4 * v4 + 3] = a4.w;
+      qq[4 * v4] = b4.x; qq[4 * v4 + 1] = b4.y; qq[4 * v4 + 2] = b4.z; qq[4 * v4 + 3] = b4.w;
+    }
+    const float vi = vs[i32];
+    float kvp = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      s[jj] *= decay;
+      kvp = __builtin_fmaf(s[jj], kk[jj], kvp);
+    }
+    const float kv = group8_sum(kvp);
+    const float d = (vi - kv) * beta;
+    float* S = Ly.state + (size_t)vh * HD * HD;
+    float yp = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      s[jj] = __builtin_fmaf(d, kk[jj], s[jj]);
+      co_st(S + (size_t)(js * 16 + jj) * HD + i, s[jj]);
+      yp = __builtin_fmaf(s[jj], qq[jj], yp);
+    }
+    const float yy = group8_sum(yp);
+    if (js == 0) ll_st(y + (size_t)vh * HD + i, yy, tag);
+    const float ys = wave_sum(js == 0 ? yy * yy : 0.f);
+    if (lane == 0) ll_st(yss + (size_t)vh * 16 + quarter * 4 + w4, ys, tag);
+  }
+  return true;
+}
+
+// ------------------------------------------------------------------ phase B': attention chunk
+
+// Workgroup (kv-head, chunk g) of attention.rs:56-208.  The sync wave takes the q/k/v sums of the
+// kv-head's GRP query heads, applies the q/k RMSNorm, the reference's +/+ partial RoPE on dims 0..63
+// (pairs (i, i+32), rope.rs:187-231) and q *= 1/sqrt(hd), and appends k/v when the chunk holds the
+// new position; all waves then run the online softmax over the chunk's positions and publish one
+// (m, l, o[hd]) record per query head.  pf() (the out-projection prefetch) runs after the last
+// cache read.
+template <bool SYNC, int GRP, class Pf>
+__device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, const PtkPlan& P, const PtkLayer& Ly, int w,
                                            unsigned tid, int pos, const u64* qkv, unsigned tag_q, u64* rec,
-                                           unsigned tag, const PtkErr& e) {
+                                           unsigned tag, const PtkErr& e, const Pf& pf, const TraceAt& tr) {
   constexpr int HD = 256;
   const int kvh = w / P.gmax, g = w % P.gmax;
   int chunk, gc;
   attn_chunks(P, pos, &chunk, &gc);
-  if (kvh >= P.nkv || g >= gc) return true;
+  if (kvh >= P.nkv || g >= gc) {
+    if constexpr (!SYNC) pf();
+    return wg_ok(smem, SYNC ? prior : true);
+  }
   const unsigned lane = tid & 63u, wave = tid >> 6;
   const int ctx = pos + 1, p0 = g * chunk, p1 = min(ctx, p0 + chunk);
   const bool has_new = p1 == ctx;
-  float* qs = lds_ptr<float>(smem, kLdsScratch);        // [GRP][HD]
-  float* kn = qs + GRP * HD;                            // [HD]
-  float* vn = kn + HD;                                  // [HD]
-  float* red = vn + HD;                                 // [GRP+1][4]
-  float* wm = red + (GRP + 1) * 4;                      // [8][GRP]
-  float* wl = wm + kPtkWaves * GRP;                     // [8][GRP]
-  float* wo = lds_ptr<float>(smem, 0);                  // [8][GRP][HD] in the LUT area (unused here)
-  const int half = P.rope_dim / 2;
-  const float* cs = P.rope + (size_t)pos * P.rope_dim;
-  // raw projections, one dim per thread (threads 0..255)
-  float qv[GRP];
-  float kvv = 0.f, vvv = 0.f;
-  bool ok = true;
-  if (tid < HD) {
-    const u64* a[GRP + 2];
+  float* qs = lds_ptr<float>(smem, kLdsScratch);  // [GRP][HD]
+  float* kn = qs + GRP * HD;                      // [HD]
+  float* vn = kn + HD;                            // [HD]
+  float* wm = vn + HD;                            // [8][GRP]
+  float* wl = wm + kPtkWaves * GRP;               // [8][GRP]
+  float* wo = lds_ptr<float>(smem, 0);            // [8][GRP][HD] in the table area (unused here)
+  bool ok = SYNC ? prior : true;
+  if (SYNC && ok) {
+    const int half = P.rope_dim / 2;  // 32 (checked on the host)
+    const float* cs = P.rope + (size_t)pos * P.rope_dim;
+    const float cr = cs[lane & 31u], sr = cs[half + (lane & 31u)];
+    float qn[4], kw[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      qn[m] = Ly.q_norm[lane + 64 * m];
+      kw[m] = Ly.k_norm[lane + 64 * m];
+    }
+    constexpr int N = GRP * 4 + 8;
     const int64_t kb = (int64_t)P.nq * 2 * HD;
+    u64 x[N];
+    auto addr = [&](int s, unsigned ln) -> const u64* {
+      const int d = (int)ln + 64 * (s & 3);
+      if (s < GRP * 4) return qkv + (int64_t)(kvh * GRP + s / 4) * 2 * HD + d;
+      if (s < GRP * 4 + 4) return qkv + kb + (int64_t)kvh * HD + d;
+      return qkv + kb + (int64_t)P.nkv * HD + (int64_t)kvh * HD + d;
+    };
+    ok = poll<N>(addr, [](int) { return true; }, TagC{tag_q}, x, e);
+    // q/k RMSNorm over 256 dims (attention.rs:101-119), then RoPE: the partner of dim d < 64 is lane ^ 32
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) a[gi] = qkv + (int64_t)(kvh * GRP + gi) * 2 * HD + tid;
-    a[GRP] = qkv + kb + (int64_t)kvh * HD + tid;
-    a[GRP + 1] = qkv + kb + (int64_t)P.nkv * HD + (int64_t)kvh * HD + tid;
-    u64 wv[GRP + 2];
-    ok = ll_wait<GRP + 2>(a, wv, tag_q, e);
+    for (int gi = 0; gi <= GRP; ++gi) {
+      float v[4];
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) qv[gi] = ll_val(wv[gi]);
-    kvv = ll_val(wv[GRP]);
-    vvv = ll_val(wv[GRP + 1]);
-  } else {
+      for (int m = 0; m < 4; ++m) v[m] = ll_val(x[gi * 4 + m]);
+      const float ss = wave_sum((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
+      const float in = 1.0f / sqrtf(ss / (float)HD + P.eps);
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) qv[gi] = 0.f;
+      for (int m = 0; m < 4; ++m) v[m] = (v[m] * in) * (gi < GRP ? qn[m] : kw[m]);
+      const float o = __shfl_xor(v[0], 32, 64);
+      v[0] = __builtin_fmaf(v[0], cr, o * sr);
+      float* dst = gi < GRP ? qs + gi * HD : kn;
+      const float scl = gi < GRP ? 1.0f / sqrtf((float)HD) : 1.0f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) dst[lane + 64 * m] = gi < GRP ? v[m] * scl : v[m];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vn[lane + 64 * m] = ll_val(x[GRP * 4 + 4 + m]);
+    if (has_new && ok) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        co_st(Ly.kc + ((size_t)kvh * P.max_ctx + pos) * HD + lane + 64 * m, kn[lane + 64 * m]);
+        co_st(Ly.vc + ((size_t)kvh * P.max_ctx + pos) * HD + lane + 64 * m, vn[lane + 64 * m]);
+      }
+    }
+    tr(tid, 0, 3);
   }
   if (!wg_ok(smem, ok)) return false;
-  // per-head RMSNorm over 256 dims (waves 0..3 hold the dims)
-#pragma unroll
-  for (int gi = 0; gi < GRP; ++gi) {
-    const float sq = wave_sum(qv[gi] * qv[gi]);
-    if (lane == 0 && wave < 4) red[gi * 4 + wave] = sq;
-  }
-  {
-    const float sq = wave_sum(kvv * kvv);
-    if (lane == 0 && wave < 4) red[GRP * 4 + wave] = sq;
-  }
-  lds_barrier();
-  if (tid < HD) {
-#pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      const float ssum = (red[gi * 4 + 0] + red[gi * 4 + 1]) + (red[gi * 4 + 2] + red[gi * 4 + 3]);
-      const float in = 1.0f / sqrtf(ssum / (float)HD + P.eps);
-      qs[gi * HD + tid] = (qv[gi] * in) * Ly.q_norm[tid];
-    }
-    const float ssum = (red[GRP * 4 + 0] + red[GRP * 4 + 1]) + (red[GRP * 4 + 2] + red[GRP * 4 + 3]);
-    const float in = 1.0f / sqrtf(ssum / (float)HD + P.eps);
-    kn[tid] = (kvv * in) * Ly.k_norm[tid];
-    vn[tid] = vvv;
-  }
-  lds_barrier();
-  float r1[GRP], r2[GRP];
-  float kr1 = 0.f, kr2 = 0.f;
-  if ((int)tid < half) {
-    const float c = cs[tid], sn = cs[half + tid];
-#pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      const float x1 = qs[gi * HD + tid], x2 = qs[gi * HD + tid + half];
-      r1[gi] = __builtin_fmaf(x1, c, x2 * sn);
-      r2[gi] = __builtin_fmaf(x2, c, x1 * sn);
-    }
-    const float x1 = kn[tid], x2 = kn[tid + half];
-    kr1 = __builtin_fmaf(x1, c, x2 * sn);
-    kr2 = __builtin_fmaf(x2, c, x1 * sn);
-  }
-  lds_barrier();
-  if ((int)tid < half) {
-#pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      qs[gi * HD + tid] = r1[gi];
-      qs[gi * HD + tid + half] = r2[gi];
-    }
-    kn[tid] = kr1;
-    kn[tid + half] = kr2;
-  }
-  lds_barrier();
-  const float qscale = 1.0f / sqrtf((float)HD);
-  if (tid < HD) {
-#pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) qs[gi * HD + tid] *= qscale;
-    if (has_new) {
-      co_st(Ly.kc + ((size_t)kvh * P.max_ctx + pos) * HD + tid, kn[tid]);
-      co_st(Ly.vc + ((size_t)kvh * P.max_ctx + pos) * HD + tid, vn[tid]);
-    }
-  }
-  lds_barrier();
-  // online softmax over this wave's positions; lane holds dims 4*lane .. 4*lane+3
+  // online softmax over this wave's positions (attention.rs:149-199); lane holds dims 4*lane..+3
   float m[GRP], l[GRP];
   float4 o[GRP], q4[GRP];
 #pragma unroll
@@ -692,16 +869,13 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, const PtkPlan& P
   }
   const float* kb = Ly.kc + (size_t)kvh * P.max_ctx * HD;
   const float* vb = Ly.vc + (size_t)kvh * P.max_ctx * HD;
-  auto ld4 = [&](const float* p) {
-    return make_float4(co_ld(p), co_ld(p + 1), co_ld(p + 2), co_ld(p + 3));
-  };
   auto loadkv = [&](int p, float4& k4, float4& v4) {
     if (p == pos) {
       k4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
       v4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
     } else {
-      k4 = ld4(kb + (size_t)p * HD + 4 * lane);
-      v4 = ld4(vb + (size_t)p * HD + 4 * lane);
+      k4 = co_ld4(kb + (size_t)p * HD + 4 * lane);
+      v4 = co_ld4(vb + (size_t)p * HD + 4 * lane);
     }
   };
   int p = p0 + (int)wave;
@@ -716,15 +890,19 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, const PtkPlan& P
     va = vb1;
     kb1 = kc;
     vb1 = vc;
+    float dp[GRP];
 #pragma unroll
     for (int gi = 0; gi < GRP; ++gi) {
-      float dp = q4[gi].x * k4.x;
-      dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
-      dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
-      dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
-      const float score = wave_sum(dp);
+      float t = q4[gi].x * k4.x;
+      t = __builtin_fmaf(q4[gi].y, k4.y, t);
+      t = __builtin_fmaf(q4[gi].z, k4.z, t);
+      dp[gi] = __builtin_fmaf(q4[gi].w, k4.w, t);
+    }
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      const float score = wave_sum(dp[gi]);
       const float mn = fmaxf(m[gi], score);
-      const float al = expf(m[gi] - mn), be = expf(score - mn);
+      const float al = __expf(m[gi] - mn), be = __expf(score - mn);
       l[gi] = l[gi] * al + be;
       o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
       o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
@@ -733,6 +911,8 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, const PtkPlan& P
       m[gi] = mn;
     }
   }
+  tr(tid, 64, 1);
+  if constexpr (!SYNC) pf();  // no cache read follows
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {
     if (lane == 0) {
@@ -742,164 +922,130 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, const PtkPlan& P
     *reinterpret_cast<float4*>(&wo[(wave * GRP + gi) * HD + 4 * lane]) = o[gi];
   }
   lds_barrier();
-  // the KV append is complete before the chunk records become visible
-  wait_stores();
-  // merge the 8 waves (a wave without positions has l = 0) and publish each q-head's record
-  if (tid < HD) {
-#pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      float M = -INFINITY;
-      for (int wv = 0; wv < kPtkWaves; ++wv) M = fmaxf(M, wm[wv * GRP + gi]);
-      float L = 0.f, O = 0.f;
-      for (int wv = 0; wv < kPtkWaves; ++wv) {
-        const float ex = wl[wv * GRP + gi] > 0.f ? expf(wm[wv * GRP + gi] - M) : 0.f;
-        L = __builtin_fmaf(wl[wv * GRP + gi], ex, L);
-        O = __builtin_fmaf(wo[(wv * GRP + gi) * HD + tid], ex, O);
-      }
-      u64* rc = rec + ((size_t)(kvh * GRP + gi) * P.gmax + g) * (2 + HD);
-      if (tid == 0) {
-        ll_st(rc, M, tag);
-        ll_st(rc + 1, L, tag);
-      }
-      ll_st(rc + 2 + tid, O, tag);
+  // merge the 8 waves (a wave without positions has l = 0): the per-(wave, head) rescale factors
+  // once, then every output dim, and publish each query head's record
+  float* wx = wl + kPtkWaves * GRP;  // [8][GRP] rescale factors, then [GRP] M and [GRP] L
+  if (tid < (unsigned)GRP) {
+    const int gi = (int)tid;
+    float M = -INFINITY;
+    for (int wv = 0; wv < kPtkWaves; ++wv) M = fmaxf(M, wm[wv * GRP + gi]);
+    float L = 0.f;
+    for (int wv = 0; wv < kPtkWaves; ++wv) {
+      const float ex = wl[wv * GRP + gi] > 0.f ? __expf(wm[wv * GRP + gi] - M) : 0.f;
+      wx[wv * GRP + gi] = ex;
+      L = __builtin_fmaf(wl[wv * GRP + gi], ex, L);
     }
+    wx[kPtkWaves * GRP + gi] = M;
+    wx[kPtkWaves * GRP + GRP + gi] = L;
   }
-  lds_barrier();  // wo lives in the LUT area
-  return true;
-}
-
-// R'': merge the chunk records of each q-head and apply the output gate (attention.rs:189-203):
-// ao[h*hd + d] = (O/L) * sigmoid(gate).  Wave v handles outputs j0+v, j0+v+8, ...; lane = chunk.
-template <class Pf>
-__device__ __forceinline__ bool phase_attn_merge(unsigned char* smem, const PtkPlan& P, int w, unsigned tid, int pos,
-                                                 const u64* rec, unsigned tag_r, const u64* qkv, unsigned tag_q,
-                                                 u64* ao, unsigned tag, const PtkErr& e, const Pf& pf) {
-  constexpr int HD = 256;
-  int chunk, gc;
-  attn_chunks(P, pos, &chunk, &gc);
-  int j0, j1;
-  even_split(w, P.G, P.nq * HD, &j0, &j1);
-  const unsigned lane = tid & 63u, wave = tid >> 6;
-  bool ok = true;
-  for (int j = j0 + (int)wave; j < j1 && ok; j += kPtkWaves) {
-    const int h = j / HD, d = j % HD;
-    float mv = -INFINITY, lv = 0.f, ov = 0.f, gate = 0.f;
-    if ((int)lane < gc) {
-      const u64* r = rec + ((size_t)h * P.gmax + lane) * (2 + HD);
-      const u64* a[3] = {r, r + 1, r + 2 + d};
-      u64 wv[3];
-      ok = ll_wait<3>(a, wv, tag_r, e);
-      mv = ll_val(wv[0]);
-      lv = ll_val(wv[1]);
-      ov = ll_val(wv[2]);
+  lds_barrier();
+  for (int idx = (int)tid; idx < GRP * HD; idx += kPtkThreads) {
+    const int gi = idx / HD, d = idx % HD;
+    float O = 0.f;
+    for (int wv = 0; wv < kPtkWaves; ++wv) O = __builtin_fmaf(wo[(wv * GRP + gi) * HD + d], wx[wv * GRP + gi], O);
+    u64* rc = rec + ((size_t)(kvh * GRP + gi) * P.gmax + g) * (2 + HD);
+    if (d == 0) {
+      ll_st(rc, wx[kPtkWaves * GRP + gi], tag);
+      ll_st(rc + 1, wx[kPtkWaves * GRP + GRP + gi], tag);
     }
-    if (lane == 0 && ok) ok = ll_wait1(qkv + (int64_t)(h * 2 + 1) * HD + d, gate, tag_q, e);
-    ok = __builtin_amdgcn_readfirstlane((int)ok) && __all(ok);
-    const float M = wave_max(mv);
-    const float ex = (int)lane < gc ? expf(mv - M) : 0.f;
-    const float L = wave_sum(lv * ex), O = wave_sum(ov * ex);
-    gate = __shfl(gate, 0, 64);
-    if (lane == 0 && ok) ll_st(ao + j, (O * (1.0f / L)) * sigmoidf_(gate), tag);
+    ll_st(rc + 2 + d, O, tag);
   }
-  if (!wg_ok(smem, ok)) return false;
-  pf();
+  tr(tid, 64, 2);
   return true;
 }
 
 // ------------------------------------------------------------------ phase L: lm_head + argmax
 
-// Full K per workgroup: rows [rb0, rb1) of the vocabulary, tile by tile (LUT per tile), with the
-// next tile's weights in flight; logits = inv_rms(h) * W (h * output_norm) (forward.rs:332-341),
-// the statistics accumulated while staging.
-template <int U>
-__device__ __forceinline__ bool phase_lm(unsigned char* smem, const PtkPlan& P, const PtkRun& r, int i, int w,
-                                         unsigned tid, const u64* h_fin, unsigned tag_h, u64* cand_v, u64* cand_i,
-                                         unsigned tag) {
+// Full K per workgroup: rows [rb0, rb1) of the vocabulary, tile by tile (one table per tile), on
+// weights requested one tile ahead; logits = inv_rms(h) * W (h * output_norm) (forward.rs:332-341).
+// The tile loop is unrolled (NTH bounds the tile count), so that no loaded value is carried around a
+// loop (a phi, resolved with register copies that wait for the loads).
+template <bool SYNC, int NTH, int U_LM, int U>
+__device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const PtkPlan& P, const PtkRun& r, int i, int w,
+                                         unsigned tid, const u64* h_fin, unsigned tag_h, WRegs<U>& cur, u64* cand_v,
+                                         u64* cand_i, unsigned tag) {
   const PtkErr& e = r.err;
-  const unsigned lane = tid & 63u, wave = tid >> 6;
+  const unsigned lane = tid & 63u, wave = tid >> 6, cw = wave - 1;
   int rb0, rb1;
   even_split(w, P.G, P.nrb_v, &rb0, &rb1);
-  float acc[U];
+  float acc[U_LM];
 #pragma unroll
-  for (int m = 0; m < U; ++m) acc[m] = 0.f;
+  for (int m = 0; m < U_LM; ++m) acc[m] = 0.f;
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
-  WRegs<U> cur;
-  {
-    Assign a0;
-    a0.t = 0;
-    a0.rb0 = rb0;
-    a0.rb1 = rb1;
-    gemv_prefetch(P.w_lm, P.nT_h, a0, wave, lane, cur);
-  }
-  float ssq = 0.f;  // this thread's share of sum(h^2): the output norm's statistics
-  for (int t = 0; t < P.nT_h; ++t) {
-    SrcNormedLL src{h_fin, tag_h, P.output_norm, P.H, nullptr};
-    float sq;
-    const bool ok = src.stage(xs, t, tid, e, sq);
-    ssq += sq;
+  float* red = lds_ptr<float>(smem, kLdsRed);
+  float ssq = 0.f;  // sync wave: this lane's share of sum(h^2), the output norm's statistics
+  bool ok = SYNC ? prior : true;
+  if constexpr (!SYNC) gemv_prefetch<U_LM>(P.w_lm, NTH, 0, rb0, rb1, tid, cur);
+#pragma unroll
+  for (int t = 0; t < NTH; ++t) {  // NTH is the tile count itself (checked on the host)
+    if (SYNC && ok) {
+      SrcNormedLL src{h_fin, tag_h, P.output_norm, P.H, nullptr};
+      float sq;
+      ok = src.stage(xs, t, lane, e, sq);
+      ssq += sq;
+    }
     if (!wg_ok(smem, ok)) return false;
     build_lut<kPtkThreads>(lut, xs, tid);
     lds_barrier();
-    WRegs<U> nxt;
-    const bool more = t + 1 < P.nT_h;
-    {
-      Assign an;
-      an.t = more ? t + 1 : t;
-      an.rb0 = rb0;
-      an.rb1 = more ? rb1 : rb0;
-      gemv_prefetch(P.w_lm, P.nT_h, an, wave, lane, nxt);
-    }
-    unsigned c[16];
-    make_pos_consts(lane, c);
+    if constexpr (!SYNC) {
+      unsigned c[16];
+      make_pos_consts(lane, c);
 #pragma unroll
-    for (int m = 0; m < U; ++m) {
-      const int rb = rb0 + (int)wave + kPtkWaves * m;
-      if (rb < rb1) acc[m] += unit_dot(cur.u[m], c);
-    }
-#pragma unroll
-    for (int m = 0; m < U; ++m) cur.u[m] = nxt.u[m];
-    lds_barrier();
-  }
-  // logits = inv_rms(h) * W (h * output_norm), and this workgroup's (max, first index)
-  const float inv = 1.0f / sqrtf(block_sum512(ssq, lds_ptr<float>(smem, kLdsRed), tid) / (float)P.H + P.eps);
-  float bv = -INFINITY;
-  int bi = 0x7FFFFFFF;
-  const bool last = i == r.n_tok - 1;
-#pragma unroll
-  for (int m = 0; m < U; ++m) {
-    const int rb = rb0 + (int)wave + kPtkWaves * m;
-    const int row = rb * kRowBlock + (int)lane;
-    if (rb < rb1 && row < P.vocab) {
-      const float lg = acc[m] * inv;
-      if (r.want_logits) {
-        if (P.logits_all) P.logits_all[(size_t)i * P.vocab + row] = lg;
-        if (last) P.logits[row] = lg;
+      for (int m = 0; m < U_LM; ++m) {
+        const int rb = rb0 + (int)cw + kCW * m;
+        if (rb < rb1) acc[m] += unit_dot(cur.u[m], c);
       }
-      if (am_better(lg, row, bv, bi)) {
-        bv = lg;
-        bi = row;
-      }
+      // the next tile (after the last one, slots without row-blocks: one cache line)
+      gemv_prefetch<U_LM>(P.w_lm, NTH, t + 1 < NTH ? t + 1 : t, rb0, t + 1 < NTH ? rb1 : rb0, tid, cur);
     }
   }
-  wave_argmax(bv, bi);
-  float* sv = lds_ptr<float>(smem, kLdsScratch + 64);
-  int* si = lds_ptr<int>(smem, kLdsScratch + 128);
-  if (lane == 0) {
-    sv[wave] = bv;
-    si[wave] = bi;
+  if constexpr (SYNC) {
+    const float s = wave_sum(ssq);
+    if (tid == 0) red[32] = 1.0f / sqrtf(s / (float)P.H + P.eps);
   }
   lds_barrier();
-  if (tid == 0) {
-    for (int wv = 1; wv < kPtkWaves; ++wv)
-      if (am_better(sv[wv], si[wv], bv, bi)) {
-        bv = sv[wv];
-        bi = si[wv];
+  const float inv = red[32];
+  float* sv = lds_ptr<float>(smem, kLdsScratch);
+  int* si = lds_ptr<int>(smem, kLdsScratch + 64);
+  if constexpr (!SYNC) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    const bool last = i == r.n_tok - 1;
+#pragma unroll
+    for (int m = 0; m < U_LM; ++m) {
+      const int rb = rb0 + (int)cw + kCW * m;
+      const int row = rb * kRowBlock + (int)lane;
+      if (rb < rb1 && row < P.vocab) {
+        const float lg = acc[m] * inv;
+        if (r.want_logits) {
+          if (P.logits_all) P.logits_all[(size_t)i * P.vocab + row] = lg;
+          if (last) P.logits[row] = lg;
+        }
+        if (am_better(lg, row, bv, bi)) {
+          bv = lg;
+          bi = row;
+        }
+      }
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) {
+      sv[cw] = bv;
+      si[cw] = bi;
+    }
+  }
+  lds_barrier();
+  if (SYNC && tid == 0) {
+    float bv = sv[0];
+    int bi = si[0];
+    for (int k = 1; k < kCW; ++k)
+      if (am_better(sv[k], si[k], bv, bi)) {
+        bv = sv[k];
+        bi = si[k];
       }
     ll_st(cand_v + w, bv, tag);
     ll_st(cand_i + w, __int_as_float(bi), tag);
   }
-  lds_barrier();
   return true;
 }
 
@@ -916,27 +1062,233 @@ __device__ __forceinline__ Assign asg_at(unsigned char* smem, int k) {
 }
 __device__ __forceinline__ bool asg_lead(unsigned char* smem, int k) { return lds_ptr<int>(smem, kLdsAsg)[4 * k + 3] != 0; }
 
-// Completion time of phase `ph` of token i on this workgroup (tracing runs only).
-__device__ __forceinline__ void ptk_mark(const PtkRun& r, const PtkPlan& P, int i, int ph, int w, unsigned tid) {
-  if (r.trace && tid == 0) glb(r.trace)[((size_t)i * P.ppt + ph) * P.G + w] = __builtin_amdgcn_s_memrealtime();
+
+// Template bounds: NTH K tiles of hidden (DeltaNet / q,k,v / SwiGLU sums), GRP query heads per kv
+// head, U_* row-block slots per compute wave of the in-proj, out-proj, gate/up, down and lm_head
+// phases, QR terms per lane of the residual sums, MF ffn channels per lane of the SwiGLU phase, MR
+// rows per lane of the q/k/v sums, MO attention outputs per workgroup of the chunk merge (all
+// checked on the host).
+#define DZ_PTK_TPARAMS int NTH, int GRP, int U_IN, int U_OUT, int U_GU, int U_DN, int U_LM, int QR, int MF, int MR, int MO
+
+// The token loop of one role: SYNC for wave 0, else for a compute wave.  Both roles walk the same
+// phases and meet at the same barriers (each phase function holds both roles' barriers); a role's
+// registers (the sync wave's poll words, a compute wave's weights) exist only in its own copy.
+template <bool SYNC, DZ_PTK_TPARAMS>
+__device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
+  const PtkPlan P0 = plan_view(r.plan);
+  const PtkErr& e = r.err;
+  const int w0 = (int)blockIdx.x, G = P0.G;
+  const PtkOffsets& O = P0.off;
+  const int64_t ld_in_h = (int64_t)P0.nrb_h * kRowBlock;
+  const int64_t cand_off = ld_in_h;  // token region: h_emb [ld_in_h], cand_v [G], cand_i [G]
+  // a compute wave's weight registers: each GEMV phase's weights from the phase that requested them
+  // to the phase that uses them
+  constexpr int UW = U_IN > U_OUT ? (U_IN > U_GU ? (U_IN > U_DN ? U_IN : U_DN) : (U_GU > U_DN ? U_GU : U_DN))
+                                  : (U_OUT > U_GU ? (U_OUT > U_DN ? U_OUT : U_DN) : (U_GU > U_DN ? U_GU : U_DN));
+  constexpr int UWL = UW > U_LM ? UW : U_LM;
+  WRegs<UWL> wn;
+  float sreg[16];  // DeltaNet state rows (waves 4..7), from the in-projection phase to the DeltaNet phase
+  // `ok` carries the sync wave's outcome from its poll phases to the next workgroup barrier
+  bool ok = true;
+  int seq = 0;     // hand-off points passed (sync_point)
+  int dn_seq = 0;  // DeltaNet phases passed (the compute waves' conv-input arrivals count 3 per phase)
+  for (int i = 0; i < r.n_tok; ++i) {
+    const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
+    const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);
+    const int pos = r.pos0 + i;
+    u64* tokreg = ll_region(P0, par, P0.n_layers);
+    const u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
+    if constexpr (SYNC) {
+      ok = s_select(P0, r, i, w0, threadIdx.x, tokreg, prev_tok + cand_off, prev_tok + cand_off + G,
+                    tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos);
+      ptk_mark(r, P0, i, 0, w0, threadIdx.x, 0);
+    }
+    sync_point<SYNC>(smem, seq);
+    const u64* h_in = tokreg;
+    unsigned tag_h = tb;
+    for (int l = 0; l < P0.n_layers; ++l) {
+      // opaque copies of the thread index, the workgroup index and the plan's dimensions: values
+      // derived from them are recomputed in each layer instead of being hoisted out of the loops
+      // (and kept live, or spilled, for the whole kernel)
+      unsigned tid = threadIdx.x;
+      asm volatile("" : "+v"(tid));
+      PtkPlan P = P0;
+      int w = w0;
+#define DZ_OPQ(f) f = opaque_s(f)
+      DZ_OPQ(w); DZ_OPQ(P.G); DZ_OPQ(P.H); DZ_OPQ(P.F); DZ_OPQ(P.nT_h); DZ_OPQ(P.nT_f); DZ_OPQ(P.nrb_h);
+      DZ_OPQ(P.nrb_gu); DZ_OPQ(P.nrb_v); DZ_OPQ(P.gmax); DZ_OPQ(P.max_ctx); DZ_OPQ(P.nkh); DZ_OPQ(P.nvh);
+      DZ_OPQ(P.qkvd); DZ_OPQ(P.inner); DZ_OPQ(P.off_z); DZ_OPQ(P.off_a); DZ_OPQ(P.off_b); DZ_OPQ(P.nq);
+      DZ_OPQ(P.nkv); DZ_OPQ(P.rope_dim);
+#undef DZ_OPQ
+      const PtkLayer Ly = layer_at(P, l);
+      u64* R = ll_region(P, par, l);
+      const unsigned t0 = tb + (unsigned)Ly.ph0;
+      const int64_t ld_in = (int64_t)Ly.nrb_in * kRowBlock;
+      const Assign a_out = asg_at(smem, 2 + Ly.attn);
+      const Assign a_gu = asg_at(smem, 4);
+      const Assign a_dn = asg_at(smem, 5);
+      // this layer's in-projection weights, once the sync wave has polled the previous residual sum
+      // (or the token).  Every prefetch is issued in the block that uses it: a loaded value carried
+      // around a loop becomes a phi, resolved with register copies that wait for the loads.
+      // The DeltaNet state rows go first (every layer loads: an attention layer reads 16 words of one
+      // cache line, so that no phi forms), then the in-projection.
+      if constexpr (!SYNC) {
+        sync_wait(smem, seq);
+        dn_state_load(P, Ly, w, tid, sreg);
+        const Assign a = asg_at(smem, Ly.attn);
+        gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
+      }
+      auto nopf = []() {};
+      // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream)
+      {
+        const Assign a = asg_at(smem, Ly.attn);
+        SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
+        // (the next weights depend on the layer kind: requested in its branch)
+        if (!gemv_phase<SYNC, U_IN>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid, e, nopf,
+                                    TraceAt{&r, &P, i, Ly.ph0, w}))
+          return;
+      }
+      // R0: in-projection sums (q|k|v|z|alpha|beta of a DeltaNet layer, q|gate|k|v of an attention layer)
+      if constexpr (SYNC) {
+        ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 0, 1);
+        ok = s_qkv<NTH, MR>(P, Ly, w, tid, R + O.sst_in, R + O.pin, t0, R + O.qkv, t0 + 1, e);
+        ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 0);
+      }
+      sync_point<SYNC>(smem, seq);
+      unsigned tag_o;
+      int k;
+      if (!Ly.attn) {
+        // B: DeltaNet
+        ++dn_seq;
+        if (!phase_dn<SYNC>(smem, ok, P, Ly, lds_ptr<int>(smem, kLdsRing)[l], w, tid, pos, R + O.qkv, t0 + 1, R + O.y,
+                            R + O.zs, R + O.yss, t0 + 2, e, sreg, dn_seq, TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+          return;
+        if constexpr (!SYNC) {
+          ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
+          // the out-projection weights: the sync wave's next polls are this GEMV's own inputs
+          gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
+        }
+        // C: out-proj
+        SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
+        if (!gemv_phase<SYNC, U_OUT>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e, nopf,
+                                     TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
+          return;
+        tag_o = t0 + 3;
+        k = 4;
+      } else {
+        // B': attention chunks
+        if (!phase_attn<SYNC, GRP>(smem, ok, P, Ly, w, tid, pos, R + O.qkv, t0 + 1, R + O.rec, t0 + 2, e, nopf,
+                                   TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+          return;
+        if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 64);
+        // R'': chunk merge and output gate
+        if constexpr (SYNC) {
+          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0, 1);
+          ok = s_merge<MO>(P, w, tid, pos, R + O.rec, t0 + 2, R + O.qkv, t0 + 1, R + O.ao, t0 + 3, e,
+                           TraceAt{&r, &P, i, Ly.ph0 + 3, w});
+          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0);
+        }
+        sync_point<SYNC>(smem, seq);
+        // the out-projection weights (after the merge's polls)
+        if constexpr (!SYNC) {
+          sync_wait(smem, seq);
+          gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
+        }
+        // C': out-proj
+        SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
+        if (!gemv_phase<SYNC, U_OUT>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e, nopf,
+                                     TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
+          return;
+        tag_o = t0 + 4;
+        k = 5;
+      }
+      // R1: h_mid = h + out-proj.  The sync wave's conv ring / KV cache stores of this layer are
+      // complete before anything it publishes from here on.
+      if constexpr (SYNC) {
+        wait_stores();
+        ptk_mark(r, P, i, Ly.ph0 + k, w, tid, 0, 1);
+        ok = s_resid<QR>(P, w, tid, h_in, tag_h, R + O.po, Ly.nt_out, ld_in_h, tag_o, R + O.hmid, t0 + k, e);
+        ptk_mark(r, P, i, Ly.ph0 + k, w, tid, 0);
+      }
+      sync_point<SYNC>(smem, seq);
+      // the gate/up weights (after R1's polls; issued once after the layer kinds' branches join, so
+      // that no phi of two loads forms)
+      if constexpr (!SYNC) {
+        sync_wait(smem, seq);
+        gemv_prefetch<U_GU>(Ly.w_gu, P.nT_h, a_gu.t, a_gu.rb0, a_gu.rb1, tid, wn);
+      }
+      // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
+      {
+        SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};
+        if (!gemv_phase<SYNC, U_GU>(smem, ok, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
+                                    (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nopf, TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
+          return;
+      }
+      // R2: SwiGLU
+      if constexpr (SYNC) {
+        ptk_mark(r, P, i, Ly.ph0 + k + 2, w, tid, 0, 1);
+        ok = s_swiglu<NTH, MF>(P, w, tid, R + O.sst_mid, R + O.pgu, t0 + k + 1, R + O.sw, t0 + k + 2, e);
+        ptk_mark(r, P, i, Ly.ph0 + k + 2, w, tid, 0);
+      }
+      sync_point<SYNC>(smem, seq);
+      // the down weights (after R2's polls)
+      if constexpr (!SYNC) {
+        sync_wait(smem, seq);
+        gemv_prefetch<U_DN>(Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1, tid, wn);
+      }
+      // E: down
+      {
+        SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
+        if (!gemv_phase<SYNC, U_DN>(smem, ok, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e, nopf,
+                                    TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
+          return;
+      }
+      // R3: h = h_mid + down
+      if constexpr (SYNC) {
+        ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 0, 1);
+        ok = s_resid<QR>(P, w, tid, R + O.hmid, t0 + k, R + O.pd, P.nT_f, ld_in_h, t0 + k + 3, R + O.h, t0 + k + 4, e);
+        ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 0);
+      }
+      sync_point<SYNC>(smem, seq);
+      h_in = R + O.h;
+      tag_h = t0 + k + 4;
+    }
+    // L: lm_head + argmax candidates (its first tile's weights once R3's polls are done)
+    if constexpr (!SYNC) sync_wait(smem, seq);
+    if (!phase_lm<SYNC, NTH, U_LM>(smem, ok, P0, r, i, w0, threadIdx.x, h_in, tag_h, wn, tokreg + cand_off,
+                                   tokreg + cand_off + G, tb + (unsigned)P0.ph_l))
+      return;
+    if constexpr (SYNC) ptk_mark(r, P0, i, P0.ph_l, w0, threadIdx.x, 0);
+  }
+  // greedy pick after the last token, published as toklog[pos0 + n_tok] (workgroup 0)
+  if constexpr (SYNC) {
+    if (w0 == 0) {
+      const int i = r.n_tok;
+      const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
+      const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);
+      const u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
+      bool pk = true;
+      const int tok = s_pick(P0, threadIdx.x, prev_tok + cand_off, prev_tok + cand_off + G,
+                             tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, e, pk);
+      if (threadIdx.x == 0 && pk) P0.toklog[r.pos0 + r.n_tok] = tok;
+    }
+  }
 }
 
-// NTH / NTO / NTF bound the K-tile counts of hidden, mixer output and ffn; U_* are the row-block
-// slots per wave of the in-proj, out-proj, gate/up, down and lm_head phases.
-template <int NTH, int NTO, int NTF, int GRP, int U_IN, int U_OUT, int U_GU, int U_DN, int U_LM>
+template <DZ_PTK_TPARAMS>
 __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
   extern __shared__ __align__(16) unsigned char smem[];
   const PtkPlan P = plan_view(r.plan);
-  const PtkErr& e = r.err;
-  const unsigned tid = threadIdx.x, lane = tid & 63u;
+  const unsigned tid = threadIdx.x;
   const int w = (int)blockIdx.x, G = P.G;
-  if (tid == 0) *lds_ptr<int>(smem, kLdsFlag) = 0;
+  if (tid < 4) lds_ptr<int>(smem, kLdsFlag)[tid] = 0;
   // this workgroup's GEMV assignments per matrix kind (0/1: in-proj of a DeltaNet/attention layer,
   // 2/3: out-proj, 4: gate/up, 5: down) and the conv ring bases, fixed for the launch
   if (tid < 6) {
     const int k = (int)tid;
-    const int T = k < 2 ? P.nT_h : k < 4 ? P.nt_out_k[k - 2] : k == 4 ? P.nT_h : P.nT_f;
-    const int nrb = k < 2 ? P.nrb_in_k[k] : k < 4 ? P.nrb_h : k == 4 ? P.nrb_gu : P.nrb_h;
+    // (selects, not indexing: a thread-dependent index into the plan would put it in scratch memory)
+    const int T = k < 2 ? P.nT_h : k == 2 ? P.nt_out_k[0] : k == 3 ? P.nt_out_k[1] : k == 4 ? P.nT_h : P.nT_f;
+    const int nrb = k == 0 ? P.nrb_in_k[0] : k == 1 ? P.nrb_in_k[1] : k < 4 ? P.nrb_h : k == 4 ? P.nrb_gu : P.nrb_h;
     const Assign a = gemv_assign(w, G, T, nrb);
     int* q = lds_ptr<int>(smem, kLdsAsg) + 4 * k;
     q[0] = a.t;
@@ -949,165 +1301,12 @@ __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
     lds_ptr<int>(smem, kLdsRing)[l] = t->attn ? 0 : *glb(t->ring_base);
   }
   lds_barrier();
-  const PtkOffsets& O = P.off;
-  const int64_t ld_in_h = (int64_t)P.nrb_h * kRowBlock;
-  const int64_t cand_off = ld_in_h;  // token region: h_emb [ld_in_h], cand_v [G], cand_i [G]
-  // one register set carries the next matrix phase's weights from the phase that requested them
-  // to the phase that uses them (their live ranges never overlap)
-  constexpr int UW = U_IN > U_OUT ? (U_IN > U_GU ? (U_IN > U_DN ? U_IN : U_DN) : (U_GU > U_DN ? U_GU : U_DN))
-                                  : (U_OUT > U_GU ? (U_OUT > U_DN ? U_OUT : U_DN) : (U_GU > U_DN ? U_GU : U_DN));
-  WRegs<UW> wn;
-  const unsigned wave = tid >> 6;
-  for (int i = 0; i < r.n_tok; ++i) {
-    const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P.ppt;
-    const int par = (int)((r.tag0 / (unsigned)P.ppt + (unsigned)i) & 1u);
-    const int pos = r.pos0 + i;
-    u64* tokreg = ll_region(P, par, P.n_layers);
-    const u64* prev_tok = ll_region(P, par ^ 1, P.n_layers);
-    int tok;
-    // weights of the next matrix phase are requested right after a phase's own polls
-    auto pf_in = [&](int l) {
-      return [&, l]() {
-        const PtkLayer Ln = layer_at(P, l);
-        gemv_prefetch(Ln.w_in, P.nT_h, asg_at(smem, Ln.attn), wave, lane, wn);
-      };
-    };
-    if (!phase_select(smem, P, r, i, w, tid, tokreg, prev_tok + cand_off, prev_tok + cand_off + G,
-                      tb - (unsigned)P.ppt + (unsigned)P.ph_l, tb, pos, tok, pf_in(0)))
-      return;
-    ptk_mark(r, P, i, 0, w, tid);
-    const u64* h_in = tokreg;
-    unsigned tag_h = tb;
-    for (int l = 0; l < P.n_layers; ++l) {
-      // an opaque copy of the thread index: values derived from it are recomputed in each layer
-      // instead of being hoisted out of the loops (and kept live, or spilled, for the whole kernel)
-      unsigned tid = threadIdx.x;
-      asm volatile("" : "+v"(tid));
-      const unsigned lane = tid & 63u, wave = tid >> 6;
-      const PtkLayer Ly = layer_at(P, l);
-      u64* R = ll_region(P, par, l);
-      const unsigned t0 = tb + (unsigned)Ly.ph0;
-      const int64_t ld_in = (int64_t)Ly.nrb_in * kRowBlock;
-      const Assign a_out = asg_at(smem, 2 + Ly.attn);
-      auto pf_out = [&]() { gemv_prefetch(Ly.w_out, Ly.nt_out, a_out, wave, lane, wn); };
-      // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream)
-      {
-        const Assign a = asg_at(smem, Ly.attn);
-        SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
-        if (!gemv_phase(smem, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid, e)) return;
-        ptk_mark(r, P, i, Ly.ph0, w, tid);
-      }
-      unsigned tag_o;
-      int k;
-      if (!Ly.attn) {
-        // B: DeltaNet (then C's weights)
-        if (!phase_deltanet<NTH>(smem, P, Ly, lds_ptr<int>(smem, kLdsRing)[l], w, tid, pos, R + O.sst_in, R + O.pin,
-                                 t0, R + O.y, R + O.zs, R + O.yss, t0 + 1, e, pf_out))
-          return;
-        ptk_mark(r, P, i, Ly.ph0 + 1, w, tid);
-        // C: out-proj
-        SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 1, Ly.ssm_norm, P.inner};
-        if (!gemv_phase(smem, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 2, tid, e)) return;
-        ptk_mark(r, P, i, Ly.ph0 + 2, w, tid);
-        tag_o = t0 + 2;
-        k = 3;
-      } else {
-        if (!phase_qkv<NTH>(smem, P, Ly, w, tid, R + O.sst_in, R + O.pin, t0, R + O.qkv, t0 + 1, e)) return;
-        ptk_mark(r, P, i, Ly.ph0 + 1, w, tid);
-        if (!phase_attn<GRP>(smem, P, Ly, w, tid, pos, R + O.qkv, t0 + 1, R + O.rec, t0 + 2, e)) return;
-        ptk_mark(r, P, i, Ly.ph0 + 2, w, tid);
-        if (!phase_attn_merge(smem, P, w, tid, pos, R + O.rec, t0 + 2, R + O.qkv, t0 + 1, R + O.ao, t0 + 3, e, pf_out))
-          return;
-        ptk_mark(r, P, i, Ly.ph0 + 3, w, tid);
-        SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
-        if (!gemv_phase(smem, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e)) return;
-        ptk_mark(r, P, i, Ly.ph0 + 4, w, tid);
-        tag_o = t0 + 4;
-        k = 5;
-      }
-      // R1: h_mid = h + out-proj (then D's weights)
-      const Assign a_gu = asg_at(smem, 4);
-      auto pf_gu = [&]() { gemv_prefetch(Ly.w_gu, P.nT_h, a_gu, wave, lane, wn); };
-      if (!phase_resid<NTO>(smem, P, w, tid, h_in, tag_h, R + O.po, Ly.nt_out, ld_in_h, tag_o, R + O.hmid, t0 + k, e,
-                            pf_gu))
-        return;
-      ptk_mark(r, P, i, Ly.ph0 + k, w, tid);
-      // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
-      {
-        SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};
-        if (!gemv_phase(smem, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu, (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1,
-                        tid, e))
-          return;
-        ptk_mark(r, P, i, Ly.ph0 + k + 1, w, tid);
-      }
-      // R2: SwiGLU (then E's weights)
-      const Assign a_dn = asg_at(smem, 5);
-      auto pf_dn = [&]() { gemv_prefetch(Ly.w_dn, P.nT_f, a_dn, wave, lane, wn); };
-      if (!phase_swiglu<NTH>(smem, P, w, tid, R + O.sst_mid, R + O.pgu, t0 + k + 1, R + O.sw, t0 + k + 2, e, pf_dn))
-        return;
-      ptk_mark(r, P, i, Ly.ph0 + k + 2, w, tid);
-      // E: down
-      {
-        SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
-        if (!gemv_phase(smem, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e)) return;
-        ptk_mark(r, P, i, Ly.ph0 + k + 3, w, tid);
-      }
-      // R3: h = h_mid + down (then the next layer's in-proj weights; none after the last layer)
-      auto pf_next = [&]() {
-        const bool more = l + 1 < P.n_layers;
-        const PtkLayer Ln = layer_at(P, more ? l + 1 : l);
-        Assign an = asg_at(smem, Ln.attn);
-        if (!more) an.rb1 = an.rb0;
-        gemv_prefetch(Ln.w_in, P.nT_h, an, wave, lane, wn);
-      };
-      if (!phase_resid<NTF>(smem, P, w, tid, R + O.hmid, t0 + k, R + O.pd, P.nT_f, ld_in_h, t0 + k + 3, R + O.h,
-                            t0 + k + 4, e, pf_next))
-        return;
-      ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid);
-      h_in = R + O.h;
-      tag_h = t0 + k + 4;
-    }
-    // L: lm_head + argmax candidates
-    if (!phase_lm<U_LM>(smem, P, r, i, w, tid, h_in, tag_h, tokreg + cand_off, tokreg + cand_off + G,
-                        tb + (unsigned)P.ph_l))
-      return;
-    ptk_mark(r, P, i, P.ph_l, w, tid);
-    (void)tok;
-  }
-  // greedy pick after the last token, published as toklog[pos0 + n_tok] (workgroup 0 only)
-  if (w == 0) {
-    const int i = r.n_tok;
-    const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P.ppt;
-    const int par = (int)((r.tag0 / (unsigned)P.ppt + (unsigned)i) & 1u);
-    const u64* prev_tok = ll_region(P, par ^ 1, P.n_layers);
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    bool ok = true;
-    if ((int)tid < G) {
-      const u64* a[2] = {prev_tok + cand_off + tid, prev_tok + cand_off + G + tid};
-      u64 wv[2];
-      ok = ll_wait<2>(a, wv, tb - (unsigned)P.ppt + (unsigned)P.ph_l, e);
-      bv = ll_val(wv[0]);
-      bi = __float_as_int(ll_val(wv[1]));
-    }
-    if (!wg_ok(smem, ok)) return;
-    wave_argmax(bv, bi);
-    float* sv = lds_ptr<float>(smem, kLdsScratch + 64);
-    int* si = lds_ptr<int>(smem, kLdsScratch + 128);
-    if (lane == 0) {
-      sv[tid >> 6] = bv;
-      si[tid >> 6] = bi;
-    }
-    lds_barrier();
-    if (tid == 0) {
-      for (int wv = 1; wv < kPtkWaves; ++wv)
-        if (am_better(sv[wv], si[wv], bv, bi)) {
-          bv = sv[wv];
-          bi = si[wv];
-        }
-      P.toklog[r.pos0 + r.n_tok] = bi == 0x7FFFFFFF ? 0 : bi;
-    }
-  }
+  // one wave-uniform branch into the two roles
+  if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0)
+    ptk_role<true, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
+  else
+    ptk_role<false, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
 }
+#undef DZ_PTK_TPARAMS
 
 }  // namespace dz

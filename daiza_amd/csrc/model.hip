@@ -772,9 +772,9 @@ static int ctx_set_pos_dev(dz_ctx* x, int pos) {
 // ---------------------------------------------------------------- persistent token kernel (host)
 
 // Kernel instantiation for a model shape (the template bounds of ptk_kernel): K tiles of hidden (exact), GQA
-// group, row-block slots per compute wave of each GEMV kind, terms per lane of the residual sums,
-// ffn channels per lane of the SwiGLU sums, rows per lane of the in-projection sums and outputs per
-// workgroup of the attention merge.  Other shapes run on the graph path.
+// group, row-block slots per compute wave of each GEMV kind, terms per thread of the reducers'
+// residual sums, gate/up items per thread of their SwiGLU sums, rows per thread of their in-projection
+// sums and outputs per workgroup of the attention merge.  Other shapes run on the graph path.
 struct PtkShape {
   int th, grp, u_in, u_out, u_gu, u_dn, u_lm, qr, mf, mr, mo;
 };
@@ -783,8 +783,8 @@ static bool ptk_fits(const PtkShape& s, const PtkShape& b) {
          s.u_dn <= b.u_dn && s.u_lm <= b.u_lm && s.qr <= b.qr && s.mf <= b.mf && s.mr <= b.mr && s.mo <= b.mo;
 }
 static const void* ptk_pick(const PtkShape& s) {
-  if (ptk_fits(s, PtkShape{10, 6, 2, 1, 4, 2, 3, 12, 2, 2, 24}))
-    return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 2, 2, 24>);
+  if (ptk_fits(s, PtkShape{10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32}))
+    return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32>);
   if (ptk_fits(s, PtkShape{1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8}))
     return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8>);
   return nullptr;
@@ -814,25 +814,27 @@ static int ptk_prepare(dz_ctx* x) {
   if (!coop || c.head_dim != 256 || c.rope_dim != 64 || c.ssm_state != 128 || G < 8 || G > kPtkThreads ||
       c.n_layers > kPtkMaxLayers || th > kMaxTilesH || c.hidden < G)
     return DZ_OK;
+  // workgroup roles: GEMV workgroups [0, Gp), reducers [Gp, G) (one in eight)
+  const int NR = std::max(8, G / 8), Gp = G - NR;
   // shape limits of the static work split: row-block slots per compute wave of each matrix kind
   const int nrb_h = (int)(ld_h / kRowBlock), nrb_gu = (int)(ld_gu / kRowBlock), nrb_v = (int)m->lm_head.nrb;
   auto slots = [&](int T, int nrb) {
-    if (T > G) return 1 << 20;
+    if (T > Gp) return 1 << 20;
     int mx = 0;
     for (int t = 0; t < T; ++t) {
-      const int nw = tile_first_wg(t + 1, T, G) - tile_first_wg(t, T, G);
+      const int nw = tile_first_wg(t + 1, T, Gp) - tile_first_wg(t, T, Gp);
       mx = std::max(mx, (nrb + nw - 1) / nw);
     }
     return (mx + kCW - 1) / kCW;
   };
-  auto per_wg = [&](int n) { return (n + G - 1) / G; };  // items per workgroup of an even split
-  const int nc = per_wg(c.hidden);                       // residual columns per workgroup
-  auto resid_q = [&](int np) {                           // terms per lane of a residual sum
-    const int K = np + 1, nq = std::min(64 / nc, K);
-    return (K + nq - 1) / nq;
+  auto per = [](int n, int k) { return (n + k - 1) / k; };  // items per part of an even split
+  const int nc = per(c.hidden, NR);                        // reducer residual columns per workgroup
+  auto resid_q = [&](int np) {                             // terms per thread of a residual sum
+    const int K = np + 1, nq = std::min(kPtkThreads / nc, K);
+    return per(K, nq);
   };
-  PtkShape sh{th, grp, 0, 0, slots(th, nrb_gu), slots(tf, nrb_h), (per_wg(nrb_v) + kCW - 1) / kCW, 0,
-              (per_wg(c.ffn) + 63) / 64, 0, per_wg(c.n_head * c.head_dim)};
+  PtkShape sh{th, grp, 0, 0, slots(th, nrb_gu), slots(tf, nrb_h), per(per(nrb_v, G), kCW), 0,
+              per(2 * per(c.ffn, NR), kPtkThreads), 0, per(c.n_head * c.head_dim, Gp)};
   int max_rows_in = 0;
   for (auto& l : m->L) {
     sh.u_in = std::max(sh.u_in, slots(th, (int)l.in_proj.nrb));
@@ -841,19 +843,21 @@ static int ptk_prepare(dz_ctx* x) {
     max_rows_in = std::max(max_rows_in, (int)l.in_proj.rows);
   }
   sh.qr = std::max(sh.qr, resid_q(tf));
-  sh.mr = (per_wg(max_rows_in) + 63) / 64;
-  if (nc > 64 || sh.mo > 64 || sh.mo > c.head_dim) return DZ_OK;
+  sh.mr = per(per(max_rows_in, NR), kPtkThreads);
+  if (nc > kPtkThreads || sh.mo > 64 || sh.mo > c.head_dim || 2 * per(c.ffn, NR) * 4 > kLdsScratchBytes) return DZ_OK;
   const void* kfn = ptk_pick(sh);
   if (!kfn) return DZ_OK;
   int occ = 0;
   DZ_HIP_CHECK(hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
   DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kPtkThreads, kPtkLds));
   if (occ < 1) return DZ_OK;
-  const int gmax = std::min(64, G / std::max(1, c.n_head_kv));
-  if (4 * c.ssm_v_heads > G || c.n_head_kv * gmax > G || gmax < 1) return DZ_OK;
+  const int gmax = std::min(64, Gp / std::max(1, c.n_head_kv));
+  if (4 * c.ssm_v_heads > Gp || c.n_head_kv * gmax > Gp || gmax < 1) return DZ_OK;
   PtkPlan& P = x->ptk.plan;
   memset(&P, 0, sizeof P);
   P.G = G;
+  P.Gp = Gp;
+  P.NR = NR;
   P.n_layers = c.n_layers;
   P.H = c.hidden;
   P.F = c.ffn;

@@ -138,7 +138,8 @@ struct PtkOffsets {
 
 struct PtkPlan {
   // dimensions
-  int G;
+  int G;                       // workgroups (one per CU)
+  int Gp, NR;                  // GEMV workgroups [0, Gp) and reducer workgroups [Gp, G)
   int n_layers;
   int H, F, vocab;
   int nT_h, nrb_h, nT_f, nrb_gu, nrb_v;
@@ -146,7 +147,7 @@ struct PtkPlan {
   int nq, nkv, hd, rope_dim, grp;
   int nrb_in_k[2];             // in-proj row-blocks of a DeltaNet [0] / attention [1] layer
   int nt_out_k[2];             // out-proj K tiles of a DeltaNet [0] / attention [1] layer
-  int gmax;                    // attention chunks per kv-head at most (G / nkv)
+  int gmax;                    // attention chunks per kv-head at most (Gp / nkv)
   int max_ctx;
   float eps;
   int embd_f16;

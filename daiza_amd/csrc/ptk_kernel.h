@@ -97,31 +97,6 @@ __device__ __forceinline__ bool poll(const A& addr, const V& valid, const T& tag
   }
 }
 
-// Hand-offs from the sync wave to the compute waves inside a workgroup.  A CU's vector memory
-// pipeline returns data in issue order across all its waves, so a poll issued behind a phase's
-// weight prefetch waits for the whole prefetch to arrive.  The compute waves therefore request a
-// GEMV's weights only once the sync wave has finished the polls of the phase before it (a residual
-// or SwiGLU sum, which needs no weights), and the weights then overlap the GEMV's own input
-// hand-over.  Both roles count the hand-off points in the same order: the sync wave publishes its
-// count in LDS (sync_bump), a compute wave waits until the count reaches its own (sync_wait,
-// bounded; the sync wave bumps even after a failed poll).
-__device__ __forceinline__ void sync_bump(unsigned char* smem, int seq) {
-  if ((threadIdx.x & 63u) == 0)
-    __hip_atomic_store(reinterpret_cast<int*>(smem + kLdsFlag + 8), seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void sync_wait(unsigned char* smem, int seq) {
-  const int* c = reinterpret_cast<const int*>(smem + kLdsFlag + 8);
-  for (int spin = 0; spin < (1 << 22); ++spin) {
-    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) - seq >= 0) return;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-template <bool SYNC>
-__device__ __forceinline__ void sync_point(unsigned char* smem, int& seq) {
-  ++seq;
-  if constexpr (SYNC) sync_bump(smem, seq);
-}
-
 struct TagC {
   unsigned t;
   __device__ __forceinline__ unsigned operator()(int) const { return t; }
@@ -283,7 +258,7 @@ struct TraceAt {  // where a GEMV phase stamps its sub-points
 __device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->trace != nullptr; }
 
 // One split-K GEMV phase, run by both roles (SYNC: the sync wave, else a compute wave) with the same
-// barriers.  The sync wave stages the tile's inputs (prior: its previous phases succeeded) and the
+// barriers (prior: this thread's previous phases succeeded).  The sync wave stages the tile's inputs and the
 // first workgroup of each tile publishes the tile's sum of squares when the source provides one;
 // all waves build the table; the compute waves run their row-blocks on weights already in
 // registers (requested by an earlier phase), publish LL partials [t][row] and call pf() (the next
@@ -295,9 +270,8 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
                                            const PtkErr& e, const Pf& pf, const TraceAt& tr) {
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
-  bool ok = true;
+  bool ok = prior;
   if constexpr (SYNC) {
-    ok = prior;
     if (ok) {
       float sq = 0.f;
       ok = src.stage(xs, a.t, tid, e, sq);
@@ -399,109 +373,138 @@ __device__ __forceinline__ bool s_select(const PtkPlan& P, const PtkRun& r, int 
   return ok;
 }
 
-// R1 / R3: h_out[c] = h_in[c] + sum_t part[t][c] for this workgroup's columns c (term 0 is h_in,
-// then the tiles in order).  Lane (j, q) sums terms [q*Q, q*Q+Q) of column j; lane j then adds the
-// nq slices in order.
+// ------------------------------------------------------------------ reducer phases
+//
+// The last NR workgroups are reducers: in every layer all their threads form the per-column sums of
+// the split-K partials (R0: in-projection, R1: out-projection + residual, R2: SwiGLU of gate/up,
+// R3: down + residual).  They stream no weights, so their polls never wait behind a weight stream
+// in their CU's memory pipeline, and the GEMV workgroups request their next weights as soon as
+// their lookups are done.  wr is the reducer index (0..NR-1); columns are split evenly over them.
+
+// R1 / R3: h_out[c] = h_in[c] + sum_t part[t][c] (term 0 is h_in, then the tiles in order).  Thread
+// (j, q) sums terms [q*Q, q*Q+Q) of column j into LDS; thread j then adds the nq slices in order.
 template <int QMAX>
-__device__ __forceinline__ bool s_resid(const PtkPlan& P, int w, unsigned lane, const u64* h_in, unsigned tag_h,
-                                        const u64* part, int np, int64_t ldp, unsigned tag_p, u64* h_out, unsigned tag,
-                                        const PtkErr& e) {
+__device__ __forceinline__ bool r_resid(unsigned char* smem, bool prior, const PtkPlan& P, int wr, unsigned tid,
+                                        const u64* h_in, unsigned tag_h, const u64* part, int np, int64_t ldp,
+                                        unsigned tag_p, u64* h_out, unsigned tag, const PtkErr& e) {
+  float* slice = lds_ptr<float>(smem, kLdsScratch);  // nq * nc <= 512 floats
   int c0, c1;
-  even_split(w, P.G, P.H, &c0, &c1);
-  const int nc = c1 - c0;
-  if (nc <= 0) return true;
-  const int K = np + 1;
-  const int nq = min(64 / nc, K);
+  even_split(wr, P.NR, P.H, &c0, &c1);
+  const int nc = c1 - c0, K = np + 1;
+  const int nq = nc > 0 ? min(kPtkThreads / nc, K) : 1;
   const int Q = (K + nq - 1) / nq;
-  const int j = (int)lane % nc, q = (int)lane / nc;
+  const int j = nc > 0 ? (int)tid % nc : 0, q = nc > 0 ? (int)tid / nc : nq;
   const int k0 = q * Q;
-  const bool act = q < nq;
-  u64 x[QMAX];
-  auto addr = [&](int s, unsigned ln) {
-    const int jl = (int)ln % nc, k = ((int)ln / nc) * Q + s;
-    return k == 0 ? h_in + c0 + jl : part + (size_t)(k - 1) * ldp + c0 + jl;
-  };
-  auto valid = [&](int s) { return act && s < Q && k0 + s < K; };
-  auto tagf = [&](int s) { return k0 + s == 0 ? tag_h : tag_p; };
-  const bool ok = poll<QMAX>(addr, valid, tagf, x, e);
-  float sl = 0.f;
+  bool ok = prior;
+  if (ok && q < nq) {
+    u64 x[QMAX];
+    auto addr = [&](int sl, unsigned) {
+      const int k = k0 + sl;
+      return k == 0 ? h_in + c0 + j : part + (size_t)(k - 1) * ldp + c0 + j;
+    };
+    auto valid = [&](int sl) { return sl < Q && k0 + sl < K; };
+    auto tagf = [&](int sl) { return k0 + sl == 0 ? tag_h : tag_p; };
+    ok = poll<QMAX>(addr, valid, tagf, x, e);
+    float sv = 0.f;
 #pragma unroll
-  for (int s = 0; s < QMAX; ++s)
-    if (valid(s)) sl += ll_val(x[s]);
-  float tot = 0.f;
-  for (int qq = 0; qq < nq; ++qq) tot += __shfl(sl, j + qq * nc, 64);
-  if ((int)lane < nc && ok) ll_st(h_out + c0 + lane, tot, tag);
-  return ok;
+    for (int sl = 0; sl < QMAX; ++sl)
+      if (valid(sl)) sv += ll_val(x[sl]);
+    slice[q * nc + j] = sv;
+  }
+  if (!wg_ok(smem, ok)) return false;
+  if ((int)tid < nc) {
+    float tot = 0.f;
+    for (int qq = 0; qq < nq; ++qq) tot += slice[qq * nc + (int)tid];
+    ll_st(h_out + c0 + tid, tot, tag);
+  }
+  lds_barrier();  // the slices are reused by the next reducer phase
+  return true;
 }
 
-// R2: sw[f] = silu(inv * sum_t g[t][f]) * (inv * sum_t u[t][f]) for this workgroup's ffn channels f
-// (lane handles f0 + lane + 64m), inv from h_mid's tile sums of squares (mlp.rs:28-47).
+// R2: sw[f] = silu(inv * sum_t g[t][f]) * (inv * sum_t u[t][f]) (mlp.rs:28-47), inv from h_mid's tile
+// sums of squares.  Items 0..nf-1 are the gate rows of this reducer's channels, nf..2nf-1 the up
+// rows; thread tid sums items tid + 512m (m < MF) into LDS, then thread f combines its channel.
 template <int NTH, int MF>
-__device__ __forceinline__ bool s_swiglu(const PtkPlan& P, int w, unsigned lane, const u64* sstm, const u64* pgu,
-                                         unsigned tag_p, u64* sw, unsigned tag, const PtkErr& e) {
+__device__ __forceinline__ bool r_swiglu(unsigned char* smem, bool prior, const PtkPlan& P, int wr, unsigned tid,
+                                         const u64* sstm, const u64* pgu, unsigned tag_p, u64* sw, unsigned tag,
+                                         const PtkErr& e) {
+  float* gu = lds_ptr<float>(smem, kLdsScratch);  // 2 nf floats
+  float* red = lds_ptr<float>(smem, kLdsRed);
   int f0, f1;
-  even_split(w, P.G, P.F, &f0, &f1);
+  even_split(wr, P.NR, P.F, &f0, &f1);
   const int nf = f1 - f0;
   const int64_t ldp = (int64_t)P.nrb_gu * kRowBlock;
   const int T = P.nT_h;
-  constexpr int N = MF * 2 * NTH + 1;
-  u64 x[N];
-  auto addr = [&](int s, unsigned ln) -> const u64* {
-    if (s == N - 1) return sstm + ln;
-    const int m = s / (2 * NTH), g = (s / NTH) & 1, k = s % NTH;
-    const int f = f0 + (int)ln + 64 * m;
-    return pgu + (size_t)k * ldp + (g ? P.F + f : f);
-  };
-  auto valid = [&](int s) {
-    if (s == N - 1) return (int)lane < T;
-    const int m = s / (2 * NTH), k = s % NTH;
-    return k < T && (int)lane + 64 * m < nf;
-  };
-  const bool ok = poll<N>(addr, valid, TagC{tag_p}, x, e);
-  const float ss = wave_sum((int)lane < T ? ll_val(x[N - 1]) : 0.f);
-  const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+  bool ok = prior;
+  if (ok) {
+    constexpr int N = MF * NTH + NTH;
+    u64 x[N];
+    auto item_row = [&](int it) { return it < nf ? f0 + it : P.F + f0 + (it - nf); };
+    auto addr = [&](int sl, unsigned) -> const u64* {
+      if (sl >= MF * NTH) return sstm + (sl - MF * NTH);
+      return pgu + (size_t)(sl % NTH) * ldp + item_row((int)tid + kPtkThreads * (sl / NTH));
+    };
+    auto valid = [&](int sl) {
+      if (sl >= MF * NTH) return sl - MF * NTH < T;
+      return sl % NTH < T && (int)tid + kPtkThreads * (sl / NTH) < 2 * nf;
+    };
+    ok = poll<N>(addr, valid, TagC{tag_p}, x, e);
 #pragma unroll
-  for (int m = 0; m < MF; ++m) {
-    const int f = (int)lane + 64 * m;
-    if (f < nf && ok) {
-      float g = 0.f, u = 0.f;
+    for (int m = 0; m < MF; ++m) {
+      const int it = (int)tid + kPtkThreads * m;
+      if (it < 2 * nf) {
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < NTH; ++k)
+          if (k < T) v += ll_val(x[m * NTH + k]);
+        gu[it] = v;
+      }
+    }
+    if (tid == 0) {
+      float ss = 0.f;
 #pragma unroll
       for (int k = 0; k < NTH; ++k)
-        if (k < T) {
-          g += ll_val(x[m * 2 * NTH + k]);
-          u += ll_val(x[m * 2 * NTH + NTH + k]);
-        }
-      ll_st(sw + f0 + f, siluf_(g * inv) * (u * inv), tag);
+        if (k < T) ss += ll_val(x[MF * NTH + k]);
+      red[33] = 1.0f / sqrtf(ss / (float)P.H + P.eps);
     }
   }
-  return ok;
+  if (!wg_ok(smem, ok)) return false;
+  const float inv = red[33];
+  for (int f = (int)tid; f < nf; f += kPtkThreads) ll_st(sw + f0 + f, siluf_(gu[f] * inv) * (gu[nf + f] * inv), tag);
+  lds_barrier();
+  return true;
 }
 
-// R0: q|gate|k|v projections = inv * sum of in-proj partials for this workgroup's rows.
+// R0: in-projection outputs = inv * sum of the tile partials (q|k|v|z|alpha|beta of a DeltaNet layer,
+// q|gate|k|v of an attention layer), rows tid + 512m of this reducer's share.  The per-thread
+// outcome is agreed on at the next reducer barrier.
 template <int NTH, int MR>
-__device__ __forceinline__ bool s_qkv(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned lane, const u64* sst_in,
+__device__ __forceinline__ bool r_qkv(const PtkPlan& P, const PtkLayer& Ly, int wr, unsigned tid, const u64* sst_in,
                                       const u64* pin, unsigned tag_in, u64* qkv, unsigned tag, const PtkErr& e) {
   int r0, r1;
-  even_split(w, P.G, Ly.rows_in, &r0, &r1);
+  even_split(wr, P.NR, Ly.rows_in, &r0, &r1);
   const int nr = r1 - r0;
   const int64_t ldp = (int64_t)Ly.nrb_in * kRowBlock;
   const int T = P.nT_h;
-  constexpr int N = MR * NTH + 1;
+  constexpr int N = MR * NTH + NTH;
   u64 x[N];
-  auto addr = [&](int s, unsigned ln) -> const u64* {
-    if (s == N - 1) return sst_in + ln;
-    return pin + (size_t)(s % NTH) * ldp + r0 + (int)ln + 64 * (s / NTH);
+  auto addr = [&](int sl, unsigned) -> const u64* {
+    if (sl >= MR * NTH) return sst_in + (sl - MR * NTH);
+    return pin + (size_t)(sl % NTH) * ldp + r0 + (int)tid + kPtkThreads * (sl / NTH);
   };
-  auto valid = [&](int s) {
-    if (s == N - 1) return (int)lane < T;
-    return s % NTH < T && (int)lane + 64 * (s / NTH) < nr;
+  auto valid = [&](int sl) {
+    if (sl >= MR * NTH) return sl - MR * NTH < T;
+    return sl % NTH < T && (int)tid + kPtkThreads * (sl / NTH) < nr;
   };
   const bool ok = poll<N>(addr, valid, TagC{tag_in}, x, e);
-  const float ss = wave_sum((int)lane < T ? ll_val(x[N - 1]) : 0.f);
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NTH; ++k)
+    if (k < T) ss += ll_val(x[MR * NTH + k]);
   const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    const int row = (int)lane + 64 * m;
+    const int row = (int)tid + kPtkThreads * m;
     if (row < nr && ok) {
       float v = 0.f;
 #pragma unroll
@@ -521,65 +524,57 @@ __device__ __forceinline__ void attn_chunks(const PtkPlan& P, int pos, int* chun
   *gc = (ctx + ch - 1) / ch;
 }
 
+// Max over each row of 16 lanes (DPP); every lane gets its row's maximum.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 // R'': merge the chunk records of each query head and apply the output gate (attention.rs:189-203):
-// ao[h*hd + d] = (O/L) * sigmoid(gate).  Lane g holds chunk g; this workgroup's outputs [j0, j1)
-// span at most two heads.
-template <int MO, class Tr>
-__device__ __forceinline__ bool s_merge(const PtkPlan& P, int w, unsigned lane, int pos, const u64* rec,
-                                        unsigned tag_r, const u64* qkv, unsigned tag_q, u64* ao, unsigned tag,
-                                        const PtkErr& e, const Tr& tr) {
+// ao[h*hd + d] = (O/L) * sigmoid(gate), on all waves of a GEMV workgroup.  Output jj of this
+// workgroup's share [j0, j1) (<= 32 outputs) is handled by the 16 lanes of row jj; lane s of the row
+// holds chunks s, s+16, s+32, s+48 (gmax <= 64), and the row's max and sums are DPP reductions, so no
+// barrier is involved.  The per-thread outcome is agreed on at the next barrier.
+template <int MO>
+__device__ __forceinline__ bool phase_merge(const PtkPlan& P, int w, unsigned tid, int pos, const u64* rec,
+                                            unsigned tag_r, const u64* qkv, unsigned tag_q, u64* ao, unsigned tag,
+                                            const PtkErr& e) {
+  static_assert(MO <= kPtkThreads / 16, "one 16-lane row per attention output");
   constexpr int HD = 256;
   int chunk, gc;
   attn_chunks(P, pos, &chunk, &gc);
   int j0, j1;
-  even_split(w, P.G, P.nq * HD, &j0, &j1);
-  const int no = j1 - j0;
-  if (no <= 0) return true;
-  const int hf = j0 / HD, hl = (j1 - 1) / HD;
-  const bool lg = (int)lane < gc;
-  // slots: 0..3 = m, l of heads hf, hf+1; 4..4+MO-1 = o of output jj; last = gate of output `lane`
-  constexpr int N = 4 + MO + 1;
-  u64 x[N];
-  auto addr = [&](int s, unsigned ln) -> const u64* {
-    auto recp = [&](int h) { return rec + ((size_t)h * P.gmax + ln) * (2 + HD); };
-    if (s < 4) return recp(hf + (s >> 1)) + (s & 1);
-    if (s < 4 + MO) {
-      const int j = j0 + (s - 4);
-      return recp(j / HD) + 2 + (j % HD);
-    }
-    const int j = j0 + (int)ln;
-    return qkv + (int64_t)((j / HD) * 2 + 1) * HD + (j % HD);
+  even_split(w, P.Gp, P.nq * HD, &j0, &j1);
+  const int jj = (int)(tid >> 4), sub = (int)(tid & 15u);
+  const bool act = jj < j1 - j0;
+  const int j = j0 + (act ? jj : 0), h = j / HD, d = j % HD;
+  // slots 3q + {0, 1, 2} = m, l, o[d] of chunk sub + 16q; slot 12 = the output's gate
+  u64 x[13];
+  auto addr = [&](int sl, unsigned) -> const u64* {
+    if (sl == 12) return qkv + (int64_t)(h * 2 + 1) * HD + d;
+    const u64* rc = rec + ((size_t)h * P.gmax + sub + 16 * (sl / 3)) * (2 + HD);
+    return sl % 3 == 2 ? rc + 2 + d : rc + sl % 3;
   };
-  auto valid = [&](int s) {
-    if (s < 4) return lg && hf + (s >> 1) <= hl;
-    if (s < 4 + MO) return lg && s - 4 < no;
-    return (int)lane < no;
-  };
-  auto tagf = [&](int s) { return s < 4 + MO ? tag_r : tag_q; };
-  const bool ok = poll<N>(addr, valid, tagf, x, e);
-  tr(lane, 0, 2);
-  float ex[2], L[2];
+  auto valid = [&](int sl) { return act && (sl == 12 || sub + 16 * (sl / 3) < gc); };
+  auto tagf = [&](int sl) { return sl == 12 ? tag_q : tag_r; };
+  bool ok = true;
+  if (act) ok = poll<13>(addr, valid, tagf, x, e);
+  float mv[4];
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const float mv = valid(2 * hh) ? ll_val(x[2 * hh]) : -INFINITY;
-    const float M = wave_max(mv);
-    ex[hh] = valid(2 * hh) ? __expf(mv - M) : 0.f;
-    L[hh] = wave_sum((valid(2 * hh) ? ll_val(x[2 * hh + 1]) : 0.f) * ex[hh]);
-  }
-  const int gb = __float_as_int((int)lane < no ? ll_val(x[N - 1]) : 0.f);
-  float mine = 0.f;
+  for (int q = 0; q < 4; ++q) mv[q] = valid(3 * q) ? ll_val(x[3 * q]) : -INFINITY;
+  const float M = row16_max(fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3])));
+  float lp = 0.f, op = 0.f;
 #pragma unroll
-  for (int jj = 0; jj < MO; ++jj) {
-    if (jj < no) {
-      const int hh = (j0 + jj) / HD - hf;
-      const float ov = valid(4 + jj) ? ll_val(x[4 + jj]) : 0.f;
-      const float O = wave_sum(ov * (hh ? ex[1] : ex[0]));
-      const float gate = __int_as_float(__builtin_amdgcn_readlane(gb, jj));
-      const float v = (O * (1.0f / (hh ? L[1] : L[0]))) * sigmoidf_(gate);
-      if ((int)lane == jj) mine = v;
-    }
+  for (int q = 0; q < 4; ++q) {
+    const float ex = valid(3 * q) ? __expf(mv[q] - M) : 0.f;
+    lp = __builtin_fmaf(valid(3 * q) ? ll_val(x[3 * q + 1]) : 0.f, ex, lp);
+    op = __builtin_fmaf(valid(3 * q) ? ll_val(x[3 * q + 2]) : 0.f, ex, op);
   }
-  if ((int)lane < no && ok) ll_st(ao + j0 + lane, mine, tag);
+  const float L = row16_sum(lp), O = row16_sum(op);
+  if (act && sub == 0 && ok) ll_st(ao + j, (O * (1.0f / L)) * sigmoidf_(ll_val(x[12])), tag);
   return ok;
 }
 
@@ -1065,19 +1060,21 @@ __device__ __forceinline__ bool asg_lead(unsigned char* smem, int k) { return ld
 
 // Template bounds: NTH K tiles of hidden (DeltaNet / q,k,v / SwiGLU sums), GRP query heads per kv
 // head, U_* row-block slots per compute wave of the in-proj, out-proj, gate/up, down and lm_head
-// phases, QR terms per lane of the residual sums, MF ffn channels per lane of the SwiGLU phase, MR
-// rows per lane of the q/k/v sums, MO attention outputs per workgroup of the chunk merge (all
-// checked on the host).
+// phases, QR terms per thread of the reducers' residual sums, MF gate/up items per thread of the
+// reducers' SwiGLU sums, MR rows per thread of the reducers' in-projection sums, MO attention outputs
+// per workgroup of the chunk merge (all checked on the host).
 #define DZ_PTK_TPARAMS int NTH, int GRP, int U_IN, int U_OUT, int U_GU, int U_DN, int U_LM, int QR, int MF, int MR, int MO
 
 // The token loop of one role: SYNC for wave 0, else for a compute wave.  Both roles walk the same
 // phases and meet at the same barriers (each phase function holds both roles' barriers); a role's
-// registers (the sync wave's poll words, a compute wave's weights) exist only in its own copy.
+// registers (the sync wave's poll words, a compute wave's weights) exist only in its own copy.  In a
+// reducer workgroup both roles run the same reducer code.
 template <bool SYNC, DZ_PTK_TPARAMS>
 __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   const PtkPlan P0 = plan_view(r.plan);
   const PtkErr& e = r.err;
   const int w0 = (int)blockIdx.x, G = P0.G;
+  const bool reducer = w0 >= P0.Gp;
   const PtkOffsets& O = P0.off;
   const int64_t ld_in_h = (int64_t)P0.nrb_h * kRowBlock;
   const int64_t cand_off = ld_in_h;  // token region: h_emb [ld_in_h], cand_v [G], cand_i [G]
@@ -1087,10 +1084,9 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
                                   : (U_OUT > U_GU ? (U_OUT > U_DN ? U_OUT : U_DN) : (U_GU > U_DN ? U_GU : U_DN));
   constexpr int UWL = UW > U_LM ? UW : U_LM;
   WRegs<UWL> wn;
-  float sreg[16];  // DeltaNet state rows (waves 4..7), from the in-projection phase to the DeltaNet phase
+  float sreg[16];  // DeltaNet state rows (waves 4..7), from the layer's start to the DeltaNet phase
   // `ok` carries the sync wave's outcome from its poll phases to the next workgroup barrier
   bool ok = true;
-  int seq = 0;     // hand-off points passed (sync_point)
   int dn_seq = 0;  // DeltaNet phases passed (the compute waves' conv-input arrivals count 3 per phase)
   for (int i = 0; i < r.n_tok; ++i) {
     const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
@@ -1103,7 +1099,6 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
                     tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos);
       ptk_mark(r, P0, i, 0, w0, threadIdx.x, 0);
     }
-    sync_point<SYNC>(smem, seq);
     const u64* h_in = tokreg;
     unsigned tag_h = tb;
     for (int l = 0; l < P0.n_layers; ++l) {
@@ -1115,146 +1110,112 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
       PtkPlan P = P0;
       int w = w0;
 #define DZ_OPQ(f) f = opaque_s(f)
-      DZ_OPQ(w); DZ_OPQ(P.G); DZ_OPQ(P.H); DZ_OPQ(P.F); DZ_OPQ(P.nT_h); DZ_OPQ(P.nT_f); DZ_OPQ(P.nrb_h);
-      DZ_OPQ(P.nrb_gu); DZ_OPQ(P.nrb_v); DZ_OPQ(P.gmax); DZ_OPQ(P.max_ctx); DZ_OPQ(P.nkh); DZ_OPQ(P.nvh);
-      DZ_OPQ(P.qkvd); DZ_OPQ(P.inner); DZ_OPQ(P.off_z); DZ_OPQ(P.off_a); DZ_OPQ(P.off_b); DZ_OPQ(P.nq);
-      DZ_OPQ(P.nkv); DZ_OPQ(P.rope_dim);
+      DZ_OPQ(w); DZ_OPQ(P.G); DZ_OPQ(P.Gp); DZ_OPQ(P.NR); DZ_OPQ(P.H); DZ_OPQ(P.F); DZ_OPQ(P.nT_h); DZ_OPQ(P.nT_f);
+      DZ_OPQ(P.nrb_h); DZ_OPQ(P.nrb_gu); DZ_OPQ(P.nrb_v); DZ_OPQ(P.gmax); DZ_OPQ(P.max_ctx); DZ_OPQ(P.nkh);
+      DZ_OPQ(P.nvh); DZ_OPQ(P.qkvd); DZ_OPQ(P.inner); DZ_OPQ(P.off_z); DZ_OPQ(P.off_a); DZ_OPQ(P.off_b);
+      DZ_OPQ(P.nq); DZ_OPQ(P.nkv); DZ_OPQ(P.rope_dim);
 #undef DZ_OPQ
       const PtkLayer Ly = layer_at(P, l);
       u64* R = ll_region(P, par, l);
       const unsigned t0 = tb + (unsigned)Ly.ph0;
-      const int64_t ld_in = (int64_t)Ly.nrb_in * kRowBlock;
-      const Assign a_out = asg_at(smem, 2 + Ly.attn);
-      const Assign a_gu = asg_at(smem, 4);
-      const Assign a_dn = asg_at(smem, 5);
-      // this layer's in-projection weights, once the sync wave has polled the previous residual sum
-      // (or the token).  Every prefetch is issued in the block that uses it: a loaded value carried
-      // around a loop becomes a phi, resolved with register copies that wait for the loads.
-      // The DeltaNet state rows go first (every layer loads: an attention layer reads 16 words of one
-      // cache line, so that no phi forms), then the in-projection.
-      if constexpr (!SYNC) {
-        sync_wait(smem, seq);
-        dn_state_load(P, Ly, w, tid, sreg);
-        const Assign a = asg_at(smem, Ly.attn);
-        gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
-      }
-      auto nopf = []() {};
-      // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream)
-      {
-        const Assign a = asg_at(smem, Ly.attn);
-        SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
-        // (the next weights depend on the layer kind: requested in its branch)
-        if (!gemv_phase<SYNC, U_IN>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid, e, nopf,
-                                    TraceAt{&r, &P, i, Ly.ph0, w}))
-          return;
-      }
-      // R0: in-projection sums (q|k|v|z|alpha|beta of a DeltaNet layer, q|gate|k|v of an attention layer)
-      if constexpr (SYNC) {
-        ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 0, 1);
-        ok = s_qkv<NTH, MR>(P, Ly, w, tid, R + O.sst_in, R + O.pin, t0, R + O.qkv, t0 + 1, e);
+      const int k = Ly.attn ? 5 : 4;  // R1's phase offset within the layer
+      if (reducer) {
+        // R0, R1, R2, R3 of this layer (all threads)
+        const int wr = w - P.Gp;
+        if (ok) ok = r_qkv<NTH, MR>(P, Ly, wr, tid, R + O.sst_in, R + O.pin, t0, R + O.qkv, t0 + 1, e);
         ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 0);
-      }
-      sync_point<SYNC>(smem, seq);
-      unsigned tag_o;
-      int k;
-      if (!Ly.attn) {
-        // B: DeltaNet
-        ++dn_seq;
-        if (!phase_dn<SYNC>(smem, ok, P, Ly, lds_ptr<int>(smem, kLdsRing)[l], w, tid, pos, R + O.qkv, t0 + 1, R + O.y,
-                            R + O.zs, R + O.yss, t0 + 2, e, sreg, dn_seq, TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+        const unsigned tag_o = t0 + (unsigned)(k - 1);
+        if (!r_resid<QR>(smem, ok, P, wr, tid, h_in, tag_h, R + O.po, Ly.nt_out, ld_in_h, tag_o, R + O.hmid, t0 + k, e))
           return;
-        if constexpr (!SYNC) {
-          ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
-          // the out-projection weights: the sync wave's next polls are this GEMV's own inputs
-          gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
-        }
-        // C: out-proj
-        SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
-        if (!gemv_phase<SYNC, U_OUT>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e, nopf,
-                                     TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
-          return;
-        tag_o = t0 + 3;
-        k = 4;
-      } else {
-        // B': attention chunks
-        if (!phase_attn<SYNC, GRP>(smem, ok, P, Ly, w, tid, pos, R + O.qkv, t0 + 1, R + O.rec, t0 + 2, e, nopf,
-                                   TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
-          return;
-        if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 64);
-        // R'': chunk merge and output gate
-        if constexpr (SYNC) {
-          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0, 1);
-          ok = s_merge<MO>(P, w, tid, pos, R + O.rec, t0 + 2, R + O.qkv, t0 + 1, R + O.ao, t0 + 3, e,
-                           TraceAt{&r, &P, i, Ly.ph0 + 3, w});
-          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0);
-        }
-        sync_point<SYNC>(smem, seq);
-        // the out-projection weights (after the merge's polls)
-        if constexpr (!SYNC) {
-          sync_wait(smem, seq);
-          gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
-        }
-        // C': out-proj
-        SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
-        if (!gemv_phase<SYNC, U_OUT>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e, nopf,
-                                     TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
-          return;
-        tag_o = t0 + 4;
-        k = 5;
-      }
-      // R1: h_mid = h + out-proj.  The sync wave's conv ring / KV cache stores of this layer are
-      // complete before anything it publishes from here on.
-      if constexpr (SYNC) {
-        wait_stores();
-        ptk_mark(r, P, i, Ly.ph0 + k, w, tid, 0, 1);
-        ok = s_resid<QR>(P, w, tid, h_in, tag_h, R + O.po, Ly.nt_out, ld_in_h, tag_o, R + O.hmid, t0 + k, e);
         ptk_mark(r, P, i, Ly.ph0 + k, w, tid, 0);
-      }
-      sync_point<SYNC>(smem, seq);
-      // the gate/up weights (after R1's polls; issued once after the layer kinds' branches join, so
-      // that no phi of two loads forms)
-      if constexpr (!SYNC) {
-        sync_wait(smem, seq);
-        gemv_prefetch<U_GU>(Ly.w_gu, P.nT_h, a_gu.t, a_gu.rb0, a_gu.rb1, tid, wn);
-      }
-      // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
-      {
-        SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};
-        if (!gemv_phase<SYNC, U_GU>(smem, ok, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
-                                    (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nopf, TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
+        if (!r_swiglu<NTH, MF>(smem, true, P, wr, tid, R + O.sst_mid, R + O.pgu, t0 + k + 1, R + O.sw, t0 + k + 2, e))
           return;
-      }
-      // R2: SwiGLU
-      if constexpr (SYNC) {
-        ptk_mark(r, P, i, Ly.ph0 + k + 2, w, tid, 0, 1);
-        ok = s_swiglu<NTH, MF>(P, w, tid, R + O.sst_mid, R + O.pgu, t0 + k + 1, R + O.sw, t0 + k + 2, e);
         ptk_mark(r, P, i, Ly.ph0 + k + 2, w, tid, 0);
-      }
-      sync_point<SYNC>(smem, seq);
-      // the down weights (after R2's polls)
-      if constexpr (!SYNC) {
-        sync_wait(smem, seq);
-        gemv_prefetch<U_DN>(Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1, tid, wn);
-      }
-      // E: down
-      {
-        SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
-        if (!gemv_phase<SYNC, U_DN>(smem, ok, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e, nopf,
-                                    TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
+        if (!r_resid<QR>(smem, true, P, wr, tid, R + O.hmid, t0 + k, R + O.pd, P.nT_f, ld_in_h, t0 + k + 3, R + O.h,
+                         t0 + k + 4, e))
           return;
-      }
-      // R3: h = h_mid + down
-      if constexpr (SYNC) {
-        ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 0, 1);
-        ok = s_resid<QR>(P, w, tid, R + O.hmid, t0 + k, R + O.pd, P.nT_f, ld_in_h, t0 + k + 3, R + O.h, t0 + k + 4, e);
         ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 0);
+      } else {
+        const int64_t ld_in = (int64_t)Ly.nrb_in * kRowBlock;
+        const Assign a_out = asg_at(smem, 2 + Ly.attn);
+        const Assign a_gu = asg_at(smem, 4);
+        const Assign a_dn = asg_at(smem, 5);
+        auto nopf = []() {};
+        // The DeltaNet state rows (every layer loads: an attention layer reads 16 words of one cache
+        // line, so that no phi forms), then the in-projection weights.  Every prefetch is issued in
+        // the block that uses it: a loaded value carried around a loop becomes a phi, resolved with
+        // register copies that wait for the loads.
+        if constexpr (!SYNC) {
+          dn_state_load(P, Ly, w, tid, sreg);
+          const Assign a = asg_at(smem, Ly.attn);
+          gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
+        }
+        // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream)
+        {
+          const Assign a = asg_at(smem, Ly.attn);
+          SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
+          if (!gemv_phase<SYNC, U_IN>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid, e, nopf,
+                                      TraceAt{&r, &P, i, Ly.ph0, w}))
+            return;
+        }
+        if (!Ly.attn) {
+          // B: DeltaNet (q/k/v/z/alpha/beta summed by the reducers in R0)
+          ++dn_seq;
+          if (!phase_dn<SYNC>(smem, true, P, Ly, lds_ptr<int>(smem, kLdsRing)[l], w, tid, pos, R + O.qkv, t0 + 1,
+                              R + O.y, R + O.zs, R + O.yss, t0 + 2, e, sreg, dn_seq, TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+            return;
+          if constexpr (!SYNC) {
+            ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
+            gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
+          }
+          // C: out-proj
+          SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
+          if (!gemv_phase<SYNC, U_OUT>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e, nopf,
+                                       TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
+            return;
+        } else {
+          // B': attention chunks (then the out-proj weights, after the cache reads they would delay)
+          auto pf_out = [&]() {
+            gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
+          };
+          if (!phase_attn<SYNC, GRP>(smem, true, P, Ly, w, tid, pos, R + O.qkv, t0 + 1, R + O.rec, t0 + 2, e, pf_out,
+                                     TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+            return;
+          if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 64);
+          // R'': chunk merge and output gate (all waves)
+          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0, 1);
+          ok = phase_merge<MO>(P, w, tid, pos, R + O.rec, t0 + 2, R + O.qkv, t0 + 1, R + O.ao, t0 + 3, e) && ok;
+          ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0);
+          // C': out-proj
+          SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
+          if (!gemv_phase<SYNC, U_OUT>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e, nopf,
+                                       TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
+            return;
+        }
+        // the gate/up weights (issued once after the layer kinds' branches join, so that no phi of two
+        // loads forms); the sync wave's next polls are this GEMV's own inputs (h_mid, from R1)
+        if constexpr (!SYNC) gemv_prefetch<U_GU>(Ly.w_gu, P.nT_h, a_gu.t, a_gu.rb0, a_gu.rb1, tid, wn);
+        // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
+        {
+          SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};
+          if (!gemv_phase<SYNC, U_GU>(smem, true, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
+                                      (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nopf,
+                                      TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
+            return;
+        }
+        if constexpr (!SYNC) gemv_prefetch<U_DN>(Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1, tid, wn);
+        // E: down (its input is R2's SwiGLU)
+        {
+          SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
+          if (!gemv_phase<SYNC, U_DN>(smem, true, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e, nopf,
+                                      TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
+            return;
+        }
       }
-      sync_point<SYNC>(smem, seq);
       h_in = R + O.h;
       tag_h = t0 + k + 4;
     }
-    // L: lm_head + argmax candidates (its first tile's weights once R3's polls are done)
-    if constexpr (!SYNC) sync_wait(smem, seq);
+    // L: lm_head + argmax candidates (all workgroups)
     if (!phase_lm<SYNC, NTH, U_LM>(smem, ok, P0, r, i, w0, threadIdx.x, h_in, tag_h, wn, tokreg + cand_off,
                                    tokreg + cand_off + G, tb + (unsigned)P0.ph_l))
       return;
@@ -1289,12 +1250,13 @@ __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
     // (selects, not indexing: a thread-dependent index into the plan would put it in scratch memory)
     const int T = k < 2 ? P.nT_h : k == 2 ? P.nt_out_k[0] : k == 3 ? P.nt_out_k[1] : k == 4 ? P.nT_h : P.nT_f;
     const int nrb = k == 0 ? P.nrb_in_k[0] : k == 1 ? P.nrb_in_k[1] : k < 4 ? P.nrb_h : k == 4 ? P.nrb_gu : P.nrb_h;
-    const Assign a = gemv_assign(w, G, T, nrb);
+    const int Gp = P.Gp, wg = w < Gp ? w : 0;  // a reducer's assignment is never used
+    const Assign a = gemv_assign(wg, Gp, T, nrb);
     int* q = lds_ptr<int>(smem, kLdsAsg) + 4 * k;
     q[0] = a.t;
     q[1] = a.rb0;
     q[2] = a.rb1;
-    q[3] = w == tile_first_wg(a.t, T, G);
+    q[3] = w < Gp && w == tile_first_wg(a.t, T, Gp);
   }
   for (int l = (int)tid; l < P.n_layers; l += kPtkThreads) {
     const DZ_AS_CONST PtkLayer* t = (const DZ_AS_CONST PtkLayer*)P.L + l;

@@ -351,6 +351,10 @@ __device__ __forceinline__ bool s_select(const PtkPlan& P, const PtkRun& r, int 
     tok = s_pick(P, lane, cand_v, cand_i, tag_prev, r.err, ok);
   }
   if (w == 0 && lane == 0) P.toklog[pos] = tok;
+  // This wave's conv ring and KV cache stores of the previous token are complete before its first
+  // publish of this token.  Every workgroup's layer-0 input depends on every workgroup's embedding
+  // columns, so any read of those stores in this token happens after them.
+  wait_stores();
   int c0, c1;
   even_split(w, P.G, P.H, &c0, &c1);
   for (int col = c0 + (int)lane; col < c1; col += 64) {
@@ -626,9 +630,38 @@ __device__ __forceinline__ int64_t dn_conv_row(const PtkPlan& P, int kh, int vh,
                                                    : 2 * kdim + (int64_t)vh * 128 + quarter * 32 + (c - 256);
 }
 
+// The conv inputs a compute thread of waves 1..3 brings to the DeltaNet phase: ring history (3) and
+// conv weights (4) of channels c = tid-64 and tid-64+192, and (thread 64) ssm_a, dt_bias.  Loaded at
+// the start of the layer, long before the phase, so that they are never in the CU's memory pipeline
+// ahead of the sync wave's polls.  Every thread loads: one without channels (or in an attention
+// layer) reads distinct words of one cache line, so that no phi forms.
+struct DnConvIn {
+  float rh[2][3], cw[2][4], g[2];
+};
+__device__ __forceinline__ void dn_conv_load(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned tid, int ring_base,
+                                             int pos, DnConvIn& ci) {
+  const bool wgv = !Ly.attn && w < 4 * P.nvh && tid >= 64 && tid < 256;
+  const int vh = w >> 2, quarter = w & 3, kh = vh % P.nkh;
+  const int hb = (ring_base + pos) & 3;
+  const int64_t qkvd = P.qkvd;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int c = (int)tid - 64 + 192 * k;
+    const bool v = wgv && c < kDnCh;
+    const int64_t row = v ? dn_conv_row(P, kh, vh, quarter, c) : 0;
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      ci.rh[k][t] = co_ld(v ? Ly.conv + (size_t)((hb + 1 + t) & 3) * qkvd + row : P.output_norm + 7 * k + t);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ci.cw[k][t] = v ? Ly.conv_w[(size_t)t * qkvd + row] : P.output_norm[7 * k + 3 + t];
+  }
+  const bool gv = wgv && tid == 64;
+  ci.g[0] = gv ? Ly.ssm_a[vh] : P.output_norm[14];
+  ci.g[1] = gv ? Ly.dt_bias[vh] : P.output_norm[15];
+}
+
 // Workgroup w < 4*nvh: v-head w/4, state rows (w%4)*32 .. +32 (ssm.rs:425-616).  Compute waves 1..3
-// bring the conv ring history, conv weights and gate constants into LDS (memory traffic kept off the
-// sync wave's pipeline position, ahead of its polls) and count themselves in; the sync wave takes
+// write the conv inputs they loaded at the layer's start into LDS and count themselves in; the sync wave takes
 // its in-projection channels (q and k of the tiled k-head kh = vh % nkh, this quarter's v and z
 // channels, alpha, beta; summed and scaled by 1/rms in phase R0), runs the conv ring + causal conv +
 // SiLU, the q/k L2 norms and the gates, and publishes silu(z); waves 4..7 then run the delta rule on
@@ -638,7 +671,7 @@ template <bool SYNC>
 __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const PtkPlan& P, const PtkLayer& Ly,
                                          int ring_base, int w, unsigned tid, int pos, const u64* qkvz, unsigned tag_in,
                                          u64* y, u64* zs, u64* yss, unsigned tag, const PtkErr& e, float (&s)[16],
-                                         int dn_seq, const TraceAt& tr) {
+                                         const DnConvIn& ci, int dn_seq, const TraceAt& tr) {
   constexpr int HD = 128;
   if (w >= 4 * P.nvh) return wg_ok(smem, SYNC ? prior : true);
   float* qs = lds_ptr<float>(smem, kLdsScratch);
@@ -654,21 +687,20 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
   const int64_t qkvd = P.qkvd;
   bool ok = SYNC ? prior : true;
   if (!SYNC && tid < 256) {
-    // waves 1..3: conv inputs of channels c = tid-64 and tid-64+192
+    // waves 1..3: conv inputs of channels c = tid-64 and tid-64+192 (loaded at the layer's start)
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int c = (int)tid - 64 + 192 * k;
       if (c < kDnCh) {
-        const int64_t row = dn_conv_row(P, kh, vh, quarter, c);
 #pragma unroll
-        for (int t = 0; t < 3; ++t) rl[t * kDnCh + c] = co_ld(Ly.conv + (size_t)((hb + 1 + t) & 3) * qkvd + row);
+        for (int t = 0; t < 3; ++t) rl[t * kDnCh + c] = ci.rh[k][t];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) cwl[t * kDnCh + c] = Ly.conv_w[(size_t)t * qkvd + row];
+        for (int t = 0; t < 4; ++t) cwl[t * kDnCh + c] = ci.cw[k][t];
       }
     }
     if (tid == 64) {
-      gl[0] = Ly.ssm_a[vh];
-      gl[1] = Ly.dt_bias[vh];
+      gl[0] = ci.g[0];
+      gl[1] = ci.g[1];
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are done (lgkmcnt(0))
     if ((tid & 63u) == 0) __hip_atomic_fetch_add(arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1085,6 +1117,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   constexpr int UWL = UW > U_LM ? UW : U_LM;
   WRegs<UWL> wn;
   float sreg[16];  // DeltaNet state rows (waves 4..7), from the layer's start to the DeltaNet phase
+  DnConvIn cin;    // DeltaNet conv inputs (waves 1..3), likewise
   // `ok` carries the sync wave's outcome from its poll phases to the next workgroup barrier
   bool ok = true;
   int dn_seq = 0;  // DeltaNet phases passed (the compute waves' conv-input arrivals count 3 per phase)
@@ -1146,6 +1179,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         // the block that uses it: a loaded value carried around a loop becomes a phi, resolved with
         // register copies that wait for the loads.
         if constexpr (!SYNC) {
+          dn_conv_load(P, Ly, w, tid, lds_ptr<int>(smem, kLdsRing)[l], pos, cin);
           dn_state_load(P, Ly, w, tid, sreg);
           const Assign a = asg_at(smem, Ly.attn);
           gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
@@ -1162,7 +1196,8 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           // B: DeltaNet (q/k/v/z/alpha/beta summed by the reducers in R0)
           ++dn_seq;
           if (!phase_dn<SYNC>(smem, true, P, Ly, lds_ptr<int>(smem, kLdsRing)[l], w, tid, pos, R + O.qkv, t0 + 1,
-                              R + O.y, R + O.zs, R + O.yss, t0 + 2, e, sreg, dn_seq, TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
+                              R + O.y, R + O.zs, R + O.yss, t0 + 2, e, sreg, cin, dn_seq,
+                              TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
             return;
           if constexpr (!SYNC) {
             ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);

@@ -136,6 +136,29 @@ __device__ __forceinline__ void gemv_prefetch(const uint8_t* W, int ntiles, int 
   }
 }
 
+// One slot of gemv_prefetch.
+template <int U>
+__device__ __forceinline__ void gemv_prefetch_slot(const uint8_t* W, int ntiles, int t, int rb0, int rb1, unsigned tid,
+                                                   WRegs<U>& r, int m) {
+  const unsigned lane = tid & 63u, cw = (tid >> 6) - 1;
+  const int rb = rb0 + (int)cw + kCW * m;
+  const bool v = rb < rb1;
+  const uint8_t* unit = W + ((size_t)(v ? rb : 0) * ntiles + t) * kUnitBytes;
+  const u32x4* sp = reinterpret_cast<const u32x4*>(v ? unit + (size_t)lane * 16 : W + (size_t)m * 80);
+  const int cs = v ? 64 : 1;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) r.u[m].s[c] = __builtin_nontemporal_load(sp + c * cs);
+  const u32x2* scp = reinterpret_cast<const u32x2*>(v ? unit + kUnitSignBytes + (size_t)lane * 8 : W + (size_t)m * 80 + 64);
+  r.u[m].sc = __builtin_nontemporal_load(scp);
+}
+
+// The next GEMV phase's weights (UNX slots, 0 for none), requested by a GEMV phase when it is done
+// with its own.
+struct NextW {
+  const uint8_t* W;
+  int ntiles, t, rb0, rb1;
+};
+
 // LUT input sources: the sync wave (lane = 0..63) writes xs[lane + 64*m] (m < 8) for tile t after
 // waiting for their words.  sq receives this lane's share of the tile's sum of v^2 when the source
 // is normed (the GEMV publishes the tile sum from one workgroup per tile when sst is set: the
@@ -261,13 +284,13 @@ __device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->t
 // barriers (prior: this thread's previous phases succeeded).  The sync wave stages the tile's inputs and the
 // first workgroup of each tile publishes the tile's sum of squares when the source provides one;
 // all waves build the table; the compute waves run their row-blocks on weights already in
-// registers (requested by an earlier phase), publish LL partials [t][row] and call pf() (the next
-// GEMV's weight prefetch into the same registers).  The sync wave leaves once the table is built
-// and goes on to its next phase while the compute waves finish.
-template <bool SYNC, int UN, int U, class Src, class Pf>
+// registers (requested by an earlier phase), publish LL partials [t][row] and request the next
+// GEMV's weights (nx, UNX slots) into the same registers.  The sync wave leaves once the table is
+// built and goes on to its next phase while the compute waves finish.
+template <bool SYNC, int UN, int UNX, int U, class Src>
 __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, const Src& src, WRegs<U>& r, const Assign& a,
                                            bool lead, u64* out, int64_t ld, unsigned tag, unsigned tid,
-                                           const PtkErr& e, const Pf& pf, const TraceAt& tr) {
+                                           const PtkErr& e, const NextW& nx, const TraceAt& tr) {
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
   bool ok = prior;
@@ -292,8 +315,10 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
     const unsigned cw = (tid >> 6) - 1, lane = tid & 63u;
     unsigned c[16];
     make_pos_consts(lane, c);
-    // every dot product before the first store: gfx9 counts loads and stores on one vmcnt, and with
-    // a store pending the wait for the next row-block's weights becomes a wait for everything
+    // Every lookup before the first store: gfx9 counts loads and stores on one vmcnt, and with a
+    // store pending the wait for a row-block's weights becomes a wait for everything.  The next
+    // GEMV's weights after the stores: the CU's memory pipeline is in order, and stores queued
+    // behind a prefetch reach the consumers only after it.
     float y[UN];
 #pragma unroll
     for (int m = 0; m < UN; ++m) y[m] = a.rb0 + (int)cw + kCW * m < a.rb1 ? unit_dot(r.u[m], c) : 0.f;
@@ -303,7 +328,8 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
       if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, y[m], tag);
     }
     tr.last_wave(smem, tid);
-    pf();
+#pragma unroll
+    for (int m = 0; m < UNX; ++m) gemv_prefetch_slot<U>(nx.W, nx.ntiles, nx.t, nx.rb0, nx.rb1, tid, r, m);
   }
   return true;
 }
@@ -1173,7 +1199,6 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         const Assign a_out = asg_at(smem, 2 + Ly.attn);
         const Assign a_gu = asg_at(smem, 4);
         const Assign a_dn = asg_at(smem, 5);
-        auto nopf = []() {};
         // The DeltaNet state rows (every layer loads: an attention layer reads 16 words of one cache
         // line, so that no phi forms), then the in-projection weights.  Every prefetch is issued in
         // the block that uses it: a loaded value carried around a loop becomes a phi, resolved with
@@ -1184,12 +1209,15 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           const Assign a = asg_at(smem, Ly.attn);
           gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
         }
-        // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream)
+        // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream).
+        // In a DeltaNet layer the out-proj weights follow slot by slot (an attention layer requests
+        // them after its cache reads, and here reads one line per slot instead).
         {
           const Assign a = asg_at(smem, Ly.attn);
           SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
-          if (!gemv_phase<SYNC, U_IN>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid, e, nopf,
-                                      TraceAt{&r, &P, i, Ly.ph0, w}))
+          const NextW nx{Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, Ly.attn ? a_out.rb0 : a_out.rb1};
+          if (!gemv_phase<SYNC, U_IN, U_OUT>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid,
+                                             e, nx, TraceAt{&r, &P, i, Ly.ph0, w}))
             return;
         }
         if (!Ly.attn) {
@@ -1199,14 +1227,11 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
                               R + O.y, R + O.zs, R + O.yss, t0 + 2, e, sreg, cin, dn_seq,
                               TraceAt{&r, &P, i, Ly.ph0 + 2, w}))
             return;
-          if constexpr (!SYNC) {
-            ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
-            gemv_prefetch<U_OUT>(Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, a_out.rb1, tid, wn);
-          }
+          if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
           // C: out-proj
           SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
-          if (!gemv_phase<SYNC, U_OUT>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e, nopf,
-                                       TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
+          if (!gemv_phase<SYNC, U_OUT, 0>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e,
+                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
             return;
         } else {
           // B': attention chunks (then the out-proj weights, after the cache reads they would delay)
@@ -1223,8 +1248,8 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           ptk_mark(r, P, i, Ly.ph0 + 3, w, tid, 0);
           // C': out-proj
           SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
-          if (!gemv_phase<SYNC, U_OUT>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e, nopf,
-                                       TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
+          if (!gemv_phase<SYNC, U_OUT, 0>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e,
+                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
             return;
         }
         // the gate/up weights (issued once after the layer kinds' branches join, so that no phi of two
@@ -1233,17 +1258,17 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
         {
           SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};
-          if (!gemv_phase<SYNC, U_GU>(smem, true, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
-                                      (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nopf,
-                                      TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
+          const NextW nx_dn{Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1};
+          if (!gemv_phase<SYNC, U_GU, U_DN>(smem, true, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
+                                            (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nx_dn,
+                                            TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
             return;
         }
-        if constexpr (!SYNC) gemv_prefetch<U_DN>(Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1, tid, wn);
         // E: down (its input is R2's SwiGLU)
         {
           SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
-          if (!gemv_phase<SYNC, U_DN>(smem, true, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e, nopf,
-                                      TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
+          if (!gemv_phase<SYNC, U_DN, 0>(smem, true, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e,
+                                         NextW{}, TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
             return;
         }
       }

@@ -94,6 +94,7 @@ def lib():
     L.dz_q1_0_shape.argtypes = [_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
     L.dz_q1_0_matvec.argtypes = [_vp, _f32p, _f32p, ctypes.c_int]
     L.dz_q1_0_matvec_multi.argtypes = [ctypes.POINTER(_vp), ctypes.c_int, _f32p, ctypes.POINTER(_f32p)]
+    L.dz_q1_0_matvec_batch.argtypes = [_vp, _f32p, ctypes.c_int, _f32p, ctypes.c_int]
     L.dz_q1_0_matvec_dev.argtypes = [_vp, _vp, _vp, ctypes.c_int, _vp]
     L.dz_q1_0_dequant_rows.argtypes = [_vp, ctypes.c_size_t, ctypes.c_size_t, _f32p]
     L.dz_q1_0_gemv_partials.argtypes = [_vp, _vp, _vp, _vp]
@@ -137,7 +138,7 @@ _MODEL_PROTOS = {
 
 EXPORTED_SYMBOLS = [
     "dz_config_bonsai27b", "dz_last_error", "dz_device_init",
-    "dz_q1_0_upload", "dz_q1_0_free", "dz_q1_0_shape", "dz_q1_0_matvec", "dz_q1_0_matvec_multi",
+    "dz_q1_0_upload", "dz_q1_0_free", "dz_q1_0_shape", "dz_q1_0_matvec", "dz_q1_0_matvec_multi", "dz_q1_0_matvec_batch",
     "dz_q1_0_matvec_dev", "dz_q1_0_dequant_rows", "dz_q1_0_gemv_partials", "dz_q1_0_partials_ld", "dz_q1_0_ntiles",
 ] + list(k for k in _MODEL_PROTOS if k != "dz_config_bonsai27b")
 
@@ -202,6 +203,26 @@ class Q1_0Matrix:
         hs = (_vp * n)(*[m._h for m in matrices])
         ys = (_f32p * n)(*[_f(o) for o in outputs])
         _check(lib().dz_q1_0_matvec_multi(hs, n, _f(x), ys))
+
+    def matvec_batch_into_slice(self, x, n_batch, y):
+        """y[i] = W x[i] for i < n_batch; x [n][cols], y [n][rows] (weights.rs:475-682)."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.size == n_batch * self.cols and y.size == n_batch * self.rows
+        assert y.dtype == np.float32 and y.flags.c_contiguous
+        _check(lib().dz_q1_0_matvec_batch(self._h, _f(x), n_batch, _f(y), 0))
+
+    def matvec_add_batch_into_slice(self, x, n_batch, y):
+        """y[i] += W x[i] for i < n_batch (weights.rs:976-980)."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.size == n_batch * self.cols and y.size == n_batch * self.rows
+        assert y.dtype == np.float32 and y.flags.c_contiguous
+        _check(lib().dz_q1_0_matvec_batch(self._h, _f(x), n_batch, _f(y), 1))
+
+    def matvec_batch(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.cols)
+        y = np.empty((x.shape[0], self.rows), np.float32)
+        self.matvec_batch_into_slice(x, x.shape[0], y)
+        return y
 
     def row_into_slice(self, row, y):
         """Dequantised row (weights.rs:106 -> quant.rs:161-194)."""

@@ -1,0 +1,234 @@
+// q1_gemm.h — the N-column Q1_0 product Y[n][rows] (=|+=) X[n][cols] · Wᵀ on gfx950's matrix
+// cores, for prefill and speculative verify: matvec_batch_into_slice / matvec_add_batch_into_slice
+// (Daiza-engine/src/model/weights.rs:475-682, 976-980) and the batched GEMM it dispatches to
+// (tensor/gemm.rs:336-439).
+//
+// Numerics.  A weight is ±scale with scale an f16 value, so it is exact as an f16 matrix-core
+// operand (f16 subnormal scales included).  Each token's activations are divided by a power of two
+// sig (exact) that puts their largest magnitude in [2^13, 2^14), and split into two f16 values
+// hi = f16(x/sig), lo = f16(x/sig - hi); hi + lo carries 22 significant bits.  The products of the
+// f16 operands are exact in the f32 accumulator, so y = sig·(W·hi + W·lo) differs from an f32
+// dot product only by the f32 accumulation order (the reference's GEMM reorders its sums too,
+// gemm.rs:153-225).
+//
+// Layout.  The weights stay in the GEMV layout (common.h): unit (row-block rb, tile t) holds 64
+// rows × 512 columns, each row's 64 sign bytes as four 16-byte chunks, chunk c of row L holding
+// group (L >> 4) ^ c with its bytes permuted by position ^ L.  Wave w of a workgroup owns row-block
+// rb = 4·blockIdx.x + w and walks the tiles; in a 16-row block sb of that unit, lane (r, q)
+// (r = lane & 15, q = lane >> 4) takes the chunk of row 16·sb + r that holds group q, restores the
+// byte order in registers, and feeds sign byte s of that group as the eight f16 values of
+// v_mfma_f32_16x16x32_f16's A operand for step s (columns 128q + 8s + e).  The B operand, token
+// (lane & 15)'s activations at the same columns, is read from a tile staged in LDS.
+#pragma once
+#include "common.h"
+
+namespace dz {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup
+constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup (and the padding of n)
+constexpr int kGemmRowPad = 2 * kTileCols + 16;  // LDS bytes per staged token row (16 B pad: no bank conflicts)
+constexpr size_t kGemmShmem = (size_t)2 * kGemmTok * kGemmRowPad;  // hi and lo tiles
+
+// Activations packed for the matrix cores.
+struct GemmX {
+  const uint16_t* xh;  // [Np][Kp] f16 bits of x/sig
+  const uint16_t* xl;  // [Np][Kp] f16 bits of x/sig - hi
+  const float* sig;    // [Np] power-of-two scale of each token
+  int64_t Kp;          // columns padded to the tile (ntiles * 512)
+};
+
+// The power of two that brings max|x| into [2^13, 2^14) (1 for an all-zero or non-finite row).
+__device__ __forceinline__ float pack_sig(float amax) {
+  if (!(amax > 0.f) || !(amax <= 3.0e38f)) return 1.0f;
+  int e;
+  (void)frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
+  return ldexpf(1.0f, e - 14 < -100 ? -100 : e - 14);
+}
+
+// Splits one value (already divided by sig) into its f16 hi and lo parts.
+__device__ __forceinline__ void pack_split(float v, unsigned short& h, unsigned short& l) {
+  const _Float16 hi = (_Float16)v;
+  h = __builtin_bit_cast(unsigned short, hi);
+  l = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)hi));
+}
+
+// One workgroup (256 threads) per token row n < Np: x[n][0..K) -> xh/xl[n][0..Kp), sig[n]; rows
+// n >= n_tok and columns k >= K are zero.  When w is given the row is first RMS-normalised with
+// weight w (rmsnorm_into, Daiza-engine/src/math/rmsnorm.rs:17-200: x·(1/sqrt(ss/K + eps))·w).
+__global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x, int64_t ldx, int64_t K, int n_tok,
+                                                     const float* __restrict__ w, float eps, uint16_t* __restrict__ xh,
+                                                     uint16_t* __restrict__ xl, float* __restrict__ sig, int64_t Kp) {
+  __shared__ float red[8];
+  const int n = blockIdx.x;
+  const unsigned tid = threadIdx.x;
+  const bool live = n < n_tok;
+  const float* row = x + (size_t)(live ? n : 0) * ldx;
+  float inv = 1.0f;
+  if (w) {
+    float ss = 0.f;
+    for (int64_t k = tid; k < K; k += 256) ss = __builtin_fmaf(row[k], row[k], ss);
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63u) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    inv = 1.0f / sqrtf(ss / (float)K + eps);
+    __syncthreads();
+  }
+  float amax = 0.f;
+  for (int64_t k = tid; k < K; k += 256) {
+    const float v = w ? (row[k] * inv) * w[k] : row[k];
+    amax = fmaxf(amax, fabsf(v));
+  }
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63u) == 0) red[4 + (tid >> 6)] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+  const float s = live ? pack_sig(amax) : 1.0f;
+  const float rs = 1.0f / s;  // exact: s is a power of two
+  uint16_t* oh = xh + (size_t)n * Kp;
+  uint16_t* ol = xl + (size_t)n * Kp;
+  for (int64_t k = tid; k < Kp; k += 256) {
+    unsigned short h = 0, l = 0;
+    if (live && k < K) pack_split((w ? (row[k] * inv) * w[k] : row[k]) * rs, h, l);
+    oh[k] = h;
+    ol[k] = l;
+  }
+  if (tid == 0) sig[n] = live ? s : 0.f;
+}
+
+// Sign byte s of a restored chunk (4 dwords, bit set = +scale after the sign fix-up) as the eight
+// f16 operand values: element e = f16 with magnitude |scale| (s2 = |scale| in both halves) and
+// sign from bit 8·(s & 3) + e of dword s >> 2.
+template <int S>
+__device__ __forceinline__ f16x8 expand_signs(const unsigned (&wn)[4], unsigned s2) {
+  const unsigned w = wn[S >> 2];
+  unsigned d[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    constexpr int o0 = 8 * (S & 3);
+    const int o = o0 + 2 * p;
+    const unsigned lo = o <= 15 ? (w << (15 - o)) : (w >> (o - 15));  // bit o -> 15
+    const unsigned hi = w << (30 - o);                                 // bit o+1 -> 31
+    const unsigned t = (lo & 0x00008000u) | (hi & ~0x00008000u);
+    d[p] = (t & 0x80008000u) | s2;
+  }
+  u32x4 v = {d[0], d[1], d[2], d[3]};
+  return __builtin_bit_cast(f16x8, v);
+}
+
+// Chunk of row L = 16·sb + r holding group q, bytes restored to position order and sign bits
+// turned into "bit set = sign bit of the f16 value set" (the stored bit set means +scale).
+__device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, unsigned r, unsigned (&wn)[4],
+                                              unsigned& s2) {
+  // stored byte i <-> position 16q + (i ^ r): first within dwords (i & 3), then across dwords
+  const unsigned sel = 0x03020100u ^ (0x01010101u * (r & 3u));
+  unsigned u[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] = __builtin_amdgcn_perm(v[k], v[k], sel);
+  const bool x1 = (r >> 2) & 1u, x2 = (r >> 3) & 1u;
+  unsigned t[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) t[k] = x1 ? u[k ^ 1] : u[k];
+  // sign of +scale when the bit is set, of -scale when clear: f16 sign bit = bit ^ !sign(scale)
+  const unsigned flip = (sc_bits & 0x8000u) ? 0u : 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wn[k] = (x2 ? t[k ^ 2] : t[k]) ^ flip;
+  s2 = (sc_bits & 0x7FFFu) * 0x00010001u;
+}
+
+// Grid (ceil(nrb / 4), Np / kGemmTok), 256 threads, kGemmShmem bytes of dynamic LDS.
+// y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xl)[n][k] for n < n_tok, row < rows.
+__global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
+                                                         int ntiles, const GemmX x, int n_tok, float* __restrict__ y,
+                                                         int64_t ldy, int accumulate) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const unsigned tid = threadIdx.x, lane = tid & 63u;
+  const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6);
+  const bool live = rb < nrb;
+  const int tok0 = (int)blockIdx.y * kGemmTok;
+  const unsigned r = lane & 15u, q = lane >> 4;
+  f32x4 acc[4][kGemmNB];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+    for (int nb = 0; nb < kGemmNB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int t = 0; t < ntiles; ++t) {
+    // this wave's unit: per 16-row block sb, the chunk c = sb ^ q of row 16·sb + r and its scale slot c
+    u32x4 cv[4];
+    unsigned cs[4];
+    if (live) {
+      const uint8_t* unit = W + ((size_t)rb * ntiles + t) * kUnitBytes;
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        const unsigned L = 16u * sb + r, c = (unsigned)sb ^ q;
+        cv[sb] = *reinterpret_cast<const u32x4*>(unit + ((size_t)c * 64 + L) * 16);
+        const unsigned short* scp = reinterpret_cast<const unsigned short*>(unit + kUnitSignBytes + (size_t)L * 8);
+        cs[sb] = scp[c];
+      }
+    }
+    __syncthreads();  // the previous tile's LDS reads are done
+    // stage the activations of tile t: [hi | lo][token][512 f16], rows padded to kGemmRowPad
+    for (int i = (int)tid; i < 2 * kGemmTok * 64; i += 256) {
+      const int part = i / (kGemmTok * 64), rem = i % (kGemmTok * 64), n = rem >> 6, c = rem & 63;
+      const uint16_t* src = (part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp + (size_t)t * kTileCols + 8 * c;
+      *reinterpret_cast<u32x4*>(smem + ((size_t)part * kGemmTok + n) * kGemmRowPad + 16 * c) =
+          *reinterpret_cast<const u32x4*>(src);
+    }
+    __syncthreads();
+    if (live) {
+      unsigned wn[4][4], s2[4];
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
+      // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
+      const unsigned char* bh = smem + (size_t)r * kGemmRowPad + 256u * q;
+      const unsigned char* bl = bh + (size_t)kGemmTok * kGemmRowPad;
+#define DZ_GEMM_STEP(S)                                                                               \
+  {                                                                                                   \
+    f16x8 xh_[kGemmNB], xl_[kGemmNB];                                                                 \
+    _Pragma("unroll") for (int nb = 0; nb < kGemmNB; ++nb) {                                          \
+      xh_[nb] = *reinterpret_cast<const f16x8*>(bh + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
+      xl_[nb] = *reinterpret_cast<const f16x8*>(bl + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
+    }                                                                                                 \
+    _Pragma("unroll") for (int sb = 0; sb < 4; ++sb) {                                                \
+      const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
+      _Pragma("unroll") for (int nb = 0; nb < kGemmNB; ++nb) {                                        \
+        acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], acc[sb][nb], 0, 0, 0);       \
+        acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl_[nb], acc[sb][nb], 0, 0, 0);       \
+      }                                                                                               \
+    }                                                                                                 \
+  }
+      DZ_GEMM_STEP(0) DZ_GEMM_STEP(1) DZ_GEMM_STEP(2) DZ_GEMM_STEP(3)
+      DZ_GEMM_STEP(4) DZ_GEMM_STEP(5) DZ_GEMM_STEP(6) DZ_GEMM_STEP(7)
+      DZ_GEMM_STEP(8) DZ_GEMM_STEP(9) DZ_GEMM_STEP(10) DZ_GEMM_STEP(11)
+      DZ_GEMM_STEP(12) DZ_GEMM_STEP(13) DZ_GEMM_STEP(14) DZ_GEMM_STEP(15)
+#undef DZ_GEMM_STEP
+    }
+  }
+  if (!live) return;
+  // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
+#pragma unroll
+  for (int nb = 0; nb < kGemmNB; ++nb) {
+    const int n = tok0 + 16 * nb + (int)r;
+    if (n >= n_tok) continue;
+    const float sg = x.sig[n];
+    float* yr = y + (size_t)n * ldy;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      const int64_t row0 = rb * kRowBlock + 16 * sb + 4 * (int)q;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t row = row0 + v;
+        if (row < rows) {
+          const float val = acc[sb][nb][v] * sg;
+          yr[row] = accumulate ? yr[row] + val : val;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace dz

@@ -2,6 +2,7 @@
 // C ABI (Q1_0Matrix::{from_gguf, row_into_slice, matvec_into_slice, matvec_add_into_slice,
 // matvec_multi_into_slice}, Daiza-engine/src/model/weights.rs:83-972).
 #include "runtime.h"
+#include "q1_gemm.h"
 
 #include <cstdarg>
 #include <cstdio>
@@ -241,9 +242,50 @@ int upload_q1_host(const uint8_t* aos, int64_t rows, int64_t cols, Q1Dev* out, s
   return upload_q1_host(aos, rows, cols, out, &owner);
 }
 
+// ------------------------------------------------------------------ N-column products
+
+int packed_x_reserve(Scratch& buf, int n, int64_t K, PackedX* out) {
+  const int Np = (n + kGemmTok - 1) / kGemmTok * kGemmTok;
+  const int64_t Kp = (K + kTileCols - 1) / kTileCols * kTileCols;
+  const size_t half_bytes = (size_t)Np * Kp * 2;
+  const int rc = buf.reserve(2 * half_bytes + (size_t)Np * 4);
+  if (rc) return rc;
+  char* b = static_cast<char*>(buf.ptr);
+  out->xh = reinterpret_cast<uint16_t*>(b);
+  out->xl = reinterpret_cast<uint16_t*>(b + half_bytes);
+  out->sig = reinterpret_cast<float*>(b + 2 * half_bytes);
+  out->Kp = Kp;
+  out->Np = Np;
+  return DZ_OK;
+}
+
+hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const float* w, float eps, const PackedX& p,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(x_pack_kernel, dim3((unsigned)p.Np), dim3(256), 0, s, x, ldx, K, n, w, eps, p.xh, p.xl, p.sig,
+                     p.Kp);
+  return hipGetLastError();
+}
+
+hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
+                          hipStream_t s) {
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmShmem);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  if (W.ntiles * kTileCols != p.Kp || n > p.Np) return hipErrorInvalidValue;
+  GemmX gx{p.xh, p.xl, p.sig, p.Kp};
+  const dim3 grid((unsigned)((W.nrb + 3) / 4), (unsigned)((n + kGemmTok - 1) / kGemmTok));
+  hipLaunchKernelGGL(q1_gemm_kernel, grid, dim3(256), kGemmShmem, s, W.data, W.rows, W.nrb, (int)W.ntiles, gx, n, y,
+                     ldy, accumulate);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ matrix API state
 
-static Scratch g_x, g_y, g_part;
+static Scratch g_x, g_y, g_part, g_pack;
 
 static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* const* y_dev, int accumulate,
                        hipStream_t s) {
@@ -401,6 +443,27 @@ int dz_q1_0_matvec(dz_mat* m, const float* x, float* y, int accumulate) {
 
 int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* const* ys) {
   return matvec_host(mats, n, x, ys, 0);
+}
+
+int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumulate) {
+  if (!m || !x || !y) return set_error(DZ_ERR_TENSOR, "matvec_batch: null pointer");
+  if (n < 1) return set_error(DZ_ERR_TENSOR, "matvec_batch: n = %d", n);
+  int rc = ensure_device();
+  if (rc) return rc;
+  const size_t K = (size_t)m->d.cols, R = (size_t)m->d.rows;
+  PackedX p;
+  if ((rc = packed_x_reserve(g_pack, n, (int64_t)K, &p))) return rc;
+  if ((rc = g_x.reserve((size_t)n * K * 4)) || (rc = g_y.reserve((size_t)n * R * 4))) return rc;
+  hipStream_t s = lib_stream();
+  float* xd = static_cast<float*>(g_x.ptr);
+  float* yd = static_cast<float*>(g_y.ptr);
+  DZ_HIP_CHECK(hipMemcpyAsync(xd, x, (size_t)n * K * 4, hipMemcpyHostToDevice, s));
+  if (accumulate) DZ_HIP_CHECK(hipMemcpyAsync(yd, y, (size_t)n * R * 4, hipMemcpyHostToDevice, s));
+  DZ_HIP_CHECK(launch_x_pack(xd, (int64_t)K, (int64_t)K, n, nullptr, 0.f, p, s));
+  DZ_HIP_CHECK(launch_q1_gemm(m->d, p, n, yd, (int64_t)R, accumulate, s));
+  DZ_HIP_CHECK(hipMemcpyAsync(y, yd, (size_t)n * R * 4, hipMemcpyDeviceToHost, s));
+  DZ_HIP_CHECK(hipStreamSynchronize(s));
+  return DZ_OK;
 }
 
 int dz_q1_0_dequant_rows(dz_mat* m, size_t r0, size_t n, float* out) {

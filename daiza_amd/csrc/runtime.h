@@ -58,4 +58,22 @@ struct ReduceSeg {
 hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const ReduceSeg* segs, int nseg,
                                  int accumulate, hipStream_t s);
 
+// N-column products on the matrix cores (q1_gemm.h): activations packed once per input, then
+// one launch per matrix.
+struct PackedX {
+  uint16_t* xh = nullptr;
+  uint16_t* xl = nullptr;
+  float* sig = nullptr;
+  int64_t Kp = 0;  // padded columns
+  int Np = 0;      // padded tokens (multiple of kGemmTok)
+};
+// Carves a PackedX for n tokens of K columns out of `buf` (grown on demand).
+int packed_x_reserve(Scratch& buf, int n, int64_t K, PackedX* out);
+// x[n][K] (row stride ldx) -> p; RMS-normalised with weight w first when w is non-null.
+hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const float* w, float eps, const PackedX& p,
+                         hipStream_t s);
+// y[n][rows] (row stride ldy) =|+= p · Wᵀ; W.cols must match the packed K.
+hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
+                          hipStream_t s);
+
 }  // namespace dz

@@ -1,0 +1,375 @@
+// batch_kernels.h — the n-token forward (forward_batch, Daiza-engine/src/model/forward.rs:394-1407)
+// outside the projections, which run on the matrix cores (q1_gemm.h).  Activations are token-major
+// [n][width] f32.  Used for prefill (dz_forward_batch) and for speculative verify, where the
+// DeltaNet scan records what a rollback needs instead of writing the state back.
+#pragma once
+#include "model_kernels.h"
+
+namespace dz {
+
+// The 8-lane sum of v within each aligned group of 8 lanes (quad xor 1, quad xor 2, half-row
+// mirror); every lane of the group gets it.
+__device__ __forceinline__ float lane8_sum(float v) {
+  v = dpp_add<0xB1>(v);
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x141>(v);
+  return v;
+}
+
+// h[t] = embedding row of ids[t] (forward.rs:212): the f16 table through the reference's
+// f16_to_f32 (tensor/tensor.rs:62-76), or a Q1_0 table through dequantize_q1_0_row_into
+// (quant.rs:161-194).  Grid n, 256 threads.
+__global__ __launch_bounds__(256) void bt_embed_kernel(const int* __restrict__ ids, int64_t H,
+                                                       const uint16_t* __restrict__ emb_f16,
+                                                       const uint8_t* __restrict__ emb_q1, int emb_ntiles,
+                                                       float* __restrict__ h) {
+  const int t = blockIdx.x;
+  const int tok = ids[t];
+  float* out = h + (size_t)t * H;
+  if (emb_f16) {
+    const uint16_t* row = emb_f16 + (size_t)tok * H;
+    for (int64_t c = threadIdx.x; c < H; c += 256) out[c] = ref_f16_to_f32_dev(row[c]);
+    return;
+  }
+  const int64_t rb = tok / kRowBlock;
+  const unsigned L = (unsigned)(tok % kRowBlock);
+  for (int64_t k = threadIdx.x; k < H; k += 256) {
+    const int tt = (int)(k / kTileCols);
+    const unsigned p = (unsigned)((k % kTileCols) / 8), j = (unsigned)(k % 8), s = L ^ p;
+    const uint8_t* u = emb_q1 + ((size_t)rb * emb_ntiles + tt) * kUnitBytes;
+    const unsigned byte = u[((s >> 4) * 64 + L) * 16 + (s & 15)];
+    const uint16_t* scp = reinterpret_cast<const uint16_t*>(u + kUnitSignBytes);
+    const float scale = ref_f16_to_f32_dev(scp[L * 4 + ((p >> 4) ^ (L >> 4))]);
+    out[k] = ((float)((byte >> j) & 1u) * 2.0f - 1.0f) * scale;
+  }
+}
+
+// Causal conv over the chunk + SiLU (ssm.rs:467-518): out[t][ch] = silu(Σ_tap x[t-3+tap][ch]·w[tap][ch]),
+// fma in tap order (oldest first), x[t'] = in-proj output of token t' for t' >= 0 and the conv
+// ring's entry for the earlier tokens (the token at chunk offset t' < 0 sits in slot
+// (head0 + t') & 3, head0 = slot of token 0).  Thread per (token, channel).
+__global__ __launch_bounds__(256) void bt_conv_kernel(const float* __restrict__ yin, int64_t ldin, int n,
+                                                      const float* __restrict__ ring, int head0,
+                                                      const float* __restrict__ conv_w, int64_t qkvd,
+                                                      float* __restrict__ cout) {
+  const int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (ch >= qkvd || t >= n) return;
+  float o = 0.f;
+#pragma unroll
+  for (int tap = 0; tap < 4; ++tap) {
+    const int tt = t - 3 + tap;
+    const float xv = tt >= 0 ? yin[(size_t)tt * ldin + ch] : ring[(size_t)((head0 + tt) & 3) * qkvd + ch];
+    o = __builtin_fmaf(xv, conv_w[(size_t)tap * qkvd + ch], o);
+  }
+  cout[(size_t)t * qkvd + ch] = siluf_(o);
+}
+
+// Conv ring after tokens [0, t1) of a chunk: the inputs of tokens [t0, t1) (t0 = max(0, t1 - 4))
+// go to their slots (head0 + t) & 3 (ssm.rs:467-470).
+__global__ __launch_bounds__(256) void bt_ring_kernel(const float* __restrict__ yin, int64_t ldin, int t0, int t1,
+                                                      float* __restrict__ ring, int head0, int64_t qkvd) {
+  const int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (ch >= qkvd) return;
+  for (int t = t0; t < t1; ++t) ring[(size_t)((head0 + t) & 3) * qkvd + ch] = yin[(size_t)t * ldin + ch];
+}
+
+// Per-k-head L2 norms of the conv outputs (l2norm_inplace, ssm.rs:76-135; q additionally times
+// 1/sqrt(128), ssm.rs:532-533): qk[t][0 .. kdim) = q, qk[t][kdim .. 2 kdim) = k.  Grid (n, 2 nkh),
+// 128 threads.
+__global__ __launch_bounds__(128) void bt_l2norm_kernel(const float* __restrict__ cout, int64_t qkvd, int nkh,
+                                                        float* __restrict__ qk) {
+  __shared__ float red[2];
+  const int t = blockIdx.x, hh = blockIdx.y;
+  const unsigned tid = threadIdx.x;
+  const int64_t kdim = (int64_t)nkh * 128;
+  const int64_t ch = hh < nkh ? (int64_t)hh * 128 + tid : kdim + (int64_t)(hh - nkh) * 128 + tid;
+  const float v = cout[(size_t)t * qkvd + ch];
+  const float s = wave_sum(v * v);
+  if ((tid & 63u) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
+  qk[(size_t)t * 2 * kdim + ch] = hh < nkh ? (v * inv) * (1.0f / sqrtf(128.0f)) : v * inv;
+}
+
+// Rollback record of a verify chunk for one DeltaNet layer: the decay and the delta of every token
+// (the rank-1 update S <- decay·S + d ⊗ k) and the token's key; replaying the first a of them
+// reproduces the state after a tokens bit for bit.
+struct DnRecord {
+  float* decay;  // [n][nvh]
+  float* d;      // [n][nvh * 128]
+  float* k;      // [n][nkh * 128]
+};
+
+// Gated delta rule over the chunk's tokens in order (ssm_scan_vhead, ssm.rs:153-180; fused form
+// 378-418).  Workgroup (v-head vh, quarter) holds state rows i = quarter·32 + (tid >> 3),
+// columns j = 16·(tid & 7) .. +16 of S[vh][j][i] in registers; the 8 threads of a row sum with DPP.
+// Per token: g = ssm_a·softplus(alpha + dt_bias), decay = exp(g), beta = sigmoid(b); s *= decay;
+// kv = s·k; d = (v_i - kv)·beta; s += d·k; y_i = s·q.  The next token's inputs are loaded while
+// this one computes.  With rec == null the state is written back at the end; otherwise it is left
+// as it was and every token's (decay, d, k) is recorded.
+__global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ yin, int64_t ldin,
+                                                      const float* __restrict__ cout, int64_t qkvd,
+                                                      const float* __restrict__ qk, int n, int nkh, int nvh,
+                                                      int64_t off_a, int64_t off_b, const float* __restrict__ ssm_a,
+                                                      const float* __restrict__ dt_bias, float* __restrict__ state,
+                                                      float* __restrict__ y, DnRecord rec) {
+  constexpr int HD = 128;
+  const unsigned tid = threadIdx.x;
+  const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % nkh;
+  const int i = quarter * 32 + (int)(tid >> 3), js = (int)(tid & 7u);
+  const int64_t kdim = (int64_t)nkh * HD;
+  float* S = state + (size_t)vh * HD * HD;
+  float s[16];
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  const float A = ssm_a[vh], dtb = dt_bias[vh];
+  auto load = [&](int t, float4 (&k4)[4], float4 (&q4)[4], float& v, float& al, float& be) {
+    const float* qr = qk + (size_t)t * 2 * kdim + (size_t)kh * HD + 16 * js;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      q4[c] = *reinterpret_cast<const float4*>(qr + 4 * c);
+      k4[c] = *reinterpret_cast<const float4*>(qr + kdim + 4 * c);
+    }
+    v = cout[(size_t)t * qkvd + 2 * kdim + (int64_t)vh * HD + i];
+    al = yin[(size_t)t * ldin + off_a + vh];
+    be = yin[(size_t)t * ldin + off_b + vh];
+  };
+  float4 kc[4], qc[4];
+  float vc, alc, bec;
+  load(0, kc, qc, vc, alc, bec);
+  for (int t = 0; t < n; ++t) {
+    float4 kn[4], qn[4];
+    float vn, aln, ben;
+    load(t + 1 < n ? t + 1 : t, kn, qn, vn, aln, ben);
+    const float x = alc + dtb;
+    const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
+    const float decay = expf(A * sp);
+    const float beta = sigmoidf_(bec);
+    const float* kf = reinterpret_cast<const float*>(kc);
+    const float* qf = reinterpret_cast<const float*>(qc);
+    float kvp = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      s[jj] *= decay;
+      kvp = __builtin_fmaf(s[jj], kf[jj], kvp);
+    }
+    const float kv = lane8_sum(kvp);
+    const float d = (vc - kv) * beta;
+    float yp = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      s[jj] = __builtin_fmaf(d, kf[jj], s[jj]);
+      yp = __builtin_fmaf(s[jj], qf[jj], yp);
+    }
+    const float yy = lane8_sum(yp);
+    if (js == 0) {
+      y[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = yy;
+      if (rec.d) rec.d[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = d;
+    }
+    if (rec.d && tid == 0) rec.decay[(size_t)t * nvh + vh] = decay;
+    if (rec.d && vh < nkh && quarter == 0 && js == 0) {
+      // the key of k-head vh, written once: rows i < 32 of quarter 0 cover 32 of its 128 columns x 4
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        rec.k[(size_t)t * kdim + (int64_t)vh * HD + 4 * (i & 31) + c] =
+            qk[(size_t)t * 2 * kdim + kdim + (int64_t)vh * HD + 4 * (i & 31) + c];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kc[c] = kn[c];
+      qc[c] = qn[c];
+    }
+    vc = vn;
+    alc = aln;
+    bec = ben;
+  }
+  if (!rec.d) {
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) S[(size_t)(js * 16 + jj) * HD + i] = s[jj];
+  }
+}
+
+// Applies the first a recorded tokens of a verify chunk to the state: s = decay·s, s = fma(d, k, s)
+// per token, the same operations in the same order as the scan, so the result equals a scan over
+// those a tokens.  Grid 4·nvh, 256 threads (the scan's row mapping).
+__global__ __launch_bounds__(256) void bt_commit_state_kernel(float* __restrict__ state, DnRecord rec, int a, int nkh,
+                                                              int nvh) {
+  constexpr int HD = 128;
+  const unsigned tid = threadIdx.x;
+  const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % nkh;
+  const int i = quarter * 32 + (int)(tid >> 3), js = (int)(tid & 7u);
+  float* S = state + (size_t)vh * HD * HD;
+  float s[16];
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  for (int t = 0; t < a; ++t) {
+    const float decay = rec.decay[(size_t)t * nvh + vh];
+    const float d = rec.d[(size_t)t * nvh * HD + (int64_t)vh * HD + i];
+    const float* kr = rec.k + (size_t)t * nkh * HD + (size_t)kh * HD + 16 * js;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) s[jj] *= decay;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) s[jj] = __builtin_fmaf(d, kr[jj], s[jj]);
+  }
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) S[(size_t)(js * 16 + jj) * HD + i] = s[jj];
+}
+
+// Output gate per v-head (ssm_output_gate_avx2, ssm.rs:246-286):
+// g[t][vh·128 + i] = ((y·(1/sqrt(Σy²/128 + eps)))·w_norm[i])·silu(z).  Grid (n, nvh), 128 threads.
+__global__ __launch_bounds__(128) void bt_gate_y_kernel(const float* __restrict__ y, const float* __restrict__ yin,
+                                                        int64_t ldin, int64_t off_z, const float* __restrict__ nw,
+                                                        float eps, int nvh, float* __restrict__ g) {
+  __shared__ float red[2];
+  const int t = blockIdx.x, vh = blockIdx.y;
+  const unsigned tid = threadIdx.x;
+  const int64_t col = (int64_t)vh * 128 + tid;
+  const float v = y[(size_t)t * nvh * 128 + col];
+  const float s = wave_sum(v * v);
+  if ((tid & 63u) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1]) * (1.0f / 128.0f) + eps);
+  const float z = yin[(size_t)t * ldin + off_z + col];
+  g[(size_t)t * nvh * 128 + col] = ((v * inv) * nw[tid]) * siluf_(z);
+}
+
+// Attention inputs of token t at position pos0 + t (attention.rs:87-123): per q-head RMSNorm
+// (q_norm), the reference's partial RoPE (pairs (d, d + rope_dim/2) on d < rope_dim/2, both terms
+// added: rope.rs:205-208), q·1/sqrt(256) -> qb[t][h]; the gate half -> gate[t][h]; per kv-head the
+// same for k (k_norm, no scale) appended to the cache with v.  Grid (n, nq + nkv), 256 threads.
+__global__ __launch_bounds__(256) void bt_attn_prep_kernel(const float* __restrict__ yin, int64_t ldin, int nq,
+                                                           int nkv, const float* __restrict__ q_norm,
+                                                           const float* __restrict__ k_norm, float eps,
+                                                           const float* __restrict__ rope, int rope_dim, int pos0,
+                                                           float* __restrict__ qb, float* __restrict__ gate,
+                                                           float* __restrict__ kcache, float* __restrict__ vcache,
+                                                           int max_ctx) {
+  constexpr int HD = 256;
+  __shared__ float xs[HD];
+  __shared__ float red[4];
+  const int t = blockIdx.x, hh = blockIdx.y;
+  const unsigned tid = threadIdx.x;
+  const float* row = yin + (size_t)t * ldin;
+  const bool isq = hh < nq;
+  const int kvh = hh - nq;
+  const float raw = isq ? row[(size_t)hh * 2 * HD + tid] : row[(size_t)nq * 2 * HD + (size_t)kvh * HD + tid];
+  const float s = wave_sum(raw * raw);
+  if ((tid & 63u) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float ssum = (red[0] + red[1]) + (red[2] + red[3]);
+  const float in = 1.0f / sqrtf(ssum / (float)HD + eps);
+  xs[tid] = (raw * in) * (isq ? q_norm[tid] : k_norm[tid]);
+  __syncthreads();
+  const int half = rope_dim / 2;
+  const int pos = pos0 + t;
+  float v = xs[tid];
+  if ((int)tid < rope_dim) {
+    const float* cs = rope + (size_t)pos * rope_dim;
+    const int dd = (int)tid < half ? (int)tid : (int)tid - half;
+    const float c = cs[dd], sn = cs[half + dd];
+    const float x1 = xs[dd], x2 = xs[dd + half];
+    v = (int)tid < half ? __builtin_fmaf(x1, c, x2 * sn) : __builtin_fmaf(x2, c, x1 * sn);
+  }
+  if (isq) {
+    qb[((size_t)t * nq + hh) * HD + tid] = v * (1.0f / sqrtf((float)HD));
+    gate[((size_t)t * nq + hh) * HD + tid] = row[(size_t)hh * 2 * HD + HD + tid];
+  } else {
+    kcache[((size_t)kvh * max_ctx + pos) * HD + tid] = v;
+    vcache[((size_t)kvh * max_ctx + pos) * HD + tid] =
+        row[(size_t)nq * 2 * HD + (size_t)nkv * HD + (size_t)kvh * HD + tid];
+  }
+}
+
+// Causal GQA attention of token t (position pos0 + t) over cache positions [0, pos0 + t] for the
+// GRP q-heads of kv-head kvh (online softmax, attention.rs:149-199), then o·sigmoid(gate)
+// (attention.rs:202-203) -> ao[t][h·256 ..].  The 4 waves take positions p ≡ wave (mod 4) with
+// their own running (m, l, o) and are merged at the end.  Grid (n, nkv), 256 threads.
+template <int GRP>
+__global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ qb, const float* __restrict__ gate,
+                                                      const float* __restrict__ kcache,
+                                                      const float* __restrict__ vcache, int max_ctx, int nq,
+                                                      int pos0, float* __restrict__ ao) {
+  constexpr int HD = 256;
+  __shared__ float wm[4][GRP], wl[4][GRP];
+  __shared__ float wo[4][GRP][HD];
+  const int t = blockIdx.x, kvh = blockIdx.y;
+  const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const int ctx = pos0 + t + 1;
+  float m[GRP], l[GRP];
+  float4 o[GRP], q4[GRP];
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    m[gi] = -INFINITY;
+    l[gi] = 0.f;
+    o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+    q4[gi] = *reinterpret_cast<const float4*>(qb + ((size_t)t * nq + kvh * GRP + gi) * HD + 4 * lane);
+  }
+  const float* kb = kcache + (size_t)kvh * max_ctx * HD + 4 * lane;
+  const float* vb = vcache + (size_t)kvh * max_ctx * HD + 4 * lane;
+  int p = (int)wave;
+  float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka;
+  if (p < ctx) {
+    ka = *reinterpret_cast<const float4*>(kb + (size_t)p * HD);
+    va = *reinterpret_cast<const float4*>(vb + (size_t)p * HD);
+  }
+  for (; p < ctx; p += 4) {
+    const float4 k4 = ka, v4 = va;
+    if (p + 4 < ctx) {
+      ka = *reinterpret_cast<const float4*>(kb + (size_t)(p + 4) * HD);
+      va = *reinterpret_cast<const float4*>(vb + (size_t)(p + 4) * HD);
+    }
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      float dp = q4[gi].x * k4.x;
+      dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
+      dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
+      dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
+      const float score = wave_sum(dp);
+      const float mn = fmaxf(m[gi], score);
+      const float al = expf(m[gi] - mn), be = expf(score - mn);
+      l[gi] = l[gi] * al + be;
+      o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
+      o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
+      o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
+      o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
+      m[gi] = mn;
+    }
+  }
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    if (lane == 0) {
+      wm[wave][gi] = m[gi];
+      wl[wave][gi] = l[gi];
+    }
+    *reinterpret_cast<float4*>(&wo[wave][gi][4 * lane]) = o[gi];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][gi]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      const float e = wl[w][gi] > 0.f ? expf(wm[w][gi] - M) : 0.f;
+      L = __builtin_fmaf(wl[w][gi], e, L);
+      O = __builtin_fmaf(wo[w][gi][tid], e, O);
+    }
+    const int h = kvh * GRP + gi;
+    const float gt = gate[((size_t)t * nq + h) * HD + tid];
+    ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);
+  }
+}
+
+// SwiGLU (mlp.rs:28-47, swiglu_inplace_simd): s[t][i] = silu(gate[t][i]) · up[t][i], gate rows
+// [0, F) and up rows [F, 2F) of the gate/up product.
+__global__ __launch_bounds__(256) void bt_swiglu_kernel(const float* __restrict__ gu, int64_t F, int n,
+                                                        float* __restrict__ s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (i >= F || t >= n) return;
+  const float* row = gu + (size_t)t * 2 * F;
+  s[(size_t)t * F + i] = siluf_(row[i]) * row[F + i];
+}
+
+}  // namespace dz

@@ -4,6 +4,7 @@
 #include "runtime.h"
 #include "model_kernels.h"
 #include "ptk_kernel.h"
+#include "batch_kernels.h"
 #include "daiza_synth.h"
 
 #include <cmath>
@@ -84,6 +85,23 @@ struct dz_ctx {
     uint64_t gti = 0;             // index of the next token for tags and parity
     const void* kfn = nullptr;
   } ptk;
+  // n-token forward (prefill, speculative verify): activations [cap][width], grown on demand
+  struct {
+    int cap = 0;
+    std::vector<void*> allocs;
+    int* ids = nullptr;
+    float *h = nullptr, *yin = nullptr, *cout = nullptr, *qk = nullptr, *ys = nullptr, *gy = nullptr;
+    float *ygu = nullptr, *sw = nullptr, *qb = nullptr, *gate = nullptr;
+    float* logits = nullptr;  // [logits_rows][vocab]
+    int logits_rows = 0;
+    dz::Scratch pack;
+    // verify records per DeltaNet layer: conv inputs [kv][qkvd] and the scan's rollback record
+    int kv_cap = 0;
+    std::vector<float*> rx;
+    std::vector<dz::DnRecord> rec;
+    int pending = 0;          // tokens of the last verify forward (0: none)
+    int pending_pos = 0;
+  } bt;
   std::vector<void*> allocs;
 };
 
@@ -672,11 +690,14 @@ static int ctx_build_graph(dz_ctx* x) {
 
 namespace dz {
 
+static void bt_release(dz_ctx* x);
+
 static void ctx_release(dz_ctx* x) {
   if (!x) return;
   if (x->gexec) (void)hipGraphExecDestroy(x->gexec);
   if (x->graph) (void)hipGraphDestroy(x->graph);
   if (x->s) (void)hipStreamSynchronize(x->s);
+  bt_release(x);
   for (void* p : x->allocs) (void)hipFree(p);
   if (x->s) (void)hipStreamDestroy(x->s);
   delete x;
@@ -1060,6 +1081,229 @@ static int ptk_feed(dz_ctx* x, const uint32_t* ids, int n) {
   return DZ_OK;
 }
 
+// ---------------------------------------------------------------- n-token forward (host)
+
+static void bt_release(dz_ctx* x) {
+  for (void* p : x->bt.allocs) (void)hipFree(p);
+  x->bt.allocs.clear();
+  x->bt.cap = 0;
+  x->bt.kv_cap = 0;
+  x->bt.logits_rows = 0;
+  x->bt.rx.clear();
+  x->bt.rec.clear();
+  if (x->bt.pack.ptr) (void)hipFree(x->bt.pack.ptr);
+  x->bt.pack = Scratch{};
+}
+
+// Activation buffers for chunks of up to cap tokens.
+static int bt_reserve(dz_ctx* x, int cap) {
+  if (cap <= x->bt.cap) return DZ_OK;
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  const dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  for (void* p : x->bt.allocs) (void)hipFree(p);
+  x->bt.allocs.clear();
+  x->bt.cap = 0;
+  x->bt.kv_cap = 0;
+  x->bt.logits_rows = 0;
+  x->bt.rx.clear();
+  x->bt.rec.clear();
+  const int64_t hd = c.ssm_state, kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd;
+  const int64_t qkvd = 2 * kdim + inner, qd = (int64_t)c.n_head * c.head_dim;
+  int64_t rows_in = 1;
+  for (const LayerDev& l : m->L) rows_in = std::max(rows_in, l.in_proj.rows);
+  const size_t n = (size_t)cap;
+  auto& A = x->bt.allocs;
+  int rc;
+  if ((rc = alloc_t(A, &x->bt.ids, n)) || (rc = alloc_t(A, &x->bt.h, n * c.hidden)) ||
+      (rc = alloc_t(A, &x->bt.yin, n * rows_in)) || (rc = alloc_t(A, &x->bt.cout, n * qkvd)) ||
+      (rc = alloc_t(A, &x->bt.qk, n * 2 * kdim)) || (rc = alloc_t(A, &x->bt.ys, n * inner)) ||
+      (rc = alloc_t(A, &x->bt.gy, n * std::max(inner, qd))) || (rc = alloc_t(A, &x->bt.ygu, n * 2 * c.ffn)) ||
+      (rc = alloc_t(A, &x->bt.sw, n * c.ffn)) || (rc = alloc_t(A, &x->bt.qb, n * qd)) ||
+      (rc = alloc_t(A, &x->bt.gate, n * qd)))
+    return rc;
+  x->bt.cap = cap;
+  return DZ_OK;
+}
+
+static int bt_reserve_logits(dz_ctx* x, int rows) {
+  if (rows <= x->bt.logits_rows) return DZ_OK;
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  int rc = alloc_t(x->bt.allocs, &x->bt.logits, (size_t)rows * x->m->cfg.vocab);
+  if (rc) return rc;
+  x->bt.logits_rows = rows;
+  return DZ_OK;
+}
+
+// Rollback records of a verify chunk of up to k tokens, per DeltaNet layer.
+static int bt_reserve_verify(dz_ctx* x, int k) {
+  if (k <= x->bt.kv_cap) return DZ_OK;
+  const dz_config& c = x->m->cfg;
+  const int64_t hd = c.ssm_state, kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd;
+  const int64_t qkvd = 2 * kdim + inner;
+  x->bt.rx.assign((size_t)x->m->n_ssm, nullptr);
+  x->bt.rec.assign((size_t)x->m->n_ssm, DnRecord{nullptr, nullptr, nullptr});
+  auto& A = x->bt.allocs;
+  int rc;
+  for (int i = 0; i < x->m->n_ssm; ++i) {
+    DnRecord& r = x->bt.rec[(size_t)i];
+    if ((rc = alloc_t(A, &x->bt.rx[(size_t)i], (size_t)k * qkvd)) || (rc = alloc_t(A, &r.decay, (size_t)k * c.ssm_v_heads)) ||
+        (rc = alloc_t(A, &r.d, (size_t)k * inner)) || (rc = alloc_t(A, &r.k, (size_t)k * kdim)))
+      return rc;
+  }
+  x->bt.kv_cap = k;
+  return DZ_OK;
+}
+
+template <class K, class... Args>
+static hipError_t launch(K kfn, dim3 g, dim3 b, hipStream_t s, Args... args) {
+  hipLaunchKernelGGL(kfn, g, b, 0, s, args...);
+  return hipGetLastError();
+}
+
+static hipError_t launch_bt_attn(int grp, dim3 g, hipStream_t s, const float* qb, const float* gate, const float* kc,
+                                 const float* vc, int max_ctx, int nq, int pos0, float* ao) {
+  switch (grp) {
+    case 1: return launch(bt_attn_kernel<1>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 2: return launch(bt_attn_kernel<2>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 3: return launch(bt_attn_kernel<3>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 4: return launch(bt_attn_kernel<4>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 6: return launch(bt_attn_kernel<6>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 8: return launch(bt_attn_kernel<8>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// y[n][W.rows] (=|+=) W · (optionally RMS-normalised) x[n][W.cols].
+static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int n, const float* norm_w, float* y,
+                   int64_t ldy, int accumulate) {
+  PackedX p;
+  int rc = packed_x_reserve(x->bt.pack, n, W.cols, &p);
+  if (rc) return rc;
+  DZ_HIP_CHECK(launch_x_pack(xin, ldx, W.cols, n, norm_w, x->m->cfg.rms_eps, p, x->s));
+  DZ_HIP_CHECK(launch_q1_gemm(W, p, n, y, ldy, accumulate, x->s));
+  return DZ_OK;
+}
+
+// The forward of tokens ids[0..n) (host) at positions pos_host .. pos_host+n-1 (forward_batch,
+// forward.rs:394-1407, with the per-token block order of forward.rs:204-375).  Writes the logits
+// of the last out_rows tokens to bt.logits.  With verify set, the DeltaNet states and conv rings
+// are left as they were and the rollback records are filled instead; the KV cache gets the chunk's
+// entries either way.  Does not move the position.
+static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool verify) {
+  dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  hipStream_t s = x->s;
+  int rc;
+  if ((rc = bt_reserve(x, n)) || (rc = bt_reserve_logits(x, out_rows))) return rc;
+  if (verify && (rc = bt_reserve_verify(x, n))) return rc;
+  for (int i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)c.vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", ids[i], c.vocab);
+  DZ_HIP_CHECK(hipMemcpyAsync(x->bt.ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+  const int p0 = x->pos_host;
+  const int64_t H = c.hidden, hd = c.ssm_state, F = c.ffn;
+  const int64_t kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd, qkvd = 2 * kdim + inner;
+  const int64_t qd = (int64_t)c.n_head * c.head_dim;
+  const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
+  const unsigned nb = (unsigned)n;
+  DZ_HIP_CHECK(launch(bt_embed_kernel, dim3(nb), dim3(256), s, (const int*)x->bt.ids, H, (const uint16_t*)m->emb_f16,
+                      (const uint8_t*)m->emb_q1.data, (int)m->emb_q1.ntiles, x->bt.h));
+  for (size_t li = 0; li < m->L.size(); ++li) {
+    const LayerDev& l = m->L[li];
+    const int64_t ld_in = l.in_proj.rows;
+    if ((rc = bt_gemm(x, l.in_proj, x->bt.h, H, n, l.attn_norm, x->bt.yin, ld_in, 0))) return rc;
+    if (!l.attn) {
+      const int si = l.kind_idx;
+      float* ring = x->conv + (size_t)si * 4 * qkvd;
+      const int head0 = (x->ring_base[(size_t)si] + p0) & 3;
+      const unsigned gch = (unsigned)((qkvd + 255) / 256);
+      DZ_HIP_CHECK(launch(bt_conv_kernel, dim3(gch, nb), dim3(256), s, (const float*)x->bt.yin, ld_in, n,
+                          (const float*)ring, head0, (const float*)l.conv_w, qkvd, x->bt.cout));
+      DnRecord rec{nullptr, nullptr, nullptr};
+      if (verify) {
+        rec = x->bt.rec[(size_t)si];
+        DZ_HIP_CHECK(hipMemcpy2DAsync(x->bt.rx[(size_t)si], (size_t)qkvd * 4, x->bt.yin, (size_t)ld_in * 4,
+                                      (size_t)qkvd * 4, (size_t)n, hipMemcpyDeviceToDevice, s));
+      } else {
+        DZ_HIP_CHECK(launch(bt_ring_kernel, dim3(gch), dim3(256), s, (const float*)x->bt.yin, ld_in, std::max(0, n - 4),
+                            n, ring, head0, qkvd));
+      }
+      DZ_HIP_CHECK(launch(bt_l2norm_kernel, dim3(nb, (unsigned)(2 * c.ssm_k_heads)), dim3(128), s,
+                          (const float*)x->bt.cout, qkvd, (int)c.ssm_k_heads, x->bt.qk));
+      float* state = x->ssm_state + (size_t)si * c.ssm_v_heads * hd * hd;
+      DZ_HIP_CHECK(launch(bt_scan_kernel, dim3((unsigned)(4 * c.ssm_v_heads)), dim3(256), s, (const float*)x->bt.yin,
+                          ld_in, (const float*)x->bt.cout, qkvd, (const float*)x->bt.qk, n, (int)c.ssm_k_heads,
+                          (int)c.ssm_v_heads, qkvd + inner, qkvd + inner + c.ssm_v_heads, (const float*)l.ssm_a,
+                          (const float*)l.dt_bias, state, x->bt.ys, rec));
+      DZ_HIP_CHECK(launch(bt_gate_y_kernel, dim3(nb, (unsigned)c.ssm_v_heads), dim3(128), s, (const float*)x->bt.ys,
+                          (const float*)x->bt.yin, ld_in, qkvd, (const float*)l.ssm_norm, c.rms_eps,
+                          (int)c.ssm_v_heads, x->bt.gy));
+      if ((rc = bt_gemm(x, l.out_proj, x->bt.gy, inner, n, nullptr, x->bt.h, H, 1))) return rc;
+    } else {
+      float* kc = x->kv + (size_t)l.kind_idx * 2 * kvsz;
+      float* vc = kc + kvsz;
+      DZ_HIP_CHECK(launch(bt_attn_prep_kernel, dim3(nb, (unsigned)(c.n_head + c.n_head_kv)), dim3(256), s,
+                          (const float*)x->bt.yin, ld_in, (int)c.n_head, (int)c.n_head_kv, (const float*)l.q_norm,
+                          (const float*)l.k_norm, c.rms_eps, (const float*)x->rope, (int)c.rope_dim, p0, x->bt.qb,
+                          x->bt.gate, kc, vc, (int)c.max_ctx));
+      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, dim3(nb, (unsigned)c.n_head_kv), s, x->bt.qb, x->bt.gate, kc,
+                                  vc, (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy));
+      if ((rc = bt_gemm(x, l.out_proj, x->bt.gy, qd, n, nullptr, x->bt.h, H, 1))) return rc;
+    }
+    // MLP (mlp.rs:28-47): h += W_down (silu(W_gate n) * W_up n), n = rmsnorm(h, post_attention_norm)
+    if ((rc = bt_gemm(x, l.gate_up, x->bt.h, H, n, l.post_norm, x->bt.ygu, 2 * F, 0))) return rc;
+    DZ_HIP_CHECK(launch(bt_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s, (const float*)x->bt.ygu,
+                        F, n, x->bt.sw));
+    if ((rc = bt_gemm(x, l.down, x->bt.sw, F, n, nullptr, x->bt.h, H, 1))) return rc;
+  }
+  // output norm + lm_head for the last out_rows tokens
+  const float* hl = x->bt.h + (size_t)(n - out_rows) * H;
+  if ((rc = bt_gemm(x, m->lm_head, hl, H, out_rows, m->output_norm, x->bt.logits, c.vocab, 0))) return rc;
+  return DZ_OK;
+}
+
+// After a forward of n tokens ids at p0 that is kept: the token log, TokState and the context's
+// logits (the last token's row of bt.logits, row `last_row`) as forward_single_token leaves them.
+static int bt_finish(dz_ctx* x, const uint32_t* ids, int n, int p0, int last_row) {
+  const dz_config& c = x->m->cfg;
+  DZ_HIP_CHECK(hipMemcpyAsync(x->toklog + p0, ids, (size_t)n * 4, hipMemcpyHostToDevice, x->s));
+  TokState st;
+  memset(&st, 0, sizeof st);
+  st.pos = p0 + n - 1;
+  st.token = (int)ids[n - 1];
+  st.pos_next = p0 + n;
+  DZ_HIP_CHECK(hipMemcpyAsync(x->st, &st, sizeof st, hipMemcpyHostToDevice, x->s));
+  DZ_HIP_CHECK(hipMemcpyAsync(x->logits, x->bt.logits + (size_t)last_row * c.vocab, (size_t)c.vocab * 4,
+                              hipMemcpyDeviceToDevice, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));  // the host copies above read caller memory
+  x->pos_host = p0 + n;
+  return DZ_OK;
+}
+
+// DAIZA_BATCH=0 runs forward_batch token by token through the decode path instead.
+static bool batch_wanted() {
+  const char* e = getenv("DAIZA_BATCH");
+  return !(e && e[0] == '0');
+}
+
+// Largest chunk of one n-token forward (activations ~0.3 MB per token at the 27B shape).
+constexpr int kBatchChunk = 1024;
+
+static int bt_prefill(dz_ctx* x, const uint32_t* ids, int n, float* last_logits, float* per_pos) {
+  const size_t V = (size_t)x->m->cfg.vocab;
+  const int chunk = per_pos ? 128 : kBatchChunk;
+  x->bt.pending = 0;
+  for (int i0 = 0; i0 < n; i0 += chunk) {
+    const int k = std::min(chunk, n - i0);
+    const int rows = per_pos ? k : 1;
+    int rc = bt_forward(x, ids + i0, k, rows, false);
+    if (rc || (rc = bt_finish(x, ids + i0, k, x->pos_host, rows - 1))) return rc;
+    if (per_pos) DZ_HIP_CHECK(hipMemcpy(per_pos + (size_t)i0 * V, x->bt.logits, (size_t)k * V * 4, hipMemcpyDeviceToHost));
+  }
+  if (last_logits) DZ_HIP_CHECK(hipMemcpy(last_logits, x->logits, V * 4, hipMemcpyDeviceToHost));
+  return DZ_OK;
+}
+
 }  // namespace dz
 
 extern "C" {
@@ -1162,6 +1406,7 @@ int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float
     return set_error(DZ_ERR_TENSOR, "forward_batch: start_pos %d != context position %d", start_pos, x->pos_host);
   if (x->pos_host + n > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "forward_batch: context full");
   const size_t V = (size_t)x->m->cfg.vocab;
+  if (batch_wanted()) return bt_prefill(x, ids, n, last_logits, per_pos);
   if (x->ptk.on) {
     int rc = ptk_feed(x, ids, n);
     if (rc) return rc;

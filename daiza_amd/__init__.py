@@ -134,6 +134,16 @@ _MODEL_PROTOS = {
     "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
     "dz_ctx_stream": ([_vp], _vp),
     "dz_ctx_token_kernel": ([_vp], ctypes.c_int),
+    "dz_ctx_vocab": ([_vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "dz_verify_forward": ([_vp, _u32p, ctypes.c_int, _f32p], ctypes.c_int),
+    "dz_verify_commit": ([_vp, ctypes.c_int], ctypes.c_int),
+    "dz_lcg_next": ([ctypes.POINTER(ctypes.c_uint64)], ctypes.c_float),
+    "dz_sample": ([_f32p, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_uint64), _u32p], ctypes.c_int),
+    "dz_leviathan_check": ([_f32p, _f32p, ctypes.c_int, ctypes.c_uint32, _vp, ctypes.POINTER(ctypes.c_uint64),
+                            ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "dz_sample_bonus": ([_f32p, _f32p, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_uint64), _u32p], ctypes.c_int),
+    "dz_spec_verify": ([_vp, _u32p, ctypes.c_int, _f32p, _vp, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64),
+                        ctypes.POINTER(ctypes.c_int), _u32p], ctypes.c_int),
 }
 
 EXPORTED_SYMBOLS = [
@@ -268,6 +278,52 @@ class Model:
             pass
 
 
+class SamplingParams(ctypes.Structure):
+    """SamplingParams (sampling.rs:22-32) without the repetition penalties (dz_sampling)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float)]
+
+    def __init__(self, temperature=0.7, top_k=20, top_p=0.95):
+        super().__init__(temperature, top_k, top_p)
+
+
+class LcgRng:
+    """LcgRng (sampling.rs:9-19); the state advances through every sampling call it is passed to."""
+
+    def __init__(self, seed=0xC0FFEE):
+        self.state = ctypes.c_uint64(seed)
+
+    def next_f32(self):
+        return lib().dz_lcg_next(ctypes.byref(self.state))
+
+
+def sample_top_k_top_p(logits, params, rng):
+    """sample_top_k_top_p_into (sampling.rs:144-247)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    out = ctypes.c_uint32()
+    _check(lib().dz_sample(_f(x), x.size, ctypes.byref(params), ctypes.byref(rng.state), ctypes.byref(out)))
+    return out.value
+
+
+def leviathan_check(target, draft, token, params, rng):
+    """leviathan_check (engine.rs:1791-1819)."""
+    t = np.ascontiguousarray(target, np.float32)
+    d = None if draft is None else np.ascontiguousarray(draft, np.float32)
+    acc = ctypes.c_int()
+    _check(lib().dz_leviathan_check(_f(t), _f(d) if d is not None else None, t.size, int(token), ctypes.byref(params),
+                                    ctypes.byref(rng.state), ctypes.byref(acc)))
+    return bool(acc.value)
+
+
+def sample_bonus(target, draft, params, rng):
+    """sample_bonus (engine.rs:1833-1866)."""
+    t = np.ascontiguousarray(target, np.float32)
+    d = np.ascontiguousarray(draft, np.float32)
+    out = ctypes.c_uint32()
+    _check(lib().dz_sample_bonus(_f(t), _f(d), t.size, ctypes.byref(params), ctypes.byref(rng.state),
+                                 ctypes.byref(out)))
+    return out.value
+
+
 class Context:
     """ModelState + ForwardContext (forward.rs:32-131) on the device."""
 
@@ -303,6 +359,26 @@ class Context:
 
     def set_pos(self, pos):
         _check(lib().dz_ctx_set_pos(self._h, int(pos)))
+
+    def verify_forward(self, draft, want_logits=True):
+        """Forward of the drafts without moving the position; per-position logits [k][vocab]."""
+        d = np.ascontiguousarray(draft, np.uint32)
+        out = np.empty((d.size, self.cfg.vocab), np.float32) if want_logits else None
+        _check(lib().dz_verify_forward(self._h, d.ctypes.data_as(_u32p), d.size, _f(out) if want_logits else None))
+        return out
+
+    def verify_commit(self, n_accept):
+        _check(lib().dz_verify_commit(self._h, int(n_accept)))
+
+    def spec_verify(self, draft, draft_logits, params, rng, eos_id=-1):
+        """One speculative step (dz_spec_verify); returns (n_accepted, bonus or None at an accepted EOS)."""
+        d = np.ascontiguousarray(draft, np.uint32)
+        dl = None if draft_logits is None else np.ascontiguousarray(draft_logits, np.float32)
+        na, b = ctypes.c_int(), ctypes.c_uint32()
+        _check(lib().dz_spec_verify(self._h, d.ctypes.data_as(_u32p), d.size, _f(dl) if dl is not None else None,
+                                    ctypes.byref(params), int(eos_id), ctypes.byref(rng.state), ctypes.byref(na),
+                                    ctypes.byref(b)))
+        return na.value, (None if b.value == 0xFFFFFFFF else b.value)
 
     def forward_single_token(self, token, want_logits=True):
         """forward.rs:204; returns (argmax, logits or None)."""

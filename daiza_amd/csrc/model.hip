@@ -100,7 +100,7 @@ struct dz_ctx {
     std::vector<float*> rx;
     std::vector<dz::DnRecord> rec;
     int pending = 0;          // tokens of the last verify forward (0: none)
-    int pending_pos = 0;
+    std::vector<uint32_t> pending_ids;
   } bt;
   std::vector<void*> allocs;
 };
@@ -1280,6 +1280,46 @@ static int bt_finish(dz_ctx* x, const uint32_t* ids, int n, int p0, int last_row
   return DZ_OK;
 }
 
+// Speculative verify, first half: the forward of draft[0..k) at positions pos .. pos+k-1 with
+// every position's logits (bt.logits rows), the DeltaNet states and conv rings untouched and their
+// rollback records kept.  The position does not move until bt_verify_commit.
+static int bt_verify_forward(dz_ctx* x, const uint32_t* draft, int k) {
+  if (x->pos_host + k > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "verify: context full");
+  x->bt.pending = 0;
+  int rc = bt_forward(x, draft, k, k, true);
+  if (rc) return rc;
+  x->bt.pending_ids.assign(draft, draft + k);
+  x->bt.pending = k;
+  return DZ_OK;
+}
+
+// Second half: keeps the first a drafts (0 <= a <= k) as if they alone had been forwarded: each
+// DeltaNet layer replays a recorded updates onto its state and takes their conv inputs into its
+// ring; the KV entries beyond pos + a are dropped by the position; the context's logits become
+// those after draft a-1 (unchanged for a = 0).
+static int bt_verify_commit(dz_ctx* x, int a) {
+  const int k = x->bt.pending;
+  if (a < 0 || a > k) return set_error(DZ_ERR_TENSOR, "verify commit: %d of %d drafts", a, k);
+  x->bt.pending = 0;
+  if (a == 0) return DZ_OK;
+  const dz_model* m = x->m;
+  const dz_config& c = m->cfg;
+  const int64_t hd = c.ssm_state, kdim = (int64_t)c.ssm_k_heads * hd, inner = (int64_t)c.ssm_v_heads * hd;
+  const int64_t qkvd = 2 * kdim + inner;
+  const int p0 = x->pos_host;
+  for (const LayerDev& l : m->L) {
+    if (l.attn) continue;
+    const int si = l.kind_idx;
+    DZ_HIP_CHECK(launch(bt_commit_state_kernel, dim3((unsigned)(4 * c.ssm_v_heads)), dim3(256), x->s,
+                        x->ssm_state + (size_t)si * c.ssm_v_heads * hd * hd, x->bt.rec[(size_t)si], a,
+                        (int)c.ssm_k_heads, (int)c.ssm_v_heads));
+    DZ_HIP_CHECK(launch(bt_ring_kernel, dim3((unsigned)((qkvd + 255) / 256)), dim3(256), x->s,
+                        (const float*)x->bt.rx[(size_t)si], qkvd, std::max(0, a - 4), a,
+                        x->conv + (size_t)si * 4 * qkvd, (x->ring_base[(size_t)si] + p0) & 3, qkvd));
+  }
+  return bt_finish(x, x->bt.pending_ids.data(), a, p0, a - 1);
+}
+
 // DAIZA_BATCH=0 runs forward_batch token by token through the decode path instead.
 static bool batch_wanted() {
   const char* e = getenv("DAIZA_BATCH");
@@ -1298,9 +1338,11 @@ static int bt_prefill(dz_ctx* x, const uint32_t* ids, int n, float* last_logits,
     const int rows = per_pos ? k : 1;
     int rc = bt_forward(x, ids + i0, k, rows, false);
     if (rc || (rc = bt_finish(x, ids + i0, k, x->pos_host, rows - 1))) return rc;
-    if (per_pos) DZ_HIP_CHECK(hipMemcpy(per_pos + (size_t)i0 * V, x->bt.logits, (size_t)k * V * 4, hipMemcpyDeviceToHost));
+    if (per_pos)
+      DZ_HIP_CHECK(hipMemcpyAsync(per_pos + (size_t)i0 * V, x->bt.logits, (size_t)k * V * 4, hipMemcpyDeviceToHost, x->s));
   }
-  if (last_logits) DZ_HIP_CHECK(hipMemcpy(last_logits, x->logits, V * 4, hipMemcpyDeviceToHost));
+  if (last_logits) DZ_HIP_CHECK(hipMemcpyAsync(last_logits, x->logits, V * 4, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
   return DZ_OK;
 }
 
@@ -1362,6 +1404,7 @@ int dz_ctx_free(dz_ctx* x) {
 
 int dz_ctx_reset(dz_ctx* x) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  x->bt.pending = 0;
   return ctx_zero_state(x);
 }
 
@@ -1373,6 +1416,7 @@ int dz_ctx_token_kernel(const dz_ctx* x) { return x && x->ptk.on ? 1 : 0; }
 
 int dz_forward_token(dz_ctx* x, uint32_t token, float* logits, uint32_t* argmax) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  x->bt.pending = 0;
   if (x->ptk.on) {
     int rc = ptk_feed(x, &token, 1);
     if (rc || (rc = ptk_run(x, 1, 1, false))) return rc;
@@ -1405,6 +1449,7 @@ int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float
   if (start_pos != x->pos_host)
     return set_error(DZ_ERR_TENSOR, "forward_batch: start_pos %d != context position %d", start_pos, x->pos_host);
   if (x->pos_host + n > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "forward_batch: context full");
+  x->bt.pending = 0;
   const size_t V = (size_t)x->m->cfg.vocab;
   if (batch_wanted()) return bt_prefill(x, ids, n, last_logits, per_pos);
   if (x->ptk.on) {
@@ -1436,6 +1481,7 @@ int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float
 int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_tokens) {
   if (!x || !out_tokens) return set_error(DZ_ERR_MODEL, "null argument");
   if (n < 1) return DZ_OK;
+  x->bt.pending = 0;
   const int p0 = x->pos_host;
   if (x->ptk.on) {
     int rc = ptk_feed(x, &first_token, 1);
@@ -1449,6 +1495,33 @@ int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_token
   if ((rc = ctx_peek_argmax(x))) return rc;
   DZ_HIP_CHECK(hipMemcpyAsync(out_tokens, x->toklog + p0 + 1, (size_t)n * 4, hipMemcpyDeviceToHost, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+int dz_verify_forward(dz_ctx* x, const uint32_t* draft, int k, float* per_pos_logits) {
+  if (!x || !draft) return set_error(DZ_ERR_MODEL, "null argument");
+  if (k < 1) return set_error(DZ_ERR_TENSOR, "verify: %d drafts", k);
+  if (k > kBatchChunk) return set_error(DZ_ERR_TENSOR, "verify: %d drafts (at most %d)", k, kBatchChunk);
+  int rc = bt_verify_forward(x, draft, k);
+  if (rc) return rc;
+  // the context's stream is non-blocking: copy on it, then wait
+  if (per_pos_logits)
+    DZ_HIP_CHECK(hipMemcpyAsync(per_pos_logits, x->bt.logits, (size_t)k * x->m->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                                x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+int dz_verify_commit(dz_ctx* x, int n_accept) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (x->bt.pending == 0 && n_accept == 0) return DZ_OK;
+  if (x->bt.pending == 0) return set_error(DZ_ERR_TENSOR, "verify commit without a verify forward");
+  return bt_verify_commit(x, n_accept);
+}
+
+int dz_ctx_vocab(const dz_ctx* x, int* vocab) {
+  if (!x || !vocab) return set_error(DZ_ERR_MODEL, "null argument");
+  *vocab = x->m->cfg.vocab;
   return DZ_OK;
 }
 
@@ -1548,6 +1621,7 @@ int dz_ctx_kv_len(dz_ctx* x, int layer) {
 
 int dz_kv_truncate(dz_ctx* x, int len) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  x->bt.pending = 0;
   if (len >= x->pos_host) return DZ_OK;  // KvCache::truncate keeps longer requests as no-ops
   if (len < 0) return set_error(DZ_ERR_TENSOR, "truncate to %d", len);
   return ctx_set_pos_dev(x, len);
@@ -1555,6 +1629,7 @@ int dz_kv_truncate(dz_ctx* x, int len) {
 
 int dz_ctx_set_pos(dz_ctx* x, int pos) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  x->bt.pending = 0;
   if (pos < 0 || pos >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "pos %d out of [0, max_ctx)", pos);
   // ring heads are stored relative to pos: keep each layer's physical head unchanged
   const int old = x->pos_host;

@@ -166,6 +166,57 @@ int dz_decode_greedy(dz_ctx* c, uint32_t first_token, int n, uint32_t* out_token
 
 /* Last computed logits (vocab f32) of the context. */
 int dz_ctx_logits(dz_ctx* c, float* logits);
+/* Vocabulary size of the context's model (the length of a logits row). */
+int dz_ctx_vocab(const dz_ctx* c, int* vocab);
+
+/* ---- speculative verify ----
+ * The reference verifies drafts one forward_single_token at a time and forwards only accepted
+ * ones (engine.rs:1255-1470); here the k drafts run in one n-token forward and the accepted
+ * prefix is kept afterwards.
+ *
+ * dz_verify_forward: forward of draft[0..k) at positions pos .. pos+k-1 (forward_batch with
+ * per_pos_logits, forward.rs:1319-1337).  per_pos_logits_or_null[i] (k rows of vocab) = logits after
+ * draft[i].  The DeltaNet states and conv rings are left unchanged and per-token rollback records
+ * are kept; the position does not move.
+ * dz_verify_commit: keeps the first n_accept drafts (0..k) exactly as if only they had been
+ * forwarded (DeltaNet updates replayed in the scan's order, conv rings, KV length via the position
+ * as KvCache::truncate does, kv_cache.rs:119-130; the context's logits = after draft n_accept-1).
+ * Any other forward, reset, set_pos or truncate discards a pending verify. */
+int dz_verify_forward(dz_ctx* c, const uint32_t* draft, int k, float* per_pos_logits_or_null);
+int dz_verify_commit(dz_ctx* c, int n_accept);
+
+/* SamplingParams (sampling.rs:22-32) without the repetition penalties, which the verify path does
+ * not apply by default (engine.rs:1332). */
+typedef struct dz_sampling {
+  float temperature;  /* <= 0: greedy */
+  int32_t top_k;
+  float top_p;
+} dz_sampling;
+
+/* LcgRng::next_f32 (sampling.rs:14-18); *state is the generator state (seeded e.g. 0xC0FFEE). */
+float dz_lcg_next(uint64_t* state);
+/* sample_top_k_top_p_into (sampling.rs:144-247) over logits[n]. */
+int dz_sample(const float* logits, int n, const dz_sampling* params, uint64_t* rng_state, uint32_t* out);
+/* leviathan_check (engine.rs:1791-1819): greedy = argmax(target) == token; else accept iff
+ * u < p[token]/q[token] of the untempered softmaxes (softmax_pair_single_avx2, simd_exp.rs:656-767). */
+int dz_leviathan_check(const float* target, const float* draft, int n, uint32_t token, const dz_sampling* params,
+                       uint64_t* rng_state, int* accepted);
+/* sample_bonus (engine.rs:1833-1866): sample from norm(max(0, p - q)) (residual_max_zero_sum_avx2,
+ * simd_exp.rs:605-642), or from the target when the residual has no mass. */
+int dz_sample_bonus(const float* target, const float* draft, int n, const dz_sampling* params, uint64_t* rng_state,
+                    uint32_t* out);
+/*
+ * One speculative step: verify draft[0..k) against the context (its logits predict draft[0]) with
+ * Leviathan acceptance in order, then keep the accepted prefix.  On the first rejection the bonus
+ * is sample_bonus of that position's target and draft logits (greedy: the target's argmax); with
+ * every draft accepted it is sampled from the logits after the last draft.  An accepted eos_id
+ * (>= 0) ends the step unforwarded with *bonus = 0xFFFFFFFF, as the reference stops there.  The
+ * bonus is not forwarded (the caller's next forward takes it, as the reference's Phase 3 does).
+ * draft_logits: [k][vocab] (may be NULL when greedy).  Random draws follow the reference's order:
+ * one per verified draft, one for the bonus.
+ */
+int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_logits, const dz_sampling* params,
+                   int32_t eos_id, uint64_t* rng_state, int* n_accepted, uint32_t* bonus);
 
 /* ---- state access (ModelState fields; layouts are the reference's) ---- */
 /* SSM layer state S[v_heads][128 (v index i)][128 (k index j)] (cache/ssm_state.rs:10-39) and

@@ -58,6 +58,18 @@ def lib():
                                         ctypes.c_float, ctypes.c_float, ctypes.c_int]
         L.or_lcg_next.restype = ctypes.c_float
         L.or_lcg_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.or_softmax_inplace.argtypes = [f32p, ctypes.c_size_t]
+        L.or_softmax_pair_single.argtypes = [f32p, f32p, ctypes.c_size_t, ctypes.c_size_t,
+                                             ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+        L.or_sample_top_k_top_p.restype = ctypes.c_uint32
+        L.or_sample_top_k_top_p.argtypes = [f32p, ctypes.c_size_t, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                            ctypes.POINTER(ctypes.c_uint64)]
+        L.or_sample_bonus.restype = ctypes.c_uint32
+        L.or_sample_bonus.argtypes = [f32p, f32p, ctypes.c_size_t, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                      ctypes.POINTER(ctypes.c_uint64)]
+        L.or_leviathan_check.restype = ctypes.c_int
+        L.or_leviathan_check.argtypes = [f32p, f32p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_float,
+                                         ctypes.POINTER(ctypes.c_uint64)]
         L.or_model_synth.restype = ctypes.c_void_p
         L.or_model_synth.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int]
         L.or_model_free.argtypes = [ctypes.c_void_p]
@@ -146,6 +158,47 @@ def matvec_scalar(aos, rows, cols, x, y=None, accumulate=False):
         y = np.zeros(rows, np.float32)
     lib().or_matvec_scalar(_u8(aos), rows, cols, _f(x), _f(y), int(accumulate))
     return y
+
+
+class Rng:
+    """LcgRng state (sampling.rs:9-19) shared by the sampling helpers below."""
+
+    def __init__(self, seed=0xC0FFEE):
+        self.state = ctypes.c_uint64(seed)
+
+    def next_f32(self):
+        return lib().or_lcg_next(ctypes.byref(self.state))
+
+
+def softmax(x):
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().or_softmax_inplace(_f(y), y.size)
+    return y
+
+
+def softmax_pair_single(t, d, idx):
+    t = np.ascontiguousarray(t, np.float32)
+    d = np.ascontiguousarray(d, np.float32)
+    p, q = ctypes.c_float(), ctypes.c_float()
+    lib().or_softmax_pair_single(_f(t), _f(d), t.size, idx, ctypes.byref(p), ctypes.byref(q))
+    return p.value, q.value
+
+
+def sample_top_k_top_p(logits, temperature, top_k, top_p, rng):
+    x = np.ascontiguousarray(logits, np.float32)
+    return lib().or_sample_top_k_top_p(_f(x), x.size, temperature, top_k, top_p, ctypes.byref(rng.state))
+
+
+def sample_bonus(target, draft, temperature, top_k, top_p, rng):
+    t = np.ascontiguousarray(target, np.float32)
+    d = np.ascontiguousarray(draft, np.float32)
+    return lib().or_sample_bonus(_f(t), _f(d), t.size, temperature, top_k, top_p, ctypes.byref(rng.state))
+
+
+def leviathan_check(target, draft, token, temperature, rng):
+    t = np.ascontiguousarray(target, np.float32)
+    d = np.ascontiguousarray(draft if draft is not None else target, np.float32)
+    return bool(lib().or_leviathan_check(_f(t), _f(d), t.size, token, temperature, ctypes.byref(rng.state)))
 
 
 def vec_op(name, x):

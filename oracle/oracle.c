@@ -519,6 +519,189 @@ float or_lcg_next(uint64_t* state) {
   return (float)bits / (float)0x1000000;
 }
 
+/* ------------------------------------------------------------------ sampling (speculative verify) */
+
+/* hmax_ps (simd_exp.rs:375-383) */
+static inline float hmax_ps(__m256 v) {
+  __m128 m = _mm_max_ps(_mm256_extractf128_ps(v, 1), _mm256_castps256_ps128(v));
+  __m128 s = _mm_max_ps(m, _mm_movehdup_ps(m));
+  return _mm_cvtss_f32(_mm_max_ss(s, _mm_movehl_ps(s, s)));
+}
+
+/* softmax_inplace (math/softmax.rs:15-80): AVX2 max, exp_ps + sum, multiply by 1/sum */
+void or_softmax_inplace(float* x, size_t n) {
+  size_t n8 = n / 8 * 8, i;
+  __m256 mv = _mm256_set1_ps(x[0]);
+  for (i = 0; i < n8; i += 8) mv = _mm256_max_ps(mv, _mm256_loadu_ps(x + i));
+  float mx = hmax_ps(mv);
+  for (; i < n; ++i)
+    if (x[i] > mx) mx = x[i];
+  __m256 mxv = _mm256_set1_ps(mx), sv = _mm256_setzero_ps();
+  for (i = 0; i < n8; i += 8) {
+    __m256 e = exp_ps(_mm256_sub_ps(_mm256_loadu_ps(x + i), mxv));
+    _mm256_storeu_ps(x + i, e);
+    sv = _mm256_add_ps(sv, e);
+  }
+  float sum = hsum_ps(sv);
+  for (i = n8; i < n; ++i) {
+    x[i] = expf(x[i] - mx);
+    sum += x[i];
+  }
+  float inv = 1.0f / sum;
+  __m256 iv = _mm256_set1_ps(inv);
+  for (i = 0; i < n8; i += 8) _mm256_storeu_ps(x + i, _mm256_mul_ps(_mm256_loadu_ps(x + i), iv));
+  for (i = n8; i < n; ++i) x[i] *= inv;
+}
+
+/* softmax_pair_single_avx2 (simd_exp.rs:656-767) */
+void or_softmax_pair_single(const float* t, const float* d, size_t n, size_t idx, float* p, float* q) {
+  size_t n8 = n / 8 * 8, i;
+  __m256 tm = _mm256_set1_ps(t[0]), dm = _mm256_set1_ps(d[0]);
+  for (i = 0; i < n8; i += 8) {
+    tm = _mm256_max_ps(tm, _mm256_loadu_ps(t + i));
+    dm = _mm256_max_ps(dm, _mm256_loadu_ps(d + i));
+  }
+  float tmax = hmax_ps(tm), dmax = hmax_ps(dm);
+  for (; i < n; ++i) {
+    if (t[i] > tmax) tmax = t[i];
+    if (d[i] > dmax) dmax = d[i];
+  }
+  __m256 tmv = _mm256_set1_ps(tmax), dmv = _mm256_set1_ps(dmax), ts = _mm256_setzero_ps(), ds = _mm256_setzero_ps();
+  float ti = 0.f, di = 0.f;
+  for (i = 0; i < n8; i += 8) {
+    __m256 te = exp_ps(_mm256_sub_ps(_mm256_loadu_ps(t + i), tmv));
+    __m256 de = exp_ps(_mm256_sub_ps(_mm256_loadu_ps(d + i), dmv));
+    ts = _mm256_add_ps(ts, te);
+    ds = _mm256_add_ps(ds, de);
+    if (idx >= i && idx < i + 8) {
+      float bt[8], bd[8];
+      _mm256_storeu_ps(bt, te);
+      _mm256_storeu_ps(bd, de);
+      ti = bt[idx - i];
+      di = bd[idx - i];
+    }
+  }
+  float tsum = hsum_ps(ts), dsum = hsum_ps(ds);
+  for (i = n8; i < n; ++i) {
+    float te = expf(t[i] - tmax), de = expf(d[i] - dmax);
+    tsum += te;
+    dsum += de;
+    if (i == idx) {
+      ti = te;
+      di = de;
+    }
+  }
+  if (tsum <= 0.f) tsum = 1.f;
+  if (dsum <= 0.f) dsum = 1.f;
+  *p = ti / tsum;
+  *q = di / dsum;
+}
+
+/* sample_top_k_top_p_into (math/sampling.rs:144-247).  The reference orders the top k with
+ * select_nth_unstable + sort (tie order unspecified); ties here go to the lower index. */
+uint32_t or_sample_top_k_top_p(const float* logits, size_t n, float temperature, int top_k, float top_p,
+                               uint64_t* rng) {
+  if (temperature <= 0.f) return (uint32_t)or_argmax(logits, n);
+  float inv_t = 1.0f / temperature;
+  size_t k = (size_t)top_k < n ? (size_t)top_k : n;
+  uint32_t* top = (uint32_t*)malloc(k * sizeof(uint32_t));
+  float* val = (float*)malloc(k * sizeof(float));
+  size_t have = 0;
+  for (size_t i = 0; i < n; ++i) {
+    float v = logits[i] * inv_t;  /* scale_avx2: one multiply per element */
+    if (have == k && !(v > val[k - 1])) continue;
+    size_t j = have < k ? have++ : k - 1;
+    while (j > 0 && v > val[j - 1]) {
+      val[j] = val[j - 1];
+      top[j] = top[j - 1];
+      --j;
+    }
+    val[j] = v;
+    top[j] = (uint32_t)i;
+  }
+  float mx = -INFINITY;
+  for (size_t j = 0; j < k; ++j)
+    if (val[j] > mx) mx = val[j];
+  float* pr = (float*)malloc(k * sizeof(float));
+  float sum = 0.f;
+  for (size_t j = 0; j < k; ++j) pr[j] = expf(val[j] - mx);
+  for (size_t j = 0; j < k; ++j) sum += pr[j];
+  float inv = 1.0f / sum;
+  for (size_t j = 0; j < k; ++j) pr[j] *= inv;
+  float cum = 0.f;
+  size_t cut = k;
+  for (size_t j = 0; j < k; ++j) {
+    cum += pr[j];
+    if (cum >= top_p) {
+      cut = j + 1;
+      break;
+    }
+  }
+  float ns = 0.f;
+  for (size_t j = 0; j < cut; ++j) ns += pr[j];
+  float ninv = 1.0f / ns;
+  for (size_t j = 0; j < cut; ++j) pr[j] *= ninv;
+  float r = or_lcg_next(rng), acc = 0.f;
+  uint32_t chosen = top[0];
+  for (size_t j = 0; j < cut; ++j) {
+    acc += pr[j];
+    if (r <= acc) {
+      chosen = top[j];
+      break;
+    }
+  }
+  free(top);
+  free(val);
+  free(pr);
+  return chosen;
+}
+
+/* sample_bonus (Daiza-runtime/src/engine.rs:1833-1866) with residual_max_zero_sum_avx2
+ * (simd_exp.rs:605-642) */
+uint32_t or_sample_bonus(const float* target, const float* draft, size_t n, float temperature, int top_k,
+                         float top_p, uint64_t* rng) {
+  float* p = (float*)malloc(n * sizeof(float));
+  float* q = (float*)malloc(n * sizeof(float));
+  memcpy(p, target, n * sizeof(float));
+  memcpy(q, draft, n * sizeof(float));
+  or_softmax_inplace(p, n);
+  or_softmax_inplace(q, n);
+  size_t n8 = n / 8 * 8, i;
+  __m256 sv = _mm256_setzero_ps(), z = _mm256_setzero_ps();
+  for (i = 0; i < n8; i += 8) {
+    __m256 r = _mm256_max_ps(_mm256_sub_ps(_mm256_loadu_ps(p + i), _mm256_loadu_ps(q + i)), z);
+    _mm256_storeu_ps(p + i, r);
+    sv = _mm256_add_ps(sv, r);
+  }
+  float sum = hsum_ps(sv);
+  for (i = n8; i < n; ++i) {
+    float r = fmaxf(p[i] - q[i], 0.f);
+    p[i] = r;
+    sum += r;
+  }
+  uint32_t out;
+  if (sum <= 1e-12f) {
+    out = or_sample_top_k_top_p(target, n, temperature, top_k, top_p, rng);
+  } else {
+    float inv = 1.0f / sum;
+    for (i = 0; i < n; ++i) p[i] = logf(p[i] * inv);
+    out = or_sample_top_k_top_p(p, n, temperature, top_k, top_p, rng);
+  }
+  free(p);
+  free(q);
+  return out;
+}
+
+/* leviathan_check (Daiza-runtime/src/engine.rs:1791-1819) */
+int or_leviathan_check(const float* target, const float* draft, size_t n, uint32_t token, float temperature,
+                       uint64_t* rng) {
+  if (temperature <= 0.f) return (uint32_t)or_argmax(target, n) == token;
+  float p, q;
+  or_softmax_pair_single(target, draft, n, token, &p, &q);
+  float r = q > 1e-12f ? p / q : 0.f;
+  return or_lcg_next(rng) < r;
+}
+
 /* ------------------------------------------------------------------ model */
 
 typedef struct {

@@ -55,6 +55,15 @@ void or_ssm_scan_vhead(float* s, float* y, const float* q, const float* k, const
                        float alpha_vh, float beta_vh, float dt_bias_vh, int head_dim);
 /* LcgRng::next_f32 (sampling.rs:9-19); returns the value and advances *state */
 float or_lcg_next(uint64_t* state);
+/* speculative-verify sampling (math/softmax.rs:15-80, simd_exp.rs:605-767, sampling.rs:144-247,
+ * Daiza-runtime/src/engine.rs:1791-1866) */
+void or_softmax_inplace(float* x, size_t n);
+void or_softmax_pair_single(const float* t, const float* d, size_t n, size_t idx, float* p, float* q);
+uint32_t or_sample_top_k_top_p(const float* logits, size_t n, float temperature, int top_k, float top_p, uint64_t* rng);
+uint32_t or_sample_bonus(const float* target, const float* draft, size_t n, float temperature, int top_k,
+                         float top_p, uint64_t* rng);
+int or_leviathan_check(const float* target, const float* draft, size_t n, uint32_t token, float temperature,
+                       uint64_t* rng);
 
 /* synthetic inputs of daiza_synth.h, exported for tests */
 void or_synth_q1_0_rows(uint64_t seed, int kind, int layer, uint64_t cols, uint64_t r0, uint64_t r1, uint8_t* out);

@@ -5,10 +5,15 @@ attention layers), random Q1_0 weights from include/daiza_synth.h, f16 embedding
 prefill of uniform-random ids, then `--steps` timed greedy decode tokens after `--warmup`
 untimed ones.  One step = one token through the whole stack (forward_single_token).
 
-Prints one JSON line.  `roofline` is the dominant kernel, the Q1_0 LUT GEMV, timed per launch
-with HIP events on its stream at the config-1 shape (17408 x 5120, 32 distinct matrices, more
-than the 256 MB Infinity Cache).  `cpu_baseline` is the CPU oracle (oracle/, a C restatement of
-the reference's multithreaded AVX2 path) on a bounded sample of the same workload.
+Prints one JSON line.  `roofline` is the dominant kernel of the timed decode, the persistent token
+kernel (one cooperative launch runs all timed tokens), timed with HIP events on the context's
+stream: algorithmic bytes per launch (every token's Q1_0 weights, KV-cache reads and appends,
+DeltaNet state read and write, conv ring, embedding row, logits) over the launch's duration.
+`roofline_gemv` is the Q1_0 LUT GEMV alone at the config-1 shape (17408 x 5120, 32 distinct
+matrices, more than the 256 MB Infinity Cache), timed per launch.  `config5` times speculative
+verify (k = 8 drafts at context 8192) after a batched prefill to that context.
+`cpu_baseline` is the CPU oracle (oracle/, a C restatement of the reference's multithreaded AVX2
+path) on a bounded sample of the same workload.
 """
 import argparse
 import ctypes
@@ -26,6 +31,8 @@ METRIC = "batch-1 decode tok/s (27B-shape Q1_0 synth); Q1_0 GEMV HBM GB/s vs pea
 PEAK_GBS = 8000.0
 SEED = 0xDA1A0004
 PREFILL = 1024
+VERIFY_CTX = 8192
+VERIFY_K = 8
 
 
 def log(msg):
@@ -102,17 +109,79 @@ def bench_copy(H, nbytes, reps=32):
     return {"bytes": nbytes, "us": us, "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
-def measured_traffic():
-    """HBM bytes per GEMV launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
-    WRITE_SIZE of the config-1 GEMV, each scaled by the same counter on a copy of known size),
-    or None when that summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_config1_pmc.txt")
+def measured_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary under profiles/ (FETCH_SIZE
+    and WRITE_SIZE, each scaled by the same counter on a copy of known size), or None when that
+    summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):
         if line.startswith("traffic_bytes_per_launch:"):
             return int(float(line.split(":", 1)[1]))
     return None
+
+
+def decode_bytes(cfg, wbytes, pos0, n):
+    """Algorithmic HBM bytes of n decode tokens at positions pos0 .. pos0+n-1: per token the Q1_0
+    weights, the attention layers' KV reads over the context and K/V appends, the DeltaNet
+    states read and written, the conv ring (3 history rows read, 1 written) and conv weights, the
+    embedding row and the logits."""
+    n_attn = sum(1 for i in range(cfg.n_layers) if (i + 1) % cfg.full_attn_interval == 0)
+    n_ssm = cfg.n_layers - n_attn
+    kv_row = 2 * cfg.n_head_kv * cfg.head_dim * 4           # K and V of one position, one layer
+    state = cfg.ssm_v_heads * cfg.ssm_state * cfg.ssm_state * 4
+    qkvd = cfg.qkv_dim
+    per_tok = (wbytes + n_ssm * (2 * state + 4 * qkvd * 4 + 4 * qkvd * 4) + n_attn * kv_row
+               + cfg.hidden * 2 + cfg.vocab * 4)
+    ctx_rows = sum(pos0 + i + 1 for i in range(n))            # positions read, summed over tokens
+    return n * per_tok + n_attn * kv_row * ctx_rows
+
+
+def bench_verify(dz, H, ctx, cfg, decode_ms_per_tok, reps=8):
+    """k = 8 uniform-random drafts verified in one forward at context 8192.
+    Times dz_verify_forward (+ a commit of 0, so every rep sees the same context) with HIP events
+    on the context's stream, and the full dz_spec_verify step at temperature 0.7 (Leviathan and
+    bonus sampling on the host, logits copied back) by wall clock."""
+    rng = np.random.default_rng(SEED & 0xFFF)
+    t0 = time.time()
+    while ctx.pos < VERIFY_CTX:
+        n = min(1024, VERIFY_CTX - ctx.pos)
+        ctx.forward_batch(rng.integers(0, cfg.vocab, n).astype(np.uint32))
+    fill_s = time.time() - t0
+    stream = ctypes.c_void_p(ctx.stream())
+    ev = Events(H, 2)
+    drafts = [rng.integers(0, cfg.vocab, VERIFY_K).astype(np.uint32) for _ in range(reps + 1)]
+    ctx.verify_forward(drafts[0], want_logits=False)
+    ctx.verify_commit(0)
+    H.hipDeviceSynchronize()
+    H.hipEventRecord(ev.ev[0], stream)
+    for d in drafts[1:]:
+        ctx.verify_forward(d, want_logits=False)
+        ctx.verify_commit(0)
+    H.hipEventRecord(ev.ev[1], stream)
+    H.hipEventSynchronize(ev.ev[1])
+    fwd_ms = ev.elapsed_ms(0, 1) / reps
+    params = dz.SamplingParams(0.7, 20, 0.95)
+    lcg = dz.LcgRng(0xC0FFEE)
+    dl = rng.standard_normal((VERIFY_K, cfg.vocab)).astype(np.float32)
+    p0 = ctx.pos
+    t0 = time.perf_counter()
+    acc = 0
+    for d in drafts[1:]:
+        na, _ = ctx.spec_verify(d, dl, params, lcg)
+        acc += na
+    step_ms = 1e3 * (time.perf_counter() - t0) / reps
+    return {
+        "context": p0, "k": VERIFY_K, "temperature": 0.7,
+        "verify_forward_ms": round(fwd_ms, 3),
+        "spec_verify_step_ms": round(step_ms, 3),
+        "sequential_verify_ms": round(VERIFY_K * decode_ms_per_tok, 3),
+        "accepted_total": acc,
+        "prefill_to_ctx_s": round(fill_s, 2),
+        "note": "sequential_verify_ms = k forwards of one token on this build's decode path, the reference's "
+                "verify loop (engine.rs:1255-1470); spec_verify_step_ms includes the logits copy and host sampling",
+    }
 
 
 def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
@@ -203,8 +272,9 @@ def main():
     ap.add_argument("--prefill", type=int, default=PREFILL)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--only", choices=["all", "gemv"], default="all",
-                    help="gemv: only the config-1 GEMV and the copy reference (for PMC passes)")
+    ap.add_argument("--only", choices=["all", "gemv", "decode"], default="all",
+                    help="gemv: only the config-1 GEMV and the copy reference; decode: only the prefill and "
+                         "the timed decode (both for PMC passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs the decode loop on a single GPU "
@@ -223,7 +293,7 @@ def main():
             % (g["avg_launch_us"], g["achieved_gbs"], cp["bytes"], cp["us"], cp["gbs"]))
         return 0
 
-    max_ctx = args.prefill + args.warmup + args.steps + 8
+    max_ctx = max(args.prefill + args.warmup + args.steps + 8, VERIFY_CTX + 4 * VERIFY_K * 4)
     cfg = dz.Config.bonsai27b(max_ctx=max_ctx)
     t0 = time.time()
     log("building synthetic 27B-shape model")
@@ -257,9 +327,19 @@ def main():
     tps = args.steps / (ms / 1e3)
 
     log("decode %d tokens: %.2f tok/s" % (args.steps, tps))
+    pos_timed = args.prefill + args.warmup
+    algo = decode_bytes(cfg, wbytes, pos_timed, args.steps)
+    ptk_gbs = algo / (ms * 1e-3) / 1e9
+    ptk_traffic = measured_traffic("decode_config4_pmc.txt")
+    if args.only == "decode":
+        log("token kernel: %.1f GB/s algorithmic over %.1f ms (%d B)" % (ptk_gbs, ms, algo))
+        return 0
     g = bench_gemv(dz, H)
     cp = bench_copy(H, g["algo_bytes"])
     log("gemv: %.2f us per launch; copy ceiling %.1f GB/s" % (g["avg_launch_us"], cp["gbs"]))
+    v = bench_verify(dz, H, ctx, cfg, ms / args.steps)
+    log("config 5: verify forward %.2f ms, spec step %.2f ms (sequential %.2f ms) at context %d"
+        % (v["verify_forward_ms"], v["spec_verify_step_ms"], v["sequential_verify_ms"], v["context"]))
     out = {
         "metric": METRIC,
         "value": round(tps, 2),
@@ -288,18 +368,31 @@ def main():
             "decode_wall_s": round(wall, 4),
         },
         "roofline": {
+            "kernel": "ptk_kernel (persistent token kernel: %d decode tokens per launch)" % args.steps,
+            "bound": "hbm",
+            "achieved": round(ptk_gbs, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(ptk_gbs / PEAK_GBS, 4),
+            "traffic": ptk_traffic,
+            "avg_launch_us": round(ms * 1e3, 1),
+            "launches_timed": 1,
+            "algo_bytes_per_launch": algo,
+            "copy_ceiling_gbs": round(cp["gbs"], 1),
+        },
+        "roofline_gemv": {
             "kernel": "gemv_lut_kernel (Q1_0 LUT GEMV, config 1 17408x5120, split-K partials)",
             "bound": "hbm",
             "achieved": round(g["achieved_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["achieved_gbs"] / PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic("gemv_config1_pmc.txt"),
             "avg_launch_us": round(g["avg_launch_us"], 3),
             "launches_timed": g["launches"],
             "algo_bytes_per_launch": g["algo_bytes"],
-            "copy_ceiling_gbs": round(cp["gbs"], 1),
         },
+        "config5": v,
         "cpu_baseline": None,
     }
     ctx.close()

@@ -284,18 +284,22 @@ __global__ __launch_bounds__(256) void bt_attn_prep_kernel(const float* __restri
 // Causal GQA attention of token t (position pos0 + t) over cache positions [0, pos0 + t] for the
 // GRP q-heads of kv-head kvh (online softmax, attention.rs:149-199), then o·sigmoid(gate)
 // (attention.rs:202-203) -> ao[t][h·256 ..].  The 4 waves take positions p ≡ wave (mod 4) with
-// their own running (m, l, o) and are merged at the end.  Grid (n, nkv), 256 threads.
+// their own running (m, l, o) and are merged at the end.  Grid (n, nkv, nch), 256 threads: with
+// nch > 1 workgroup z takes positions [z·csz, (z+1)·csz) and writes its record (m, l, o[256])
+// per q-head to rec[t][h][z] for bt_attn_merge_kernel instead.
 template <int GRP>
 __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ qb, const float* __restrict__ gate,
                                                       const float* __restrict__ kcache,
                                                       const float* __restrict__ vcache, int max_ctx, int nq,
-                                                      int pos0, float* __restrict__ ao) {
+                                                      int pos0, float* __restrict__ ao, int csz,
+                                                      float* __restrict__ rec) {
   constexpr int HD = 256;
   __shared__ float wm[4][GRP], wl[4][GRP];
   __shared__ float wo[4][GRP][HD];
-  const int t = blockIdx.x, kvh = blockIdx.y;
+  const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, nch = gridDim.z;
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const int ctx = pos0 + t + 1;
+  const int ctx = nch > 1 ? min(pos0 + t + 1, (z + 1) * csz) : pos0 + t + 1;
+  const int pbeg = nch > 1 ? z * csz : 0;
   float m[GRP], l[GRP];
   float4 o[GRP], q4[GRP];
 #pragma unroll
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
   }
   const float* kb = kcache + (size_t)kvh * max_ctx * HD + 4 * lane;
   const float* vb = vcache + (size_t)kvh * max_ctx * HD + 4 * lane;
-  int p = (int)wave;
+  int p = pbeg + (int)wave;
   float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka;
   if (p < ctx) {
     ka = *reinterpret_cast<const float4*>(kb + (size_t)p * HD);
@@ -356,9 +360,41 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
       O = __builtin_fmaf(wo[w][gi][tid], e, O);
     }
     const int h = kvh * GRP + gi;
-    const float gt = gate[((size_t)t * nq + h) * HD + tid];
-    ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);
+    if (nch > 1) {
+      float* rr = rec + (((size_t)t * nq + h) * nch + z) * (2 + HD);
+      if (tid == 0) {
+        rr[0] = M;
+        rr[1] = L;
+      }
+      rr[2 + tid] = O;
+    } else {
+      const float gt = gate[((size_t)t * nq + h) * HD + tid];
+      ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);
+    }
   }
+}
+
+// Merge of the position chunks of bt_attn_kernel (records with l = 0 held no position), then
+// o·sigmoid(gate).  Grid (n, nq), 256 threads.
+__global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restrict__ rec, int nch,
+                                                            const float* __restrict__ gate, int nq,
+                                                            float* __restrict__ ao) {
+  constexpr int HD = 256;
+  const int t = blockIdx.x, h = blockIdx.y;
+  const unsigned tid = threadIdx.x;
+  const float* rr = rec + ((size_t)t * nq + h) * nch * (2 + HD);
+  float M = -INFINITY;
+  for (int z = 0; z < nch; ++z)
+    if (rr[(size_t)z * (2 + HD) + 1] > 0.f) M = fmaxf(M, rr[(size_t)z * (2 + HD)]);
+  float L = 0.f, O = 0.f;
+  for (int z = 0; z < nch; ++z) {
+    const float* c = rr + (size_t)z * (2 + HD);
+    const float e = c[1] > 0.f ? expf(c[0] - M) : 0.f;
+    L = __builtin_fmaf(c[1], e, L);
+    O = __builtin_fmaf(c[2 + tid], e, O);
+  }
+  const float gt = gate[((size_t)t * nq + h) * HD + tid];
+  ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);
 }
 
 // SwiGLU (mlp.rs:28-47, swiglu_inplace_simd): s[t][i] = silu(gate[t][i]) · up[t][i], gate rows

@@ -94,7 +94,7 @@ struct dz_ctx {
     float *ygu = nullptr, *sw = nullptr, *qb = nullptr, *gate = nullptr;
     float* logits = nullptr;  // [logits_rows][vocab]
     int logits_rows = 0;
-    dz::Scratch pack;
+    dz::Scratch pack, split, arec;
     // verify records per DeltaNet layer: conv inputs [kv][qkvd] and the scan's rollback record
     int kv_cap = 0;
     std::vector<float*> rx;
@@ -1092,7 +1092,11 @@ static void bt_release(dz_ctx* x) {
   x->bt.rx.clear();
   x->bt.rec.clear();
   if (x->bt.pack.ptr) (void)hipFree(x->bt.pack.ptr);
+  if (x->bt.split.ptr) (void)hipFree(x->bt.split.ptr);
+  if (x->bt.arec.ptr) (void)hipFree(x->bt.arec.ptr);
   x->bt.pack = Scratch{};
+  x->bt.split = Scratch{};
+  x->bt.arec = Scratch{};
 }
 
 // Activation buffers for chunks of up to cap tokens.
@@ -1162,16 +1166,25 @@ static hipError_t launch(K kfn, dim3 g, dim3 b, hipStream_t s, Args... args) {
 }
 
 static hipError_t launch_bt_attn(int grp, dim3 g, hipStream_t s, const float* qb, const float* gate, const float* kc,
-                                 const float* vc, int max_ctx, int nq, int pos0, float* ao) {
+                                 const float* vc, int max_ctx, int nq, int pos0, float* ao, int csz, float* rec) {
   switch (grp) {
-    case 1: return launch(bt_attn_kernel<1>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
-    case 2: return launch(bt_attn_kernel<2>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
-    case 3: return launch(bt_attn_kernel<3>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
-    case 4: return launch(bt_attn_kernel<4>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
-    case 6: return launch(bt_attn_kernel<6>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
-    case 8: return launch(bt_attn_kernel<8>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao);
+    case 1: return launch(bt_attn_kernel<1>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 2: return launch(bt_attn_kernel<2>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 3: return launch(bt_attn_kernel<3>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 4: return launch(bt_attn_kernel<4>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 6: return launch(bt_attn_kernel<6>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 8: return launch(bt_attn_kernel<8>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Position chunks of the chunk's attention: enough workgroups to fill the device when the chunk
+// has few tokens (speculative verify at long context), one chunk for a long prefill.
+static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
+  int nch = (1024 + n * nkv - 1) / (n * nkv);
+  nch = std::max(1, std::min(nch, std::max(1, ctx_max / 64)));
+  *csz = (ctx_max + nch - 1) / nch;
+  return (ctx_max + *csz - 1) / *csz;
 }
 
 // y[n][W.rows] (=|+=) W · (optionally RMS-normalised) x[n][W.cols].
@@ -1181,7 +1194,7 @@ static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int
   int rc = packed_x_reserve(x->bt.pack, n, W.cols, &p);
   if (rc) return rc;
   DZ_HIP_CHECK(launch_x_pack(xin, ldx, W.cols, n, norm_w, x->m->cfg.rms_eps, p, x->s));
-  DZ_HIP_CHECK(launch_q1_gemm(W, p, n, y, ldy, accumulate, x->s));
+  DZ_HIP_CHECK(launch_q1_gemm(W, p, n, y, ldy, accumulate, x->s, &x->bt.split));
   return DZ_OK;
 }
 
@@ -1246,8 +1259,18 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
                           (const float*)x->bt.yin, ld_in, (int)c.n_head, (int)c.n_head_kv, (const float*)l.q_norm,
                           (const float*)l.k_norm, c.rms_eps, (const float*)x->rope, (int)c.rope_dim, p0, x->bt.qb,
                           x->bt.gate, kc, vc, (int)c.max_ctx));
-      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, dim3(nb, (unsigned)c.n_head_kv), s, x->bt.qb, x->bt.gate, kc,
-                                  vc, (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy));
+      int csz;
+      const int nch = bt_attn_chunks(n, (int)c.n_head_kv, p0 + n, &csz);
+      float* rec = nullptr;
+      if (nch > 1) {
+        if ((rc = x->bt.arec.reserve((size_t)n * c.n_head * nch * (2 + c.head_dim) * sizeof(float)))) return rc;
+        rec = static_cast<float*>(x->bt.arec.ptr);
+      }
+      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, dim3(nb, (unsigned)c.n_head_kv, (unsigned)nch), s, x->bt.qb,
+                                  x->bt.gate, kc, vc, (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy, csz, rec));
+      if (nch > 1)
+        DZ_HIP_CHECK(launch(bt_attn_merge_kernel, dim3(nb, (unsigned)c.n_head), dim3(256), s, (const float*)rec, nch,
+                            (const float*)x->bt.gate, (int)c.n_head, x->bt.gy));
       if ((rc = bt_gemm(x, l.out_proj, x->bt.gy, qd, n, nullptr, x->bt.h, H, 1))) return rc;
     }
     // MLP (mlp.rs:28-47): h += W_down (silu(W_gate n) * W_up n), n = rmsnorm(h, post_attention_norm)

@@ -27,10 +27,12 @@ namespace dz {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup
-constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup (and the padding of n)
+constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup (wide form)
+constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup of the wide form, the padding of n
 constexpr int kGemmRowPad = 2 * kTileCols + 16;  // LDS bytes per staged token row (16 B pad: no bank conflicts)
-constexpr size_t kGemmShmem = (size_t)2 * kGemmTok * kGemmRowPad;  // hi and lo tiles
+// hi and lo tiles of NB token blocks
+__host__ __device__ constexpr size_t gemm_shmem(int nb) { return (size_t)2 * 16 * nb * kGemmRowPad; }
+constexpr size_t kGemmShmem = gemm_shmem(kGemmNB);
 
 // Activations packed for the matrix cores.
 struct GemmX {
@@ -58,6 +60,8 @@ __device__ __forceinline__ void pack_split(float v, unsigned short& h, unsigned 
 // One workgroup (256 threads) per token row n < Np: x[n][0..K) -> xh/xl[n][0..Kp), sig[n]; rows
 // n >= n_tok and columns k >= K are zero.  When w is given the row is first RMS-normalised with
 // weight w (rmsnorm_into, Daiza-engine/src/math/rmsnorm.rs:17-200: x·(1/sqrt(ss/K + eps))·w).
+// One pass gathers Σx² and max|x·w| (the norm's scale is positive, so the normalised row's
+// maximum is the scale times that), the second writes.  K is a multiple of 4 (of 128 for Q1_0).
 __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x, int64_t ldx, int64_t K, int n_tok,
                                                      const float* __restrict__ w, float eps, uint16_t* __restrict__ xh,
                                                      uint16_t* __restrict__ xl, float* __restrict__ sig, int64_t Kp) {
@@ -65,56 +69,64 @@ __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x
   const int n = blockIdx.x;
   const unsigned tid = threadIdx.x;
   const bool live = n < n_tok;
-  const float* row = x + (size_t)(live ? n : 0) * ldx;
-  float inv = 1.0f;
-  if (w) {
-    float ss = 0.f;
-    for (int64_t k = tid; k < K; k += 256) ss = __builtin_fmaf(row[k], row[k], ss);
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((tid & 63u) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    inv = 1.0f / sqrtf(ss / (float)K + eps);
-    __syncthreads();
+  const float4* row = reinterpret_cast<const float4*>(x + (size_t)(live ? n : 0) * ldx);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  const int64_t K4 = live ? K / 4 : 0;
+  float ss = 0.f, amax = 0.f;
+  for (int64_t k = tid; k < K4; k += 256) {
+    const float4 v = row[k];
+    ss = __builtin_fmaf(v.x, v.x, ss);
+    ss = __builtin_fmaf(v.y, v.y, ss);
+    ss = __builtin_fmaf(v.z, v.z, ss);
+    ss = __builtin_fmaf(v.w, v.w, ss);
+    const float4 u = w ? make_float4(v.x * w4[k].x, v.y * w4[k].y, v.z * w4[k].z, v.w * w4[k].w) : v;
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
   }
-  float amax = 0.f;
-  for (int64_t k = tid; k < K; k += 256) {
-    const float v = w ? (row[k] * inv) * w[k] : row[k];
-    amax = fmaxf(amax, fabsf(v));
+  for (int o = 32; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o);
+    amax = fmaxf(amax, __shfl_xor(amax, o));
   }
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((tid & 63u) == 0) red[4 + (tid >> 6)] = amax;
+  if ((tid & 63u) == 0) {
+    red[tid >> 6] = ss;
+    red[4 + (tid >> 6)] = amax;
+  }
   __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
   amax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
-  const float s = live ? pack_sig(amax) : 1.0f;
+  const float inv = w ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
+  const float s = live ? pack_sig(amax * inv) : 1.0f;
   const float rs = 1.0f / s;  // exact: s is a power of two
-  uint16_t* oh = xh + (size_t)n * Kp;
-  uint16_t* ol = xl + (size_t)n * Kp;
-  for (int64_t k = tid; k < Kp; k += 256) {
-    unsigned short h = 0, l = 0;
-    if (live && k < K) pack_split((w ? (row[k] * inv) * w[k] : row[k]) * rs, h, l);
+  ushort4* oh = reinterpret_cast<ushort4*>(xh + (size_t)n * Kp);
+  ushort4* ol = reinterpret_cast<ushort4*>(xl + (size_t)n * Kp);
+  for (int64_t k = tid; k < Kp / 4; k += 256) {
+    ushort4 h = make_ushort4(0, 0, 0, 0), l = h;
+    if (k < K4) {
+      const float4 v = row[k];
+      float4 u = v;
+      if (w) u = make_float4((v.x * inv) * w4[k].x, (v.y * inv) * w4[k].y, (v.z * inv) * w4[k].z, (v.w * inv) * w4[k].w);
+      pack_split(u.x * rs, h.x, l.x);
+      pack_split(u.y * rs, h.y, l.y);
+      pack_split(u.z * rs, h.z, l.z);
+      pack_split(u.w * rs, h.w, l.w);
+    }
     oh[k] = h;
     ol[k] = l;
   }
   if (tid == 0) sig[n] = live ? s : 0.f;
 }
 
-// Sign byte s of a restored chunk (4 dwords, bit set = +scale after the sign fix-up) as the eight
-// f16 operand values: element e = f16 with magnitude |scale| (s2 = |scale| in both halves) and
-// sign from bit 8·(s & 3) + e of dword s >> 2.
+// Sign byte s of a restored chunk (4 dwords, bit set = sign bit of the f16 value set, after the
+// fix-up of restore_chunk) as the eight f16 operand values: element e has magnitude |scale|
+// (s2 = |scale| in both halves) and the sign of bit e of byte s.  With b the byte and
+// Y = b | b << 15, Y << (15 - 2p) holds bit 2p at position 15 and bit 2p+1 at position 31, so a
+// pair of elements costs a shift and an and-or.
 template <int S>
 __device__ __forceinline__ f16x8 expand_signs(const unsigned (&wn)[4], unsigned s2) {
-  const unsigned w = wn[S >> 2];
+  const unsigned b = __builtin_amdgcn_ubfe(wn[S >> 2], 8 * (S & 3), 8);
+  const unsigned y = (b << 15) | b;
   unsigned d[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    constexpr int o0 = 8 * (S & 3);
-    const int o = o0 + 2 * p;
-    const unsigned lo = o <= 15 ? (w << (15 - o)) : (w >> (o - 15));  // bit o -> 15
-    const unsigned hi = w << (30 - o);                                 // bit o+1 -> 31
-    const unsigned t = (lo & 0x00008000u) | (hi & ~0x00008000u);
-    d[p] = (t & 0x80008000u) | s2;
-  }
+  for (int p = 0; p < 4; ++p) d[p] = ((y << (15 - 2 * p)) & 0x80008000u) | s2;
   u32x4 v = {d[0], d[1], d[2], d[3]};
   return __builtin_bit_cast(f16x8, v);
 }
@@ -139,24 +151,32 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
   s2 = (sc_bits & 0x7FFFu) * 0x00010001u;
 }
 
-// Grid (ceil(nrb / 4), Np / kGemmTok), 256 threads, kGemmShmem bytes of dynamic LDS.
+// Grid (ceil(nrb / 4), Np / (16·NB), splits), 256 threads, gemm_shmem(NB) bytes of dynamic LDS.
+// Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
+// partial to y + z·zstride; an unsplit product (gridDim.z = 1) writes
 // y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xl)[n][k] for n < n_tok, row < rows.
+template <int NB>
 __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
-                                                         int ntiles, const GemmX x, int n_tok, float* __restrict__ y,
-                                                         int64_t ldy, int accumulate) {
+                                                         int ntiles, int tps, const GemmX x, int n_tok,
+                                                         float* __restrict__ y, int64_t ldy, int64_t zstride,
+                                                         int accumulate) {
+  constexpr int TOK = 16 * NB;
   extern __shared__ __align__(16) unsigned char smem[];
   const unsigned tid = threadIdx.x, lane = tid & 63u;
   const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6);
   const bool live = rb < nrb;
-  const int tok0 = (int)blockIdx.y * kGemmTok;
+  const int tok0 = (int)blockIdx.y * TOK;
   const unsigned r = lane & 15u, q = lane >> 4;
-  f32x4 acc[4][kGemmNB];
+  const int t_begin = (int)blockIdx.z * tps, t_end = min(ntiles, t_begin + tps);
+  y += (size_t)blockIdx.z * zstride;
+  if (gridDim.z > 1) accumulate = 0;
+  f32x4 acc[4][NB];
 #pragma unroll
   for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
-    for (int nb = 0; nb < kGemmNB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = t_begin; t < t_end; ++t) {
     // this wave's unit: per 16-row block sb, the chunk c = sb ^ q of row 16·sb + r and its scale slot c
     u32x4 cv[4];
     unsigned cs[4];
@@ -172,10 +192,10 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
     }
     __syncthreads();  // the previous tile's LDS reads are done
     // stage the activations of tile t: [hi | lo][token][512 f16], rows padded to kGemmRowPad
-    for (int i = (int)tid; i < 2 * kGemmTok * 64; i += 256) {
-      const int part = i / (kGemmTok * 64), rem = i % (kGemmTok * 64), n = rem >> 6, c = rem & 63;
+    for (int i = (int)tid; i < 2 * TOK * 64; i += 256) {
+      const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
       const uint16_t* src = (part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp + (size_t)t * kTileCols + 8 * c;
-      *reinterpret_cast<u32x4*>(smem + ((size_t)part * kGemmTok + n) * kGemmRowPad + 16 * c) =
+      *reinterpret_cast<u32x4*>(smem + ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) =
           *reinterpret_cast<const u32x4*>(src);
     }
     __syncthreads();
@@ -185,17 +205,17 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       for (int sb = 0; sb < 4; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
       // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
       const unsigned char* bh = smem + (size_t)r * kGemmRowPad + 256u * q;
-      const unsigned char* bl = bh + (size_t)kGemmTok * kGemmRowPad;
+      const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
 #define DZ_GEMM_STEP(S)                                                                               \
   {                                                                                                   \
-    f16x8 xh_[kGemmNB], xl_[kGemmNB];                                                                 \
-    _Pragma("unroll") for (int nb = 0; nb < kGemmNB; ++nb) {                                          \
+    f16x8 xh_[NB], xl_[NB];                                                                           \
+    _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                               \
       xh_[nb] = *reinterpret_cast<const f16x8*>(bh + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
       xl_[nb] = *reinterpret_cast<const f16x8*>(bl + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
     }                                                                                                 \
     _Pragma("unroll") for (int sb = 0; sb < 4; ++sb) {                                                \
       const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
-      _Pragma("unroll") for (int nb = 0; nb < kGemmNB; ++nb) {                                        \
+      _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                             \
         acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], acc[sb][nb], 0, 0, 0);       \
         acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl_[nb], acc[sb][nb], 0, 0, 0);       \
       }                                                                                               \
@@ -211,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   if (!live) return;
   // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
 #pragma unroll
-  for (int nb = 0; nb < kGemmNB; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     const int n = tok0 + 16 * nb + (int)r;
     if (n >= n_tok) continue;
     const float sg = x.sig[n];
@@ -229,6 +249,20 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       }
     }
   }
+}
+
+// y[n][row] (=|+=) Σ_z part[z][n][row] for z < splits in order (the partials of a split product).
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                int64_t zstride, int64_t rows, int n_tok,
+                                                                float* __restrict__ y, int64_t ldy, int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int n = blockIdx.y;
+  if (row >= rows || n >= n_tok) return;
+  const size_t off = (size_t)n * rows + row;
+  float v = part[off];
+  for (int z = 1; z < splits; ++z) v += part[(size_t)z * zstride + off];
+  float* yr = y + (size_t)n * ldy + row;
+  *yr = accumulate ? *yr + v : v;
 }
 
 }  // namespace dz

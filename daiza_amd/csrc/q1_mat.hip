@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 
 struct dz_mat {
@@ -266,26 +267,64 @@ hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const fl
   return hipGetLastError();
 }
 
+// Workgroups wanted in flight (two per CU): a product with fewer splits its K tiles over
+// blockIdx.z and sums the partials in a second pass.
+constexpr int kGemmMinWgs = 512;
+
+int gemm_splits(const Q1Dev& W, int n, int* tps) {
+  const int nb = n <= 16 ? 1 : kGemmNB;
+  const int64_t wgs = ((W.nrb + 3) / 4) * ((n + 16 * nb - 1) / (16 * nb));
+  const int nt = (int)W.ntiles;
+  int S = 1;
+  if (wgs < kGemmMinWgs && nt > 1) S = (int)std::min<int64_t>(nt, (kGemmMinWgs + wgs - 1) / wgs);
+  *tps = (nt + S - 1) / S;
+  return (nt + *tps - 1) / *tps;
+}
+
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
-                          hipStream_t s) {
+                          hipStream_t s, Scratch* split) {
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmShmem);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_shmem(kGemmNB));
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel<1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_shmem(1));
     if (e != hipSuccess) return e;
     attr = true;
   }
   if (W.ntiles * kTileCols != p.Kp || n > p.Np) return hipErrorInvalidValue;
   GemmX gx{p.xh, p.xl, p.sig, p.Kp};
-  const dim3 grid((unsigned)((W.nrb + 3) / 4), (unsigned)((n + kGemmTok - 1) / kGemmTok));
-  hipLaunchKernelGGL(q1_gemm_kernel, grid, dim3(256), kGemmShmem, s, W.data, W.rows, W.nrb, (int)W.ntiles, gx, n, y,
-                     ldy, accumulate);
+  int tps;
+  int S = gemm_splits(W, n, &tps);
+  if (S > 1 && !split) S = 1, tps = (int)W.ntiles;
+  float* out = y;
+  int64_t ld = ldy, zs = 0;
+  if (S > 1) {
+    zs = (int64_t)n * W.rows;
+    if (split->reserve((size_t)S * zs * sizeof(float))) return hipErrorOutOfMemory;
+    out = static_cast<float*>(split->ptr);
+    ld = W.rows;
+  }
+  const unsigned gx_ = (unsigned)((W.nrb + 3) / 4);
+  if (n <= 16) {
+    hipLaunchKernelGGL(q1_gemm_kernel<1>, dim3(gx_, 1, (unsigned)S), dim3(256), gemm_shmem(1), s, W.data, W.rows,
+                       W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+  } else {
+    hipLaunchKernelGGL(q1_gemm_kernel<kGemmNB>, dim3(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S),
+                       dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows, W.nrb, (int)W.ntiles, tps, gx, n, out, ld,
+                       zs, accumulate);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || S == 1) return e;
+  hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((W.rows + 255) / 256), (unsigned)n), dim3(256), 0, s,
+                     (const float*)out, S, zs, W.rows, n, y, ldy, accumulate);
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ matrix API state
 
-static Scratch g_x, g_y, g_part, g_pack;
+static Scratch g_x, g_y, g_part, g_pack, g_split;
 
 static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* const* y_dev, int accumulate,
                        hipStream_t s) {
@@ -460,7 +499,7 @@ int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumul
   DZ_HIP_CHECK(hipMemcpyAsync(xd, x, (size_t)n * K * 4, hipMemcpyHostToDevice, s));
   if (accumulate) DZ_HIP_CHECK(hipMemcpyAsync(yd, y, (size_t)n * R * 4, hipMemcpyHostToDevice, s));
   DZ_HIP_CHECK(launch_x_pack(xd, (int64_t)K, (int64_t)K, n, nullptr, 0.f, p, s));
-  DZ_HIP_CHECK(launch_q1_gemm(m->d, p, n, yd, (int64_t)R, accumulate, s));
+  DZ_HIP_CHECK(launch_q1_gemm(m->d, p, n, yd, (int64_t)R, accumulate, s, &g_split));
   DZ_HIP_CHECK(hipMemcpyAsync(y, yd, (size_t)n * R * 4, hipMemcpyDeviceToHost, s));
   DZ_HIP_CHECK(hipStreamSynchronize(s));
   return DZ_OK;

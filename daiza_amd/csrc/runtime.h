@@ -72,8 +72,10 @@ int packed_x_reserve(Scratch& buf, int n, int64_t K, PackedX* out);
 // x[n][K] (row stride ldx) -> p; RMS-normalised with weight w first when w is non-null.
 hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const float* w, float eps, const PackedX& p,
                          hipStream_t s);
-// y[n][rows] (row stride ldy) =|+= p · Wᵀ; W.cols must match the packed K.
+// y[n][rows] (row stride ldy) =|+= p · Wᵀ; W.cols must match the packed K.  A product with too
+// few workgroups to fill the device splits its K tiles into partials held in `split` (grown on
+// demand; NULL keeps it unsplit) and sums them in order.
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
-                          hipStream_t s);
+                          hipStream_t s, Scratch* split);
 
 }  // namespace dz

@@ -467,15 +467,17 @@ __device__ __forceinline__ bool r_swiglu(unsigned char* smem, bool prior, const 
   const int T = P.nT_h;
   bool ok = prior;
   if (ok) {
-    constexpr int N = MF * NTH + NTH;
+    // slot MF*NTH: lane k < T of wave 0 polls the tile sum of squares k (wave 0 sums them)
+    constexpr int N = MF * NTH + 1;
     u64 x[N];
+    const bool sq_lane = (int)tid < T;
     auto item_row = [&](int it) { return it < nf ? f0 + it : P.F + f0 + (it - nf); };
     auto addr = [&](int sl, unsigned) -> const u64* {
-      if (sl >= MF * NTH) return sstm + (sl - MF * NTH);
+      if (sl >= MF * NTH) return sstm + (sq_lane ? (int)tid : 0);
       return pgu + (size_t)(sl % NTH) * ldp + item_row((int)tid + kPtkThreads * (sl / NTH));
     };
     auto valid = [&](int sl) {
-      if (sl >= MF * NTH) return sl - MF * NTH < T;
+      if (sl >= MF * NTH) return sq_lane;
       return sl % NTH < T && (int)tid + kPtkThreads * (sl / NTH) < 2 * nf;
     };
     ok = poll<N>(addr, valid, TagC{tag_p}, x, e);
@@ -490,12 +492,9 @@ __device__ __forceinline__ bool r_swiglu(unsigned char* smem, bool prior, const 
         gu[it] = v;
       }
     }
-    if (tid == 0) {
-      float ss = 0.f;
-#pragma unroll
-      for (int k = 0; k < NTH; ++k)
-        if (k < T) ss += ll_val(x[MF * NTH + k]);
-      red[33] = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+    if (tid < 64) {
+      const float ss = wave_sum(sq_lane ? ll_val(x[MF * NTH]) : 0.f);
+      if (tid == 0) red[33] = 1.0f / sqrtf(ss / (float)P.H + P.eps);
     }
   }
   if (!wg_ok(smem, ok)) return false;
@@ -516,21 +515,20 @@ __device__ __forceinline__ bool r_qkv(const PtkPlan& P, const PtkLayer& Ly, int 
   const int nr = r1 - r0;
   const int64_t ldp = (int64_t)Ly.nrb_in * kRowBlock;
   const int T = P.nT_h;
-  constexpr int N = MR * NTH + NTH;
+  const int lane = (int)(tid & 63u);
+  // slot MR*NTH: lane k < T of every wave polls the tile sum of squares k (the wave sums them)
+  constexpr int N = MR * NTH + 1;
   u64 x[N];
   auto addr = [&](int sl, unsigned) -> const u64* {
-    if (sl >= MR * NTH) return sst_in + (sl - MR * NTH);
+    if (sl >= MR * NTH) return sst_in + (lane < T ? lane : 0);
     return pin + (size_t)(sl % NTH) * ldp + r0 + (int)tid + kPtkThreads * (sl / NTH);
   };
   auto valid = [&](int sl) {
-    if (sl >= MR * NTH) return sl - MR * NTH < T;
+    if (sl >= MR * NTH) return lane < T;
     return sl % NTH < T && (int)tid + kPtkThreads * (sl / NTH) < nr;
   };
   const bool ok = poll<N>(addr, valid, TagC{tag_in}, x, e);
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < NTH; ++k)
-    if (k < T) ss += ll_val(x[MR * NTH + k]);
+  const float ss = wave_sum(lane < T ? ll_val(x[MR * NTH]) : 0.f);
   const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {

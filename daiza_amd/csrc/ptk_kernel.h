@@ -907,17 +907,6 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
     }
     tr(tid, 0, 3);
   }
-  if (!wg_ok(smem, ok)) return false;
-  // online softmax over this wave's positions (attention.rs:149-199); lane holds dims 4*lane..+3
-  float m[GRP], l[GRP];
-  float4 o[GRP], q4[GRP];
-#pragma unroll
-  for (int gi = 0; gi < GRP; ++gi) {
-    m[gi] = -INFINITY;
-    l[gi] = 0.f;
-    o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
-    q4[gi] = *reinterpret_cast<const float4*>(&qs[gi * HD + 4 * lane]);
-  }
   const float* kb = Ly.kc + (size_t)kvh * P.max_ctx * HD;
   const float* vb = Ly.vc + (size_t)kvh * P.max_ctx * HD;
   auto loadkv = [&](int p, float4& k4, float4& v4) {
@@ -929,13 +918,36 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
       v4 = co_ld4(vb + (size_t)p * HD + 4 * lane);
     }
   };
+  // a compute wave's first two positions are read from the cache while the sync wave runs the
+  // prologue (only the new position comes from it, through LDS after the barrier)
+  constexpr int NW = kPtkWaves;
   int p = p0 + (int)wave;
   float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka, kb1 = ka, vb1 = ka;
-  if (p < p1) loadkv(p, ka, va);
-  if (p + kPtkWaves < p1) loadkv(p + kPtkWaves, kb1, vb1);
-  for (; p < p1; p += kPtkWaves) {
+  if (!SYNC) {
+    if (p < p1 && p != pos) loadkv(p, ka, va);
+    if (p + NW < p1 && p + NW != pos) loadkv(p + NW, kb1, vb1);
+  }
+  if (!wg_ok(smem, ok)) return false;
+  if (SYNC) {
+    if (p < p1) loadkv(p, ka, va);
+    if (p + NW < p1) loadkv(p + NW, kb1, vb1);
+  } else {
+    if (p == pos) loadkv(p, ka, va);
+    if (p + NW == pos) loadkv(p + NW, kb1, vb1);
+  }
+  // online softmax over this wave's positions (attention.rs:149-199); lane holds dims 4*lane..+3
+  float m[GRP], l[GRP];
+  float4 o[GRP], q4[GRP];
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) {
+    m[gi] = -INFINITY;
+    l[gi] = 0.f;
+    o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+    q4[gi] = *reinterpret_cast<const float4*>(&qs[gi * HD + 4 * lane]);
+  }
+  for (; p < p1; p += NW) {
     float4 kc = ka, vc = va;
-    if (p + 2 * kPtkWaves < p1) loadkv(p + 2 * kPtkWaves, kc, vc);
+    if (p + 2 * NW < p1) loadkv(p + 2 * NW, kc, vc);
     const float4 k4 = ka, v4 = va;
     ka = kb1;
     va = vb1;
@@ -963,7 +975,6 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
     }
   }
   tr(tid, 64, 1);
-  if constexpr (!SYNC) pf();  // no cache read follows
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {
     if (lane == 0) {
@@ -1002,6 +1013,8 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
     ll_st(rc + 2 + d, O, tag);
   }
   tr(tid, 64, 2);
+  // the out-projection weights, after the record stores (queued behind them, not ahead)
+  if constexpr (!SYNC) pf();
   return true;
 }
 

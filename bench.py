@@ -52,6 +52,8 @@ def hip():
     h.hipDeviceSynchronize.argtypes = []
     h.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
     h.hipFree.argtypes = [ctypes.c_void_p]
+    h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    h.hipStreamDestroy.argtypes = [ctypes.c_void_p]
     return h
 
 
@@ -68,6 +70,13 @@ class Events:
         ms = ctypes.c_float()
         assert self.H.hipEventElapsedTime(ctypes.byref(ms), self.ev[a], self.ev[b]) == 0
         return ms.value
+
+    def destroy(self):
+        """Every HIP object this script creates is destroyed before exit (profilers that tear down
+        after the program are sensitive to objects left alive)."""
+        for e in self.ev:
+            self.H.hipEventDestroy(e)
+        self.ev = []
 
 
 class Gate:
@@ -104,6 +113,8 @@ def bench_copy(H, nbytes, reps=32):
     H.hipEventSynchronize(ev.ev[1])
     g.free()
     us = 1e3 * ev.elapsed_ms(0, 1) / reps
+    ev.destroy()
+    H.hipStreamDestroy(s)
     H.hipFree(a)
     H.hipFree(b)
     return {"bytes": nbytes, "us": us, "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
@@ -162,6 +173,7 @@ def bench_verify(dz, H, ctx, cfg, decode_ms_per_tok, reps=8):
     H.hipEventRecord(ev.ev[1], stream)
     H.hipEventSynchronize(ev.ev[1])
     fwd_ms = ev.elapsed_ms(0, 1) / reps
+    ev.destroy()
     params = dz.SamplingParams(0.7, 20, 0.95)
     lcg = dz.LcgRng(0xC0FFEE)
     dl = rng.standard_normal((VERIFY_K, cfg.vocab)).astype(np.float32)
@@ -220,6 +232,8 @@ def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
     g.free()
     avg_us = 1e3 * ev.elapsed_ms(0, 1) / n
     algo = rows * (cols // 128) * 18 + cols * 4 + rows * 4  # W + x + y (config 1)
+    ev.destroy()
+    H.hipStreamDestroy(s)
     for m in mats:
         m.close()
     H.hipFree(dx)
@@ -264,6 +278,28 @@ def cpu_baseline(cfg_cls, budget_s=20.0):
                       % (n, threads, model, os.cpu_count() or 0, gen_s)}
 
 
+_KEEP = []  # objects of --only trace, alive until interpreter exit
+
+
+def trace_decode(dz, args):
+    """--only trace: the prefill and one decode launch through library calls alone, timed by the host
+    clock, for rocprofv3 passes (the profiler loses its output when this script's own HIP objects
+    exist, or when the context is freed under it, so both are left to process exit)."""
+    cfg = dz.Config.bonsai27b(max_ctx=args.prefill + args.warmup + args.steps + 8)
+    model = dz.Model.synthetic(cfg, SEED)
+    ctx = dz.Context(model)
+    prompt = np.random.default_rng(SEED & 0xFFFF).integers(0, cfg.vocab, args.prefill).astype(np.uint32)
+    t0 = time.perf_counter()
+    last = ctx.forward_batch(prompt)
+    print("[trace] prefill %d tokens in %.3f s" % (args.prefill, time.perf_counter() - t0), flush=True)
+    toks = ctx.decode_greedy(int(np.argmax(last)), max(1, args.warmup))
+    t0 = time.perf_counter()
+    ctx.decode_greedy(int(toks[-1]), args.steps)
+    dt = time.perf_counter() - t0
+    print("[trace] decode %d tokens in one launch: %.2f tok/s (host clock)" % (args.steps, args.steps / dt), flush=True)
+    return model, ctx
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,9 +308,11 @@ def main():
     ap.add_argument("--prefill", type=int, default=PREFILL)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--only", choices=["all", "gemv", "decode"], default="all",
-                    help="gemv: only the config-1 GEMV and the copy reference; decode: only the prefill and "
-                         "the timed decode (both for PMC passes)")
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "verify", "trace"], default="all",
+                    help="gemv: only the config-1 GEMV and the copy reference; decode: only the prefill, the "
+                         "timed decode and a 256 MiB copy reference; verify: only the config-5 verify; trace: the "
+                         "prefill and decode through library calls alone, timed by the host clock (for "
+                         "rocprofv3 passes, which lose their output when the script's own HIP objects exist)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs the decode loop on a single GPU "
@@ -282,6 +320,9 @@ def main():
         return 2
 
     import daiza_amd as dz
+    if args.only == "trace":
+        _KEEP.extend(trace_decode(dz, args))
+        return 0
     H = hip()
     L = dz.lib()
     if L.dz_device_init(0) != 0:
@@ -295,6 +336,16 @@ def main():
 
     max_ctx = max(args.prefill + args.warmup + args.steps + 8, VERIFY_CTX + 4 * VERIFY_K * 4)
     cfg = dz.Config.bonsai27b(max_ctx=max_ctx)
+    if args.only == "verify":
+        model = dz.Model.synthetic(cfg, SEED)
+        ctx = dz.Context(model)
+        v = bench_verify(dz, H, ctx, cfg, float("nan"))
+        log("config 5: verify forward %.2f ms, spec step %.2f ms at context %d"
+            % (v["verify_forward_ms"], v["spec_verify_step_ms"], v["context"]))
+        ctx.close()
+        model.close()
+        H.hipDeviceSynchronize()
+        return 0
     t0 = time.time()
     log("building synthetic 27B-shape model")
     model = dz.Model.synthetic(cfg, SEED)
@@ -324,6 +375,7 @@ def main():
     H.hipDeviceSynchronize()
     wall = time.perf_counter() - t0
     ms = ev.elapsed_ms(0, 1)
+    ev.destroy()
     tps = args.steps / (ms / 1e3)
 
     log("decode %d tokens: %.2f tok/s" % (args.steps, tps))
@@ -332,7 +384,12 @@ def main():
     ptk_gbs = algo / (ms * 1e-3) / 1e9
     ptk_traffic = measured_traffic("decode_config4_pmc.txt")
     if args.only == "decode":
-        log("token kernel: %.1f GB/s algorithmic over %.1f ms (%d B)" % (ptk_gbs, ms, algo))
+        cp = bench_copy(H, 256 << 20, reps=4)
+        log("token kernel: %.1f GB/s algorithmic over %.1f ms (%d B per launch); copy of %d B: %.1f GB/s"
+            % (ptk_gbs, ms, algo, cp["bytes"], cp["gbs"]))
+        ctx.close()
+        model.close()
+        H.hipDeviceSynchronize()
         return 0
     g = bench_gemv(dz, H)
     cp = bench_copy(H, g["algo_bytes"])
@@ -405,4 +462,8 @@ def main():
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # a zero status ends the script normally (no SystemExit): rocprofv3 then writes its output
+    # before the runtime's teardown
+    _rc = main()
+    if _rc:
+        sys.exit(_rc)

@@ -94,7 +94,7 @@ struct dz_ctx {
     float *ygu = nullptr, *sw = nullptr, *qb = nullptr, *gate = nullptr;
     float* logits = nullptr;  // [logits_rows][vocab]
     int logits_rows = 0;
-    dz::Scratch pack, split, arec;
+    dz::Scratch pack, split, arec, spec;
     // verify records per DeltaNet layer: conv inputs [kv][qkvd] and the scan's rollback record
     int kv_cap = 0;
     std::vector<float*> rx;
@@ -1094,9 +1094,11 @@ static void bt_release(dz_ctx* x) {
   if (x->bt.pack.ptr) (void)hipFree(x->bt.pack.ptr);
   if (x->bt.split.ptr) (void)hipFree(x->bt.split.ptr);
   if (x->bt.arec.ptr) (void)hipFree(x->bt.arec.ptr);
+  if (x->bt.spec.ptr) (void)hipFree(x->bt.spec.ptr);
   x->bt.pack = Scratch{};
   x->bt.split = Scratch{};
   x->bt.arec = Scratch{};
+  x->bt.spec = Scratch{};
 }
 
 // Activation buffers for chunks of up to cap tokens.
@@ -1341,6 +1343,17 @@ static int bt_verify_commit(dz_ctx* x, int a) {
                         x->conv + (size_t)si * 4 * qkvd, (x->ring_base[(size_t)si] + p0) & 3, qkvd));
   }
   return bt_finish(x, x->bt.pending_ids.data(), a, p0, a - 1);
+}
+
+// Device logits of a pending verify for the sampler (spec.hip): row 0 = the context's logits (they
+// predict draft 0), rows = the verify forward's per-position rows; its stream and scratch memory.
+int ctx_verify_view(dz_ctx* x, const float** row0, const float** rows, hipStream_t* s, Scratch** scratch) {
+  if (x->bt.pending == 0) return set_error(DZ_ERR_TENSOR, "no pending verify forward");
+  *row0 = x->logits;
+  *rows = x->bt.logits;
+  *s = x->s;
+  *scratch = &x->bt.spec;
+  return DZ_OK;
 }
 
 // DAIZA_BATCH=0 runs forward_batch token by token through the decode path instead.

@@ -79,3 +79,9 @@ hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int
                           hipStream_t s, Scratch* split);
 
 }  // namespace dz
+
+struct dz_ctx;
+namespace dz {
+// The device rows of a context's pending verify forward (see dz_verify_forward), for the sampler.
+int ctx_verify_view(dz_ctx* x, const float** row0, const float** rows, hipStream_t* s, Scratch** scratch);
+}  // namespace dz

@@ -5,8 +5,12 @@
 // (sample_top_k_top_p_into, Daiza-engine/src/math/sampling.rs:144-247) and its LcgRng
 // (sampling.rs:9-19).  The reference forwards each accepted draft one at a time; here all k drafts
 // run in one forward (dz_verify_forward) and the accepted prefix is kept (dz_verify_commit).
-// Sampling runs on the host over the logits rows, as in the reference.
+// The vocabulary-wide work (softmax statistics, the draft token's probabilities, top-k candidates of
+// the row or of the residual distribution) runs on the device (spec_kernels.h); the acceptance
+// draws and the final temperature / top-p draw over the k candidates run on the host, in the
+// reference's order.
 #include "runtime.h"
+#include "spec_kernels.h"
 
 #include <algorithm>
 #include <cmath>
@@ -143,6 +147,50 @@ struct Sampler {
   }
 };
 
+// The end of sample_top_k_top_p_into (sampling.rs:162-246) over the row's top-k candidates, given in
+// order (value descending, lower index first): for mode 1 the values are residual masses r, turned
+// into log-probabilities ln(r · 1/mass) as sample_bonus does; then scaled = value · (1/T), softmax
+// over the candidates, top-p cut, renormalisation and the draw.
+static uint32_t sample_candidates(const SpecCand* c, int K, int mode, float mass, const dz_sampling& sp,
+                                  uint64_t* rng) {
+  const float inv_t = 1.0f / sp.temperature;
+  const float inv_m = mode == 1 ? 1.0f / mass : 1.0f;
+  std::vector<float> scaled((size_t)K);
+  for (int j = 0; j < K; ++j) scaled[(size_t)j] = (mode == 1 ? logf(c[j].v * inv_m) : c[j].v) * inv_t;
+  float mx = -INFINITY;
+  for (int j = 0; j < K; ++j) mx = std::max(mx, scaled[(size_t)j]);
+  std::vector<float> pr((size_t)K);
+  float sum = 0.f;
+  for (int j = 0; j < K; ++j) pr[(size_t)j] = expf(scaled[(size_t)j] - mx);
+  for (int j = 0; j < K; ++j) sum += pr[(size_t)j];
+  const float inv_sum = 1.0f / sum;
+  for (int j = 0; j < K; ++j) pr[(size_t)j] *= inv_sum;
+  float cum = 0.f;
+  int cut = K;
+  for (int j = 0; j < K; ++j) {
+    cum += pr[(size_t)j];
+    if (cum >= sp.top_p) {
+      cut = j + 1;
+      break;
+    }
+  }
+  float ns = 0.f;
+  for (int j = 0; j < cut; ++j) ns += pr[(size_t)j];
+  const float ninv = 1.0f / ns;
+  for (int j = 0; j < cut; ++j) pr[(size_t)j] *= ninv;
+  const float r = lcg_next(rng);
+  float acc = 0.f;
+  uint32_t chosen = (uint32_t)c[0].i;
+  for (int j = 0; j < cut; ++j) {
+    acc += pr[(size_t)j];
+    if (r <= acc) {
+      chosen = (uint32_t)c[j].i;
+      break;
+    }
+  }
+  return chosen;
+}
+
 static int check_sampling(const dz_sampling* sp) {
   if (!sp) return set_error(DZ_ERR_TENSOR, "sampling: null parameters");
   if (sp->temperature > 0.f && (sp->top_k < 1 || !(sp->top_p > 0.f)))
@@ -204,39 +252,122 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   int vocab = 0;
   if ((rc = dz_ctx_vocab(c, &vocab))) return rc;
   const size_t V = (size_t)vocab;
-  // rows[0]: the context's logits (predict draft[0]); rows[i + 1]: after draft[i]
-  std::vector<float> rows((size_t)(k + 1) * V);
-  if ((rc = dz_ctx_logits(c, rows.data()))) return rc;
-  if ((rc = dz_verify_forward(c, draft, k, rows.data() + V))) return rc;
-  Sampler s;
-  int acc = 0;
-  bool eos = false;
-  uint32_t b = 0;
-  bool have_bonus = false;
-  for (int i = 0; i < k; ++i) {
-    const float* tl = rows.data() + (size_t)i * V;
-    const float* dl = greedy ? nullptr : draft_logits + (size_t)i * V;
-    int ok;
-    if (greedy) {
-      ok = argmax_of(tl, V) == draft[i];
-    } else {
+  const int K = greedy ? 1 : std::min(sp->top_k, vocab);
+  if (K > kSpecMaxK) {
+    // a top-k beyond what the device pass keeps: every row to the host, the sampler of dz_sample
+    std::vector<float> rows((size_t)(k + 1) * V);
+    if ((rc = dz_ctx_logits(c, rows.data()))) return rc;
+    if ((rc = dz_verify_forward(c, draft, k, rows.data() + V))) return rc;
+    Sampler s;
+    int acc = 0;
+    bool eos = false, have = false;
+    uint32_t b = 0;
+    for (int i = 0; i < k && !have && !eos; ++i) {
+      const float* tl = rows.data() + (size_t)i * V;
+      const float* dl = draft_logits + (size_t)i * V;
       float p, q;
       softmax_pair_single(tl, dl, V, draft[i], &p, &q);
       const float r = q > 1e-12f ? p / q : 0.f;
+      if (!(lcg_next(rng_state) < r)) {
+        b = s.bonus(tl, dl, V, *sp, rng_state);
+        have = true;
+      } else {
+        ++acc;
+        eos = eos_id >= 0 && draft[i] == (uint32_t)eos_id;
+      }
+    }
+    if (!have && !eos) b = s.top_k_top_p(rows.data() + (size_t)k * V, V, *sp, rng_state);
+    if ((rc = dz_verify_commit(c, eos ? acc - 1 : acc))) return rc;
+    *n_accepted = acc;
+    *bonus = eos ? 0xFFFFFFFFu : b;
+    return DZ_OK;
+  }
+  if ((rc = dz_verify_forward(c, draft, k, nullptr))) return rc;
+  const float *row0, *rows;
+  hipStream_t st;
+  Scratch* scr;
+  if ((rc = ctx_verify_view(c, &row0, &rows, &st, &scr))) return rc;
+  // scratch: draft logits [k][V] | tokens [k] | stats [k+1] | slice candidates | masses | top-k | total
+  const int nsl = spec_slices(vocab);
+  const size_t off_tok = greedy ? 0 : (size_t)k * V * 4, off_st = off_tok + 256 * ((k * 4 + 255) / 256);
+  const size_t off_cand = off_st + 256 * (((size_t)(k + 1) * sizeof(SpecRowStats) + 255) / 256);
+  const size_t off_mass = off_cand + (size_t)nsl * kSpecMaxK * sizeof(SpecCand);
+  const size_t off_top = off_mass + 256 * ((nsl * 4 + 255) / 256);
+  const size_t off_tot = off_top + kSpecMaxK * sizeof(SpecCand);
+  if ((rc = scr->reserve(off_tot + 256))) return rc;
+  char* base = static_cast<char*>(scr->ptr);
+  float* dl_dev = greedy ? nullptr : reinterpret_cast<float*>(base);
+  uint32_t* tok_dev = reinterpret_cast<uint32_t*>(base + off_tok);
+  SpecRowStats* st_dev = reinterpret_cast<SpecRowStats*>(base + off_st);
+  SpecCand* cand_dev = reinterpret_cast<SpecCand*>(base + off_cand);
+  float* mass_dev = reinterpret_cast<float*>(base + off_mass);
+  SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
+  float* tot_dev = reinterpret_cast<float*>(base + off_tot);
+  if (!greedy) DZ_HIP_CHECK(hipMemcpyAsync(dl_dev, draft_logits, (size_t)k * V * 4, hipMemcpyHostToDevice, st));
+  DZ_HIP_CHECK(hipMemcpyAsync(tok_dev, draft, (size_t)k * 4, hipMemcpyHostToDevice, st));
+  hipLaunchKernelGGL(spec_stats_kernel, dim3((unsigned)(k + 1)), dim3(1024), 0, st, row0, rows, (const float*)dl_dev, k,
+                     vocab, (const uint32_t*)tok_dev, st_dev);
+  DZ_HIP_CHECK(hipGetLastError());
+  std::vector<SpecRowStats> stats((size_t)k + 1);
+  DZ_HIP_CHECK(hipMemcpyAsync(stats.data(), st_dev, stats.size() * sizeof(SpecRowStats), hipMemcpyDeviceToHost, st));
+  DZ_HIP_CHECK(hipStreamSynchronize(st));
+  // the row (target, draft) and mode the bonus is drawn from: -1 when there is none
+  auto row_ptr = [&](int r) { return r == 0 ? row0 : rows + (size_t)(r - 1) * V; };
+  auto topk = [&](int r, int mode, std::vector<SpecCand>& out, float* mass) -> int {
+    hipLaunchKernelGGL(spec_topk_slice_kernel, dim3((unsigned)nsl), dim3(256), 0, st, row_ptr(r),
+                       (const float*)(dl_dev ? dl_dev + (size_t)r * V : nullptr), vocab, mode,
+                       (const SpecRowStats*)(st_dev + r), K, cand_dev, mass_dev);
+    DZ_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), 0, st, (const SpecCand*)cand_dev, nsl, K,
+                       (const float*)mass_dev, top_dev, tot_dev);
+    DZ_HIP_CHECK(hipGetLastError());
+    out.resize((size_t)K);
+    DZ_HIP_CHECK(hipMemcpyAsync(out.data(), top_dev, (size_t)K * sizeof(SpecCand), hipMemcpyDeviceToHost, st));
+    DZ_HIP_CHECK(hipMemcpyAsync(mass, tot_dev, 4, hipMemcpyDeviceToHost, st));
+    DZ_HIP_CHECK(hipStreamSynchronize(st));
+    return DZ_OK;
+  };
+  int acc = 0;
+  bool eos = false, have = false;
+  uint32_t b = 0;
+  std::vector<SpecCand> cands;
+  for (int i = 0; i < k && !have && !eos; ++i) {
+    const SpecRowStats& s = stats[(size_t)i];
+    bool ok;
+    if (greedy) {
+      ok = (uint32_t)s.argmax == draft[i];
+    } else {
+      const float r = s.q > 1e-12f ? s.p / s.q : 0.f;
       ok = lcg_next(rng_state) < r;
     }
     if (!ok) {
-      b = greedy ? (uint32_t)argmax_of(tl, V) : s.bonus(tl, dl, V, *sp, rng_state);
-      have_bonus = true;
-      break;
-    }
-    ++acc;
-    if (eos_id >= 0 && draft[i] == (uint32_t)eos_id) {  // an accepted EOS ends generation unforwarded
-      eos = true;
-      break;
+      have = true;
+      if (greedy) {
+        b = (uint32_t)s.argmax;
+      } else {
+        float mass = 0.f;
+        if ((rc = topk(i, 1, cands, &mass))) return rc;
+        if (mass <= 1e-12f) {  // no residual mass: sample the target itself
+          if ((rc = topk(i, 0, cands, &mass))) return rc;
+          b = sample_candidates(cands.data(), K, 0, 0.f, *sp, rng_state);
+        } else {
+          b = sample_candidates(cands.data(), K, 1, mass, *sp, rng_state);
+        }
+      }
+    } else {
+      ++acc;
+      eos = eos_id >= 0 && draft[i] == (uint32_t)eos_id;  // an accepted EOS ends generation unforwarded
     }
   }
-  if (!have_bonus && !eos) b = s.top_k_top_p(rows.data() + (size_t)k * V, V, *sp, rng_state);
+  if (!have && !eos) {
+    if (greedy) {
+      b = (uint32_t)stats[(size_t)k].argmax;
+    } else {
+      float mass = 0.f;
+      if ((rc = topk(k, 0, cands, &mass))) return rc;
+      b = sample_candidates(cands.data(), K, 0, 0.f, *sp, rng_state);
+    }
+  }
   if ((rc = dz_verify_commit(c, eos ? acc - 1 : acc))) return rc;
   *n_accepted = acc;
   *bonus = eos ? 0xFFFFFFFFu : b;

@@ -1,0 +1,200 @@
+// spec_kernels.h — the vocabulary-wide parts of speculative sampling on the device, so that a verify
+// step returns a few words instead of k+1 logits rows: per-row softmax statistics with the draft
+// token's probabilities (softmax_pair_single_avx2, Daiza-engine/src/math/simd_exp.rs:656-767) and the
+// target's argmax (argmax_avx2, simd_exp.rs:551-598), and the top-k candidates of a row or of the
+// residual distribution max(0, p - q) with its mass (sample_bonus, Daiza-runtime/src/engine.rs:
+// 1833-1866; residual_max_zero_sum_avx2, simd_exp.rs:605-642).  The host finishes the reference's
+// temperature / top-k / top-p draw (sampling.rs:144-247) on those candidates.
+#pragma once
+#include "common.h"
+
+namespace dz {
+
+struct SpecRowStats {
+  float tmax, tsum, dmax, dsum;  // target / draft maximum and sum of exp(x - max)
+  float p, q;                    // softmax(target)[token], softmax(draft)[token]
+  int argmax;                    // first maximum of the target
+  int pad;
+};
+
+struct SpecCand {
+  float v;
+  int i;
+};
+
+// (v, i) is ahead of (w, j) in the order "larger value first, then lower index".
+__device__ __forceinline__ bool cand_ahead(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+
+template <int NT>
+__device__ __forceinline__ void block_best(float& v, int& i, float* sv, int* si) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o);
+    const int j = __shfl_xor(i, o);
+    if (cand_ahead(w, j, v, i)) {
+      v = w;
+      i = j;
+    }
+  }
+  const unsigned tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63u) == 0) {
+    sv[tid >> 6] = v;
+    si[tid >> 6] = i;
+  }
+  __syncthreads();
+  v = sv[0];
+  i = si[0];
+  for (int w = 1; w < NT / 64; ++w)
+    if (cand_ahead(sv[w], si[w], v, i)) {
+      v = sv[w];
+      i = si[w];
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ float block_total(float s, float* sv) {
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const unsigned tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63u) == 0) sv[tid >> 6] = s;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < NT / 64; ++w) t += sv[w];
+  return t;
+}
+
+// Grid n, 1024 threads.  Row r's target logits: row0 for r = 0, rows + (r-1)·V after; its draft logits
+// drafts + r·V for r < nd (none for greedy or past the drafts: statistics of the target only);
+// tok[r] is draft token r (r < nd).
+__global__ __launch_bounds__(1024) void spec_stats_kernel(const float* __restrict__ row0, const float* __restrict__ rows,
+                                                          const float* __restrict__ drafts, int nd, int V,
+                                                          const uint32_t* __restrict__ tok, SpecRowStats* out) {
+  constexpr int NT = 1024;
+  __shared__ float sv[NT / 64];
+  __shared__ int si[NT / 64];
+  const int r = blockIdx.x;
+  const float* t = r == 0 ? row0 : rows + (size_t)(r - 1) * V;
+  const float* d = drafts && r < nd ? drafts + (size_t)r * V : nullptr;
+  float tm = -INFINITY, dm = -INFINITY;
+  int ti = 0x7FFFFFFF;
+  for (int i = threadIdx.x; i < V; i += NT) {
+    const float x = t[i];
+    if (cand_ahead(x, i, tm, ti)) {
+      tm = x;
+      ti = i;
+    }
+    if (d) dm = fmaxf(dm, d[i]);
+  }
+  block_best<NT>(tm, ti, sv, si);
+  float dmv = dm;
+  int dummy = 0;
+  block_best<NT>(dmv, dummy, sv, si);
+  float ts = 0.f, ds = 0.f;
+  for (int i = threadIdx.x; i < V; i += NT) {
+    ts += expf(t[i] - tm);
+    if (d) ds += expf(d[i] - dmv);
+  }
+  ts = block_total<NT>(ts, sv);
+  ds = block_total<NT>(ds, sv);
+  if (threadIdx.x == 0) {
+    SpecRowStats s;
+    const int k = r < nd ? (int)tok[r] : 0;
+    s.tmax = tm;
+    s.tsum = ts;
+    s.dmax = dmv;
+    s.dsum = ds;
+    const float tsn = ts > 0.f ? ts : 1.f, dsn = ds > 0.f ? ds : 1.f;
+    s.p = expf(t[k] - tm) / tsn;
+    s.q = d ? expf(d[k] - dmv) / dsn : 0.f;
+    s.argmax = ti;
+    s.pad = 0;
+    out[r] = s;
+  }
+}
+
+// The value a top-k pass ranks: the logit itself (mode 0) or the residual mass
+// max(0, softmax(t)_i - softmax(d)_i) of sample_bonus (mode 1, softmax as softmax_inplace: times 1/sum).
+__device__ __forceinline__ float spec_value(const float* t, const float* d, int i, int mode, const SpecRowStats& s) {
+  if (mode == 0) return t[i];
+  const float p = expf(t[i] - s.tmax) * (1.0f / s.tsum), q = expf(d[i] - s.dmax) * (1.0f / s.dsum);
+  return fmaxf(p - q, 0.0f);
+}
+
+constexpr int kSpecSlice = 4096;  // elements per slice of a top-k pass (held in LDS)
+constexpr int kSpecMaxK = 64;
+__host__ __device__ inline int spec_slices(int V) { return (V + kSpecSlice - 1) / kSpecSlice; }
+
+// Stage 1: grid spec_slices(V), 256 threads.  Slice s of the row (kSpecSlice elements, in LDS) keeps
+// its K best (value, index) in order and, in mode 1, its residual mass.
+__global__ __launch_bounds__(256) void spec_topk_slice_kernel(const float* __restrict__ t, const float* __restrict__ d,
+                                                              int V, int mode, const SpecRowStats* __restrict__ st,
+                                                              int K, SpecCand* __restrict__ cand,
+                                                              float* __restrict__ mass) {
+  constexpr int NT = 256;
+  __shared__ float sv[NT / 64];
+  __shared__ int si[NT / 64];
+  __shared__ float vals[kSpecSlice];
+  const SpecRowStats s = *st;
+  const int i0 = blockIdx.x * kSpecSlice, n = min(V - i0, kSpecSlice);
+  float m = 0.f;
+  for (int j = threadIdx.x; j < n; j += NT) {
+    const float v = spec_value(t, d, i0 + j, mode, s);
+    vals[j] = v;
+    m += v;
+  }
+  m = block_total<NT>(m, sv);  // (its barriers also publish vals)
+  if (threadIdx.x == 0) mass[blockIdx.x] = mode == 1 ? m : 0.f;
+  float pv = INFINITY;
+  int pi = -1;  // the previous pick: candidates must come after it in the order
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int j = threadIdx.x; j < n; j += NT) {
+      const float v = vals[j];
+      const int i = i0 + j;
+      if (cand_ahead(pv, pi, v, i) && cand_ahead(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+    block_best<NT>(bv, bi, sv, si);
+    if (threadIdx.x == 0) cand[(size_t)blockIdx.x * K + k] = SpecCand{bv, bi};
+    pv = bv;
+    pi = bi;
+  }
+}
+
+// Stage 2: one workgroup of 256 threads merges the slices' candidates into the row's K best, in
+// order, and adds the slices' masses in slice order.
+__global__ __launch_bounds__(256) void spec_topk_merge_kernel(const SpecCand* __restrict__ cand, int slices, int K,
+                                                              const float* __restrict__ mass, SpecCand* __restrict__ out,
+                                                              float* __restrict__ total) {
+  constexpr int NT = 256;
+  __shared__ float sv[NT / 64];
+  __shared__ int si[NT / 64];
+  const int n = slices * K;
+  float pv = INFINITY;
+  int pi = -1;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int c = threadIdx.x; c < n; c += NT) {
+      const SpecCand x = cand[c];
+      if (x.i != 0x7FFFFFFF && cand_ahead(pv, pi, x.v, x.i) && cand_ahead(x.v, x.i, bv, bi)) {
+        bv = x.v;
+        bi = x.i;
+      }
+    }
+    block_best<NT>(bv, bi, sv, si);
+    if (threadIdx.x == 0) out[k] = SpecCand{bv, bi};
+    pv = bv;
+    pi = bi;
+  }
+  if (threadIdx.x == 0) {
+    float m = 0.f;
+    for (int s = 0; s < slices; ++s) m += mass[s];
+    *total = m;
+  }
+}
+
+}  // namespace dz

@@ -122,11 +122,13 @@ def _reference_step(oracle, om, target, draft, draft_logits, T, top_k, top_p, rn
     return acc, oracle.sample_top_k_top_p(target, T, top_k, top_p, rng)
 
 
-@pytest.mark.parametrize("case", ["all_accept", "reject_at_3", "random_drafts", "greedy", "eos"])
+@pytest.mark.parametrize("case", ["all_accept", "reject_at_3", "random_drafts", "greedy", "eos", "wide_top_k"])
 def test_spec_verify_matches_sequential_reference(dz, oracle, case):
+    """The vocabulary-wide sampling runs on the device for top_k <= 64 and on the host beyond
+    (wide_top_k); both must follow the reference draw for draw."""
     cfg = dz.Config.small(n_layers=8, max_ctx=96)
     prompt = _ids(cfg, 10, 6)
-    T, top_k, top_p = (0.0, 20, 0.95) if case == "greedy" else (0.7, 20, 0.95)
+    T, top_k, top_p = (0.0, 20, 0.95) if case == "greedy" else (0.7, 100 if case == "wide_top_k" else 20, 0.95)
     k = 8
     m, ctx, _ = _gpu(dz, cfg, prompt)
     om, olg = _oracle(oracle, cfg, prompt)
@@ -146,7 +148,7 @@ def test_spec_verify_matches_sequential_reference(dz, oracle, case):
         draft[3] = int(np.argmin(dlog[3]))
         dlog[3] = rng.standard_normal(cfg.vocab).astype(np.float32) * 0.1
         dlog[3][draft[3]] = 30.0
-    elif case == "random_drafts":
+    elif case in ("random_drafts", "wide_top_k"):
         draft = _ids(cfg, k, 9)
         dlog = np.random.default_rng(10).standard_normal((k, cfg.vocab)).astype(np.float32)
     elif case == "eos":

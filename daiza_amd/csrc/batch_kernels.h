@@ -103,7 +103,8 @@ struct DnRecord {
 
 // Gated delta rule over the chunk's tokens in order (ssm_scan_vhead, ssm.rs:153-180; fused form
 // 378-418).  Workgroup (v-head vh, quarter) holds state rows i = quarter·32 + (tid >> 3),
-// columns j = 16·(tid & 7) .. +16 of S[vh][j][i] in registers; the 8 threads of a row sum with DPP.
+// columns j = 16·(tid & 7) .. +16 of S[vh][i][j] in registers (64 contiguous bytes per thread); the 8
+// threads of a row sum with DPP.
 // Per token: g = ssm_a·softplus(alpha + dt_bias), decay = exp(g), beta = sigmoid(b); s *= decay;
 // kv = s·k; d = (v_i - kv)·beta; s += d·k; y_i = s·q.  The next token's inputs are loaded while
 // this one computes.  With rec == null the state is written back at the end; otherwise it is left
@@ -119,10 +120,9 @@ __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ 
   const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % nkh;
   const int i = quarter * 32 + (int)(tid >> 3), js = (int)(tid & 7u);
   const int64_t kdim = (int64_t)nkh * HD;
-  float* S = state + (size_t)vh * HD * HD;
+  float* S = state + (size_t)vh * HD * HD + (size_t)i * HD + 16 * js;
   float s[16];
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  state_row_load(S, s);
   const float A = ssm_a[vh], dtb = dt_bias[vh];
   auto load = [&](int t, float4 (&k4)[4], float4 (&q4)[4], float& v, float& al, float& be) {
     const float* qr = qk + (size_t)t * 2 * kdim + (size_t)kh * HD + 16 * js;
@@ -184,10 +184,7 @@ __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ 
     alc = aln;
     bec = ben;
   }
-  if (!rec.d) {
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) S[(size_t)(js * 16 + jj) * HD + i] = s[jj];
-  }
+  if (!rec.d) state_row_store(S, s);
 }
 
 // Applies the first a recorded tokens of a verify chunk to the state: s = decay·s, s = fma(d, k, s)
@@ -199,10 +196,9 @@ __global__ __launch_bounds__(256) void bt_commit_state_kernel(float* __restrict_
   const unsigned tid = threadIdx.x;
   const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % nkh;
   const int i = quarter * 32 + (int)(tid >> 3), js = (int)(tid & 7u);
-  float* S = state + (size_t)vh * HD * HD;
+  float* S = state + (size_t)vh * HD * HD + (size_t)i * HD + 16 * js;
   float s[16];
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  state_row_load(S, s);
   for (int t = 0; t < a; ++t) {
     const float decay = rec.decay[(size_t)t * nvh + vh];
     const float d = rec.d[(size_t)t * nvh * HD + (int64_t)vh * HD + i];
@@ -212,8 +208,7 @@ __global__ __launch_bounds__(256) void bt_commit_state_kernel(float* __restrict_
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) s[jj] = __builtin_fmaf(d, kr[jj], s[jj]);
   }
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) S[(size_t)(js * 16 + jj) * HD + i] = s[jj];
+  state_row_store(S, s);
 }
 
 // Output gate per v-head (ssm_output_gate_avx2, ssm.rs:246-286):

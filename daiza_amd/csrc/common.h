@@ -25,6 +25,26 @@ constexpr int kLutBytes = 256 * kTilePos * 4;        // 64 KiB: f32 [256 sign-by
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
+// DeltaNet state: [v-head][row i][column j] (row-major S[i][j]).  A thread holding 16 consecutive
+// columns of one row moves them as four 16-byte words, so the 8 threads of a row cover 512
+// contiguous bytes.  p is 16-byte aligned.
+__device__ __forceinline__ void state_row_load(const float* p, float (&s)[16]) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float4 v = q[c];
+    s[4 * c] = v.x;
+    s[4 * c + 1] = v.y;
+    s[4 * c + 2] = v.z;
+    s[4 * c + 3] = v.w;
+  }
+}
+__device__ __forceinline__ void state_row_store(float* p, const float (&s)[16]) {
+  float4* q = reinterpret_cast<float4*>(p);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) q[c] = make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]);
+}
+
 // Device copy of one Q1_0 matrix in the GEMV layout.
 //   unit (rb, t) at byte offset (rb * T + t) * kUnitBytes:
 //     [chunk c 0..3][lane L 0..63][16 B]  stored sign byte s = 16c + i of lane L is the original

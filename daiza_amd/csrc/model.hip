@@ -64,7 +64,7 @@ struct dz_ctx {
   float *h_fin = nullptr, *ss_fin = nullptr, *logits = nullptr, *am_val = nullptr;
   int* am_idx = nullptr;
   int n_am = 0;
-  float* ssm_state = nullptr;  // [n_ssm][nvh][128 j][128 i]
+  float* ssm_state = nullptr;  // [n_ssm][nvh][128 i][128 j] (row-major S[i][j], as the API)
   float* conv = nullptr;       // [n_ssm][4][qkvd]
   float* kv = nullptr;         // [n_attn][2][nkv][max_ctx][hd]
   float* rope = nullptr;       // [max_ctx][rope_dim]
@@ -1584,11 +1584,8 @@ int dz_ctx_set_ssm_state(dz_ctx* x, int layer, const float* state, const float* 
   const dz_config& c = x->m->cfg;
   const int64_t hd = c.ssm_state, nvh = c.ssm_v_heads, qkvd = (2 * (int64_t)c.ssm_k_heads + nvh) * hd;
   if (conv_head < 0 || conv_head > 3) return set_error(DZ_ERR_TENSOR, "conv_head %d", conv_head);
-  std::vector<float> tr((size_t)(nvh * hd * hd));
-  for (int64_t v = 0; v < nvh; ++v)
-    for (int64_t i = 0; i < hd; ++i)
-      for (int64_t j = 0; j < hd; ++j) tr[(size_t)((v * hd + j) * hd + i)] = state[(size_t)((v * hd + i) * hd + j)];
-  DZ_HIP_CHECK(hipMemcpy(x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, tr.data(), tr.size() * 4, hipMemcpyHostToDevice));
+  DZ_HIP_CHECK(hipMemcpy(x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, state, (size_t)(nvh * hd * hd) * 4,
+                         hipMemcpyHostToDevice));
   DZ_HIP_CHECK(hipMemcpy(x->conv + (size_t)l->kind_idx * 4 * qkvd, conv_hist, (size_t)(4 * qkvd) * 4, hipMemcpyHostToDevice));
   const int base = ((conv_head - x->pos_host) % 4 + 4) % 4;
   x->ring_base[l->kind_idx] = base;
@@ -1603,12 +1600,9 @@ int dz_ctx_get_ssm_state(dz_ctx* x, int layer, float* state, float* conv_hist, i
   const dz_config& c = x->m->cfg;
   const int64_t hd = c.ssm_state, nvh = c.ssm_v_heads, qkvd = (2 * (int64_t)c.ssm_k_heads + nvh) * hd;
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
-  std::vector<float> tr((size_t)(nvh * hd * hd));
-  DZ_HIP_CHECK(hipMemcpy(tr.data(), x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, tr.size() * 4, hipMemcpyDeviceToHost));
   if (state)
-    for (int64_t v = 0; v < nvh; ++v)
-      for (int64_t i = 0; i < hd; ++i)
-        for (int64_t j = 0; j < hd; ++j) state[(size_t)((v * hd + i) * hd + j)] = tr[(size_t)((v * hd + j) * hd + i)];
+    DZ_HIP_CHECK(hipMemcpy(state, x->ssm_state + (size_t)l->kind_idx * nvh * hd * hd, (size_t)(nvh * hd * hd) * 4,
+                           hipMemcpyDeviceToHost));
   if (conv_hist)
     DZ_HIP_CHECK(hipMemcpy(conv_hist, x->conv + (size_t)l->kind_idx * 4 * qkvd, (size_t)(4 * qkvd) * 4, hipMemcpyDeviceToHost));
   if (conv_head) *conv_head = (x->ring_base[l->kind_idx] + x->pos_host) & 3;

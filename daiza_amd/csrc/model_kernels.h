@@ -431,7 +431,7 @@ struct DeltaArgs {
   const float* conv_w;  // [4][qkvd] (tap-major, tap 3 = newest)
   const float* ssm_a;   // [nvh]
   const float* dt_bias; // [nvh]
-  float* state;         // [nvh][128 j][128 i]
+  float* state;         // [nvh][128 i][128 j] (row-major S[i][j])
   float* y;             // [nvh*128] raw readout
   float* zs;            // [nvh*128] silu(z)
   int nkh, nvh;
@@ -458,10 +458,9 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
 
   // ---- every global load first (one memory round trip) ----
   // state rows i, k-slice [16*js, 16*js+16)
-  float* S = a.state + (size_t)vh * HD * HD;
+  float* S = a.state + (size_t)vh * HD * HD + (size_t)i * HD + 16 * js;
   float s[16];
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) s[jj] = S[(size_t)(js * 16 + jj) * HD + i];
+  state_row_load(S, s);
   const float inv = inv_rms_from(a.ss, a.nss, a.H, a.rms_eps);
   // conv channel of this thread: q (tid < 128) or k (tid >= 128) of k-head kh
   const int64_t ch = tid < HD ? (int64_t)kh * HD + tid : kdim + (int64_t)kh * HD + (tid - HD);
@@ -551,9 +550,9 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   for (int jj = 0; jj < 16; ++jj) {
     const int j = js * 16 + jj;
     s[jj] = __builtin_fmaf(d, ks[j], s[jj]);
-    S[(size_t)j * HD + i] = s[jj];
     yp = __builtin_fmaf(s[jj], qs[j], yp);
   }
+  state_row_store(S, s);
   part[js][i_loc] = yp;  // the kv reads of part finished before the previous barrier
   __syncthreads();
   if (js == 0) {

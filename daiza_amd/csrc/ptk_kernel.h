@@ -287,10 +287,14 @@ __device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->t
 // registers (requested by an earlier phase), publish LL partials [t][row] and request the next
 // GEMV's weights (nx, UNX slots) into the same registers.  The sync wave leaves once the table is
 // built and goes on to its next phase while the compute waves finish.
-template <bool SYNC, int UN, int UNX, int U, class Src>
+struct NoPost {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <bool SYNC, int UN, int UNX, int U, class Src, class Post = NoPost>
 __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, const Src& src, WRegs<U>& r, const Assign& a,
                                            bool lead, u64* out, int64_t ld, unsigned tag, unsigned tid,
-                                           const PtkErr& e, const NextW& nx, const TraceAt& tr) {
+                                           const PtkErr& e, const NextW& nx, const TraceAt& tr,
+                                           const Post& post = Post{}) {
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
   bool ok = prior;
@@ -328,6 +332,7 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
       if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, y[m], tag);
     }
     tr.last_wave(smem, tid);
+    post();
 #pragma unroll
     for (int m = 0; m < UNX; ++m) gemv_prefetch_slot<U>(nx.W, nx.ntiles, nx.t, nx.rb0, nx.rb1, tid, r, m);
   }
@@ -618,10 +623,10 @@ __device__ __forceinline__ void dn_state_load(const PtkPlan& P, const PtkLayer& 
   const int vh = w >> 2, quarter = w & 3;
   const unsigned lane = tid & 63u, w4 = (tid >> 6) - 4, il = lane >> 3, js = lane & 7u;
   const int i = quarter * 32 + (int)(w4 * 8 + il);
-  const float* S = v ? Ly.state + (size_t)vh * 128 * 128 + (size_t)js * 16 * 128 + i : P.output_norm;
-  const int st = v ? 128 : 1;
-#pragma unroll
-  for (int jj = 0; jj < 16; ++jj) s[jj] = co_ld(S + (size_t)jj * st);
+  // Row i's 16 columns js*16.. are 64 contiguous bytes (S[vh][i][j]).  Plain loads: within a launch
+  // these rows are written only by this thread (the delta rule below), and writes by other kernels
+  // are made visible by the launch boundary.
+  state_row_load(v ? Ly.state + (size_t)vh * 128 * 128 + (size_t)i * 128 + (size_t)js * 16 : P.output_norm, s);
 }
 
 // Workgroup w < 4*nvh: v-head w/4, state rows (w%4)*32 .. +32 (ssm.rs:425-616).  The sync wave takes
@@ -763,12 +768,13 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
       c[sl] = siluf_(o);
     }
     if (ok) {
+      // silu(z) first (the out-projection waits for it), then the conv ring
+      if (!vlane) ll_st(zs + (size_t)vh * HD + quarter * 32 + (lane - 32), siluf_(xn[4]), tag);
       if (vh < P.nkh && quarter == 0) {
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) co_st(Ly.conv + (size_t)hb * qkvd + row[sl], xn[sl]);
       }
       if (vlane) co_st(Ly.conv + (size_t)hb * qkvd + row[4], xn[4]);
-      else ll_st(zs + (size_t)vh * HD + quarter * 32 + (lane - 32), siluf_(xn[4]), tag);
     }
     if (lane == 0) {
       const float xa = xn[5] + gl[1];
@@ -813,18 +819,19 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
     }
     const float kv = group8_sum(kvp);
     const float d = (vi - kv) * beta;
-    float* S = Ly.state + (size_t)vh * HD * HD;
     float yp = 0.f;
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
       s[jj] = __builtin_fmaf(d, kk[jj], s[jj]);
-      co_st(S + (size_t)(js * 16 + jj) * HD + i, s[jj]);
       yp = __builtin_fmaf(s[jj], qq[jj], yp);
     }
     const float yy = group8_sum(yp);
     if (js == 0) ll_st(y + (size_t)vh * HD + i, yy, tag);
     const float ys = wave_sum(js == 0 ? yy * yy : 0.f);
     if (lane == 0) ll_st(yss + (size_t)vh * 16 + quarter * 4 + w4, ys, tag);
+    // the state rows after the outputs: the out-projection waits for y, and the CU's memory pipeline
+    // is in order (16 partial-line stores per thread would otherwise go first)
+    state_row_store(Ly.state + (size_t)vh * HD * HD + (size_t)i * HD + (size_t)js * 16, s);
   }
   return true;
 }
@@ -1210,25 +1217,33 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         const Assign a_out = asg_at(smem, 2 + Ly.attn);
         const Assign a_gu = asg_at(smem, 4);
         const Assign a_dn = asg_at(smem, 5);
-        // The DeltaNet state rows (every layer loads: an attention layer reads 16 words of one cache
-        // line, so that no phi forms), then the in-projection weights.  Every prefetch is issued in
-        // the block that uses it: a loaded value carried around a loop becomes a phi, resolved with
-        // register copies that wait for the loads.
+        // The in-projection weights.  Every prefetch is issued in the block that uses it: a loaded
+        // value carried around a loop becomes a phi, resolved with register copies that wait for the
+        // loads.
         if constexpr (!SYNC) {
-          dn_conv_load(P, Ly, w, tid, lds_ptr<int>(smem, kLdsRing)[l], pos, cin);
-          dn_state_load(P, Ly, w, tid, sreg);
+          ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 64, 1);
           const Assign a = asg_at(smem, Ly.attn);
           gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
+          ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 64, 2);
         }
         // A: in-proj of h * attn_norm; tile leaders publish sum(h^2) per tile (1/rms applied downstream).
-        // In a DeltaNet layer the out-proj weights follow slot by slot (an attention layer requests
-        // them after its cache reads, and here reads one line per slot instead).
+        // After its stores the compute waves request the DeltaNet conv inputs and state rows (every
+        // layer loads: an attention layer reads 16 words of one cache line, so that no phi forms) and
+        // then, in a DeltaNet layer, the out-proj weights slot by slot (an attention layer requests
+        // them after its cache reads, and here reads one line per slot instead).  Requested at the
+        // layer's start, the state rows -- 512 partial-line reads per workgroup -- sat in the CU's
+        // memory queue ahead of the sync wave's polls for this phase's inputs.
         {
           const Assign a = asg_at(smem, Ly.attn);
           SrcNormedLL src{h_in, tag_h, Ly.attn_norm, P.H, R + O.sst_in};
           const NextW nx{Ly.w_out, Ly.nt_out, a_out.t, a_out.rb0, Ly.attn ? a_out.rb0 : a_out.rb1};
+          const int ring_l = lds_ptr<int>(smem, kLdsRing)[l];
+          auto post = [&]() {
+            dn_conv_load(P, Ly, w, tid, ring_l, pos, cin);
+            dn_state_load(P, Ly, w, tid, sreg);
+          };
           if (!gemv_phase<SYNC, U_IN, U_OUT>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid,
-                                             e, nx, TraceAt{&r, &P, i, Ly.ph0, w}))
+                                             e, nx, TraceAt{&r, &P, i, Ly.ph0, w}, post))
             return;
         }
         if (!Ly.attn) {
@@ -1282,6 +1297,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
             return;
         }
+        if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 64, 1);
       }
       h_in = R + O.h;
       tag_h = t0 + k + 4;

@@ -829,11 +829,21 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
     if (js == 0) ll_st(y + (size_t)vh * HD + i, yy, tag);
     const float ys = wave_sum(js == 0 ? yy * yy : 0.f);
     if (lane == 0) ll_st(yss + (size_t)vh * 16 + quarter * 4 + w4, ys, tag);
-    // the state rows after the outputs: the out-projection waits for y, and the CU's memory pipeline
-    // is in order (16 partial-line stores per thread would otherwise go first)
-    state_row_store(Ly.state + (size_t)vh * HD * HD + (size_t)i * HD + (size_t)js * 16, s);
+    // the state rows are stored by dn_state_store after the out-projection's stores
   }
   return true;
+}
+
+// Stores the state rows updated by phase_dn (waves 4..7 of workgroups w < 4*nvh).  Called after the
+// out-projection's partial stores: the CU's memory pipeline is in order, and 16 KiB of state stores
+// issued at the end of the DeltaNet phase sat ahead of the out-projection's input polls.
+__device__ __forceinline__ void dn_state_store(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned tid,
+                                               const float (&s)[16]) {
+  if (w >= 4 * P.nvh || tid < 256) return;
+  const int vh = w >> 2, quarter = w & 3;
+  const unsigned lane = tid & 63u, w4 = (tid >> 6) - 4, il = lane >> 3, js = lane & 7u;
+  const int i = quarter * 32 + (int)(w4 * 8 + il);
+  state_row_store(Ly.state + (size_t)vh * 128 * 128 + (size_t)i * 128 + (size_t)js * 16, s);
 }
 
 // ------------------------------------------------------------------ phase B': attention chunk
@@ -916,31 +926,28 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
   }
   const float* kb = Ly.kc + (size_t)kvh * P.max_ctx * HD;
   const float* vb = Ly.vc + (size_t)kvh * P.max_ctx * HD;
-  auto loadkv = [&](int p, float4& k4, float4& v4) {
-    if (p == pos) {
-      k4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
-      v4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
-    } else {
-      k4 = co_ld4(kb + (size_t)p * HD + 4 * lane);
-      v4 = co_ld4(vb + (size_t)p * HD + 4 * lane);
-    }
+  // Cache rows of position pp into slot registers.  Every slot is loaded unconditionally: a position
+  // past the chunk or the new one (which comes from LDS) reads the chunk's first row instead, and the
+  // value is never used -- a slot that were either loaded or left as it was would become a phi, and
+  // the register copies that resolve it wait for the loads.
+  auto ldkv = [&](int pp, float4& k4, float4& v4) {
+    const int pc = (pp < p1 && pp != pos) ? pp : p0;
+    k4 = co_ld4(kb + (size_t)pc * HD + 4 * lane);
+    v4 = co_ld4(vb + (size_t)pc * HD + 4 * lane);
   };
-  // a compute wave's first two positions are read from the cache while the sync wave runs the
-  // prologue (only the new position comes from it, through LDS after the barrier)
-  constexpr int NW = kPtkWaves;
-  int p = p0 + (int)wave;
-  float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka, kb1 = ka, vb1 = ka;
+  // Each wave keeps its next KD positions in flight: a compute wave requests its first KD while the
+  // sync wave runs the prologue, the sync wave after it (its own loads would delay its polls).
+  constexpr int NW = kPtkWaves, KD = 4;
+  const int p = p0 + (int)wave;
+  float4 kq[KD], vq[KD];
   if (!SYNC) {
-    if (p < p1 && p != pos) loadkv(p, ka, va);
-    if (p + NW < p1 && p + NW != pos) loadkv(p + NW, kb1, vb1);
+#pragma unroll
+    for (int d = 0; d < KD; ++d) ldkv(p + d * NW, kq[d], vq[d]);
   }
   if (!wg_ok(smem, ok)) return false;
   if (SYNC) {
-    if (p < p1) loadkv(p, ka, va);
-    if (p + NW < p1) loadkv(p + NW, kb1, vb1);
-  } else {
-    if (p == pos) loadkv(p, ka, va);
-    if (p + NW == pos) loadkv(p + NW, kb1, vb1);
+#pragma unroll
+    for (int d = 0; d < KD; ++d) ldkv(p + d * NW, kq[d], vq[d]);
   }
   // online softmax over this wave's positions (attention.rs:149-199); lane holds dims 4*lane..+3
   float m[GRP], l[GRP];
@@ -952,33 +959,36 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
     o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
     q4[gi] = *reinterpret_cast<const float4*>(&qs[gi * HD + 4 * lane]);
   }
-  for (; p < p1; p += NW) {
-    float4 kc = ka, vc = va;
-    if (p + 2 * NW < p1) loadkv(p + 2 * NW, kc, vc);
-    const float4 k4 = ka, v4 = va;
-    ka = kb1;
-    va = vb1;
-    kb1 = kc;
-    vb1 = vc;
-    float dp[GRP];
+  const float4 knew = *reinterpret_cast<const float4*>(&kn[4 * lane]);
+  const float4 vnew = *reinterpret_cast<const float4*>(&vn[4 * lane]);
+  for (int base = p; base < p1; base += KD * NW) {
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      float t = q4[gi].x * k4.x;
-      t = __builtin_fmaf(q4[gi].y, k4.y, t);
-      t = __builtin_fmaf(q4[gi].z, k4.z, t);
-      dp[gi] = __builtin_fmaf(q4[gi].w, k4.w, t);
-    }
+    for (int d = 0; d < KD; ++d) {
+      const int pp = base + d * NW;
+      if (pp < p1) {
+        const float4 k4 = pp == pos ? knew : kq[d], v4 = pp == pos ? vnew : vq[d];
+        float dp[GRP];
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      const float score = wave_sum(dp[gi]);
-      const float mn = fmaxf(m[gi], score);
-      const float al = __expf(m[gi] - mn), be = __expf(score - mn);
-      l[gi] = l[gi] * al + be;
-      o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
-      o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
-      o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
-      o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
-      m[gi] = mn;
+        for (int gi = 0; gi < GRP; ++gi) {
+          float t = q4[gi].x * k4.x;
+          t = __builtin_fmaf(q4[gi].y, k4.y, t);
+          t = __builtin_fmaf(q4[gi].z, k4.z, t);
+          dp[gi] = __builtin_fmaf(q4[gi].w, k4.w, t);
+        }
+#pragma unroll
+        for (int gi = 0; gi < GRP; ++gi) {
+          const float score = wave_sum(dp[gi]);
+          const float mn = fmaxf(m[gi], score);
+          const float al = __expf(m[gi] - mn), be = __expf(score - mn);
+          l[gi] = l[gi] * al + be;
+          o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
+          o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
+          o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
+          o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
+          m[gi] = mn;
+        }
+      }
+      if (base + KD * NW < p1) ldkv(pp + KD * NW, kq[d], vq[d]);
     }
   }
   tr(tid, 64, 1);
@@ -1256,8 +1266,9 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + 2, w, tid, 256);
           // C: out-proj
           SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
+          auto post = [&]() { dn_state_store(P, Ly, w, tid, sreg); };
           if (!gemv_phase<SYNC, U_OUT, 0>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e,
-                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 3, w}))
+                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 3, w}, post))
             return;
         } else {
           // B': attention chunks (then the out-proj weights, after the cache reads they would delay)

@@ -173,6 +173,27 @@ def test_graph_path_matches_oracle(dz, oracle, graph_path):
     assert list(got) == want
 
 
+@pytest.mark.parametrize("L", [300, 3000, 5000])
+def test_token_kernel_long_context(dz, oracle, L):
+    """The token kernel's attention chunks at long contexts (several rounds of cache reads per wave:
+    up to 10 positions per wave at L = 5000) against the oracle: N(0,1) cache of length L."""
+    cfg = dz.Config.small(n_layers=4, max_ctx=L + 16)
+    m, ctx, om = _pair(dz, oracle, cfg, seed=SEED + 11)
+    assert ctx.token_kernel
+    kvn = cfg.n_head_kv * L * cfg.head_dim
+    k = oracle.synth_normal(SEED, K_KV, 2, kvn).reshape(cfg.n_head_kv, L, cfg.head_dim)
+    v = oracle.synth_normal(SEED, K_KV, 3, kvn).reshape(cfg.n_head_kv, L, cfg.head_dim)
+    ctx.set_kv(3, k, v)
+    om.set_kv(3, k, v)
+    ctx.set_pos(L)
+    om.set_pos(L)
+    for t in (5, 1234, 77):
+        am, lg = ctx.forward_single_token(t)
+        oam, olg = om.forward(t)
+        assert normwise_rel(lg, olg) < 1e-3, t
+        assert am == oam
+
+
 def test_token_kernel_and_graph_agree(dz, monkeypatch):
     """The two launch paths compute the same per-position logits (small stack, 20 tokens)."""
     cfg = dz.Config.small(n_layers=8, max_ctx=64)

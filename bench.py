@@ -377,6 +377,7 @@ def main():
     ms = ev.elapsed_ms(0, 1)
     ev.destroy()
     tps = args.steps / (ms / 1e3)
+    decode_ctx_end = ctx.pos  # before the config-5 verify continues on this context
 
     log("decode %d tokens: %.2f tok/s" % (args.steps, tps))
     pos_timed = args.prefill + args.warmup
@@ -416,7 +417,7 @@ def main():
                         "then greedy decode" % args.prefill,
             "prefill_tokens": args.prefill,
             "decode_tokens": args.steps,
-            "context_at_end": ctx.pos,
+            "context_at_end": decode_ctx_end,
             "q1_weight_bytes_per_token": wbytes,
             "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
             "weight_roofline_frac": round(tps * wbytes / (PEAK_GBS * 1e9), 4),

@@ -287,14 +287,16 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   hipStream_t st;
   Scratch* scr;
   if ((rc = ctx_verify_view(c, &row0, &rows, &st, &scr))) return rc;
-  // scratch: draft logits [k][V] | tokens [k] | stats [k+1] | slice candidates | masses | top-k | total
+  // scratch: draft logits [k][V] | tokens [k] | stats [k+1] | slice candidates | masses | top-k | total |
+  // per-slice statistics [k+1][nsl]
   const int nsl = spec_slices(vocab);
   const size_t off_tok = greedy ? 0 : (size_t)k * V * 4, off_st = off_tok + 256 * ((k * 4 + 255) / 256);
   const size_t off_cand = off_st + 256 * (((size_t)(k + 1) * sizeof(SpecRowStats) + 255) / 256);
   const size_t off_mass = off_cand + (size_t)nsl * kSpecMaxK * sizeof(SpecCand);
   const size_t off_top = off_mass + 256 * ((nsl * 4 + 255) / 256);
   const size_t off_tot = off_top + kSpecMaxK * sizeof(SpecCand);
-  if ((rc = scr->reserve(off_tot + 256))) return rc;
+  const size_t off_part = off_tot + 256;
+  if ((rc = scr->reserve(off_part + (size_t)(k + 1) * nsl * sizeof(SpecPart)))) return rc;
   char* base = static_cast<char*>(scr->ptr);
   float* dl_dev = greedy ? nullptr : reinterpret_cast<float*>(base);
   uint32_t* tok_dev = reinterpret_cast<uint32_t*>(base + off_tok);
@@ -303,10 +305,15 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   float* mass_dev = reinterpret_cast<float*>(base + off_mass);
   SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
   float* tot_dev = reinterpret_cast<float*>(base + off_tot);
+  SpecPart* part_dev = reinterpret_cast<SpecPart*>(base + off_part);
   if (!greedy) DZ_HIP_CHECK(hipMemcpyAsync(dl_dev, draft_logits, (size_t)k * V * 4, hipMemcpyHostToDevice, st));
   DZ_HIP_CHECK(hipMemcpyAsync(tok_dev, draft, (size_t)k * 4, hipMemcpyHostToDevice, st));
-  hipLaunchKernelGGL(spec_stats_kernel, dim3((unsigned)(k + 1)), dim3(1024), 0, st, row0, rows, (const float*)dl_dev, k,
-                     vocab, (const uint32_t*)tok_dev, st_dev);
+  // per-row statistics over the vocabulary in nsl slices per row, then one merge per row
+  hipLaunchKernelGGL(spec_stats_part_kernel, dim3((unsigned)(k + 1), (unsigned)nsl), dim3(256), 0, st, row0, rows,
+                     (const float*)dl_dev, k, vocab, part_dev);
+  DZ_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(spec_stats_merge_kernel, dim3((unsigned)(k + 1)), dim3(64), 0, st, row0, rows,
+                     (const float*)dl_dev, k, vocab, nsl, (const SpecPart*)part_dev, (const uint32_t*)tok_dev, st_dev);
   DZ_HIP_CHECK(hipGetLastError());
   std::vector<SpecRowStats> stats((size_t)k + 1);
   DZ_HIP_CHECK(hipMemcpyAsync(stats.data(), st_dev, stats.size() * sizeof(SpecRowStats), hipMemcpyDeviceToHost, st));

@@ -63,21 +63,35 @@ __device__ __forceinline__ float block_total(float s, float* sv) {
   return t;
 }
 
-// Grid n, 1024 threads.  Row r's target logits: row0 for r = 0, rows + (r-1)·V after; its draft logits
-// drafts + r·V for r < nd (none for greedy or past the drafts: statistics of the target only);
-// tok[r] is draft token r (r < nd).
-__global__ __launch_bounds__(1024) void spec_stats_kernel(const float* __restrict__ row0, const float* __restrict__ rows,
-                                                          const float* __restrict__ drafts, int nd, int V,
-                                                          const uint32_t* __restrict__ tok, SpecRowStats* out) {
-  constexpr int NT = 1024;
+constexpr int kSpecSlice = 4096;  // elements per slice of a row (a workgroup's share)
+constexpr int kSpecMaxK = 64;
+__host__ __device__ inline int spec_slices(int V) { return (V + kSpecSlice - 1) / kSpecSlice; }
+
+// Per-slice softmax statistics of one row: maxima (the target's first maximum) and sums of
+// exp(x - slice max), merged per row by spec_stats_merge_kernel.
+struct SpecPart {
+  float tmax, tsum, dmax, dsum;
+  int targ;
+  int pad[3];
+};
+
+// Grid (n rows, spec_slices(V) slices), 256 threads.  Row r's target logits: row0 for r = 0,
+// rows + (r-1)·V after; its draft logits drafts + r·V for r < nd (none for greedy or past the
+// drafts: statistics of the target only).
+__global__ __launch_bounds__(256) void spec_stats_part_kernel(const float* __restrict__ row0,
+                                                              const float* __restrict__ rows,
+                                                              const float* __restrict__ drafts, int nd, int V,
+                                                              SpecPart* __restrict__ part) {
+  constexpr int NT = 256;
   __shared__ float sv[NT / 64];
   __shared__ int si[NT / 64];
-  const int r = blockIdx.x;
+  const int r = blockIdx.x, sl = blockIdx.y;
   const float* t = r == 0 ? row0 : rows + (size_t)(r - 1) * V;
   const float* d = drafts && r < nd ? drafts + (size_t)r * V : nullptr;
+  const int i0 = sl * kSpecSlice, i1 = min(V, i0 + kSpecSlice);
   float tm = -INFINITY, dm = -INFINITY;
   int ti = 0x7FFFFFFF;
-  for (int i = threadIdx.x; i < V; i += NT) {
+  for (int i = i0 + (int)threadIdx.x; i < i1; i += NT) {
     const float x = t[i];
     if (cand_ahead(x, i, tm, ti)) {
       tm = x;
@@ -86,26 +100,78 @@ __global__ __launch_bounds__(1024) void spec_stats_kernel(const float* __restric
     if (d) dm = fmaxf(dm, d[i]);
   }
   block_best<NT>(tm, ti, sv, si);
-  float dmv = dm;
   int dummy = 0;
-  block_best<NT>(dmv, dummy, sv, si);
+  block_best<NT>(dm, dummy, sv, si);
   float ts = 0.f, ds = 0.f;
-  for (int i = threadIdx.x; i < V; i += NT) {
+  for (int i = i0 + (int)threadIdx.x; i < i1; i += NT) {
     ts += expf(t[i] - tm);
-    if (d) ds += expf(d[i] - dmv);
+    if (d) ds += expf(d[i] - dm);
   }
   ts = block_total<NT>(ts, sv);
   ds = block_total<NT>(ds, sv);
   if (threadIdx.x == 0) {
-    SpecRowStats s;
+    SpecPart q;
+    q.tmax = tm;
+    q.tsum = ts;
+    q.dmax = dm;
+    q.dsum = ds;
+    q.targ = ti;
+    q.pad[0] = q.pad[1] = q.pad[2] = 0;
+    part[(size_t)r * gridDim.y + sl] = q;
+  }
+}
+
+// Grid n rows, 64 threads: the row's statistics from its slices (sums rescaled to the row maximum),
+// then p = softmax(target)[tok[r]] and q = softmax(draft)[tok[r]] for r < nd (draft token r).
+__global__ __launch_bounds__(64) void spec_stats_merge_kernel(const float* __restrict__ row0,
+                                                              const float* __restrict__ rows,
+                                                              const float* __restrict__ drafts, int nd, int V,
+                                                              int nsl, const SpecPart* __restrict__ part,
+                                                              const uint32_t* __restrict__ tok,
+                                                              SpecRowStats* __restrict__ out) {
+  const int r = blockIdx.x;
+  const unsigned lane = threadIdx.x;
+  const SpecPart* pr = part + (size_t)r * nsl;
+  const bool has_d = drafts && r < nd;
+  float tm = -INFINITY, dm = -INFINITY;
+  int ti = 0x7FFFFFFF;
+  for (int s = (int)lane; s < nsl; s += 64) {
+    if (cand_ahead(pr[s].tmax, pr[s].targ, tm, ti)) {
+      tm = pr[s].tmax;
+      ti = pr[s].targ;
+    }
+    dm = fmaxf(dm, pr[s].dmax);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(tm, o);
+    const int j = __shfl_xor(ti, o);
+    if (cand_ahead(w, j, tm, ti)) {
+      tm = w;
+      ti = j;
+    }
+    dm = fmaxf(dm, __shfl_xor(dm, o));
+  }
+  float ts = 0.f, ds = 0.f;
+  for (int s = (int)lane; s < nsl; s += 64) {
+    ts += pr[s].tsum * expf(pr[s].tmax - tm);
+    if (has_d) ds += pr[s].dsum * expf(pr[s].dmax - dm);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    ts += __shfl_xor(ts, o);
+    ds += __shfl_xor(ds, o);
+  }
+  if (lane == 0) {
+    const float* t = r == 0 ? row0 : rows + (size_t)(r - 1) * V;
+    const float* d = has_d ? drafts + (size_t)r * V : nullptr;
     const int k = r < nd ? (int)tok[r] : 0;
+    SpecRowStats s;
     s.tmax = tm;
     s.tsum = ts;
-    s.dmax = dmv;
-    s.dsum = ds;
+    s.dmax = d ? dm : -INFINITY;
+    s.dsum = d ? ds : 0.f;
     const float tsn = ts > 0.f ? ts : 1.f, dsn = ds > 0.f ? ds : 1.f;
     s.p = expf(t[k] - tm) / tsn;
-    s.q = d ? expf(d[k] - dmv) / dsn : 0.f;
+    s.q = d ? expf(d[k] - dm) / dsn : 0.f;
     s.argmax = ti;
     s.pad = 0;
     out[r] = s;
@@ -119,10 +185,6 @@ __device__ __forceinline__ float spec_value(const float* t, const float* d, int 
   const float p = expf(t[i] - s.tmax) * (1.0f / s.tsum), q = expf(d[i] - s.dmax) * (1.0f / s.dsum);
   return fmaxf(p - q, 0.0f);
 }
-
-constexpr int kSpecSlice = 4096;  // elements per slice of a top-k pass (held in LDS)
-constexpr int kSpecMaxK = 64;
-__host__ __device__ inline int spec_slices(int V) { return (V + kSpecSlice - 1) / kSpecSlice; }
 
 // Stage 1: grid spec_slices(V), 256 threads.  Slice s of the row (kSpecSlice elements, in LDS) keeps
 // its K best (value, index) in order and, in mode 1, its residual mass.

@@ -316,7 +316,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs the decode loop on a single GPU "
-              "(multi-GPU sharding is design-only, see DESIGN.md); use --gpus 1", file=sys.stderr)
+              "(this build has no multi-GPU path); use --gpus 1", file=sys.stderr)
         return 2
 
     import daiza_amd as dz

@@ -306,33 +306,43 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
   }
   const float* kb = kcache + (size_t)kvh * max_ctx * HD + 4 * lane;
   const float* vb = vcache + (size_t)kvh * max_ctx * HD + 4 * lane;
-  int p = pbeg + (int)wave;
-  float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka;
-  if (p < ctx) {
-    ka = *reinterpret_cast<const float4*>(kb + (size_t)p * HD);
-    va = *reinterpret_cast<const float4*>(vb + (size_t)p * HD);
-  }
-  for (; p < ctx; p += 4) {
-    const float4 k4 = ka, v4 = va;
-    if (p + 4 < ctx) {
-      ka = *reinterpret_cast<const float4*>(kb + (size_t)(p + 4) * HD);
-      va = *reinterpret_cast<const float4*>(vb + (size_t)(p + 4) * HD);
-    }
+  // Each wave keeps its next KD positions (every 4th of the chunk) in flight.  Every slot is loaded
+  // unconditionally -- a position past the chunk reads the chunk's first row, never used -- so that
+  // no slot value becomes a phi (the register copies resolving one wait for the loads).
+  constexpr int KD = 4;
+  auto ld = [&](int pp, float4& k4, float4& v4) {
+    const int pc = pp < ctx ? pp : pbeg;
+    k4 = *reinterpret_cast<const float4*>(kb + (size_t)pc * HD);
+    v4 = *reinterpret_cast<const float4*>(vb + (size_t)pc * HD);
+  };
+  const int p = pbeg + (int)wave;
+  float4 kq[KD], vq[KD];
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      float dp = q4[gi].x * k4.x;
-      dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
-      dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
-      dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
-      const float score = wave_sum(dp);
-      const float mn = fmaxf(m[gi], score);
-      const float al = expf(m[gi] - mn), be = expf(score - mn);
-      l[gi] = l[gi] * al + be;
-      o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
-      o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
-      o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
-      o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
-      m[gi] = mn;
+  for (int d = 0; d < KD; ++d) ld(p + 4 * d, kq[d], vq[d]);
+  for (int base = p; base < ctx; base += 4 * KD) {
+#pragma unroll
+    for (int d = 0; d < KD; ++d) {
+      const int pp = base + 4 * d;
+      if (pp < ctx) {
+        const float4 k4 = kq[d], v4 = vq[d];
+#pragma unroll
+        for (int gi = 0; gi < GRP; ++gi) {
+          float dp = q4[gi].x * k4.x;
+          dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
+          dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
+          dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
+          const float score = wave_sum(dp);
+          const float mn = fmaxf(m[gi], score);
+          const float al = expf(m[gi] - mn), be = expf(score - mn);
+          l[gi] = l[gi] * al + be;
+          o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
+          o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
+          o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
+          o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
+          m[gi] = mn;
+        }
+      }
+      ld(pp + 4 * KD, kq[d], vq[d]);
     }
   }
 #pragma unroll

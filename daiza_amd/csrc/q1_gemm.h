@@ -30,8 +30,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup (wide form)
 constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup of the wide form, the padding of n
 constexpr int kGemmRowPad = 2 * kTileCols + 16;  // LDS bytes per staged token row (16 B pad: no bank conflicts)
-// hi and lo tiles of NB token blocks
-__host__ __device__ constexpr size_t gemm_shmem(int nb) { return (size_t)2 * 16 * nb * kGemmRowPad; }
+// hi and lo tiles of NB token blocks (two buffers of them for NB = 1)
+__host__ __device__ constexpr size_t gemm_shmem(int nb) { return (size_t)(nb == 1 ? 2 : 1) * 2 * 16 * nb * kGemmRowPad; }
 constexpr size_t kGemmShmem = gemm_shmem(kGemmNB);
 
 // Activations packed for the matrix cores.
@@ -176,35 +176,62 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = t_begin; t < t_end; ++t) {
-    // this wave's unit: per 16-row block sb, the chunk c = sb ^ q of row 16·sb + r and its scale slot c
-    u32x4 cv[4];
-    unsigned cs[4];
-    if (live) {
-      const uint8_t* unit = W + ((size_t)rb * ntiles + t) * kUnitBytes;
+  // Tile t's operands are requested one tile ahead: the wave's unit (four 16-byte chunks and their
+  // scale slots) into registers, the activations (hi and lo rows of the TOK tokens) into registers
+  // that are written to the other of two LDS buffers after the current tile's products (one buffer
+  // when NB > 1: two would not fit beside a second workgroup).  A tile past the range reloads the
+  // last one (never used), so that no loaded value becomes a phi.
+  constexpr int NBUF = NB == 1 ? 2 : 1;
+  constexpr int XV = 2 * TOK * 64 / 256;  // 16-byte activation chunks per thread and tile
+  auto load_unit = [&](int t, u32x4 (&cv)[4], unsigned (&cs)[4]) {
+    const int tc = t < t_end ? t : t_end - 1;
+    const uint8_t* unit = W + ((size_t)(live ? rb : 0) * ntiles + tc) * kUnitBytes;
 #pragma unroll
-      for (int sb = 0; sb < 4; ++sb) {
-        const unsigned L = 16u * sb + r, c = (unsigned)sb ^ q;
-        cv[sb] = *reinterpret_cast<const u32x4*>(unit + ((size_t)c * 64 + L) * 16);
-        const unsigned short* scp = reinterpret_cast<const unsigned short*>(unit + kUnitSignBytes + (size_t)L * 8);
-        cs[sb] = scp[c];
-      }
+    for (int sb = 0; sb < 4; ++sb) {
+      const unsigned L = 16u * sb + r, c = (unsigned)sb ^ q;
+      cv[sb] = *reinterpret_cast<const u32x4*>(unit + ((size_t)c * 64 + L) * 16);
+      const unsigned short* scp = reinterpret_cast<const unsigned short*>(unit + kUnitSignBytes + (size_t)L * 8);
+      cs[sb] = scp[c];
     }
-    __syncthreads();  // the previous tile's LDS reads are done
-    // stage the activations of tile t: [hi | lo][token][512 f16], rows padded to kGemmRowPad
-    for (int i = (int)tid; i < 2 * TOK * 64; i += 256) {
+  };
+  auto load_x = [&](int t, u32x4 (&xv)[XV]) {
+    const int tc = t < t_end ? t : t_end - 1;
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = (int)tid + 256 * j;
       const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
-      const uint16_t* src = (part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp + (size_t)t * kTileCols + 8 * c;
-      *reinterpret_cast<u32x4*>(smem + ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) =
-          *reinterpret_cast<const u32x4*>(src);
+      xv[j] = *reinterpret_cast<const u32x4*>((part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp +
+                                              (size_t)tc * kTileCols + 8 * c);
     }
-    __syncthreads();
+  };
+  auto put_x = [&](int b, const u32x4 (&xv)[XV]) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int i = (int)tid + 256 * j;
+      const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
+      *reinterpret_cast<u32x4*>(smem + (size_t)b * (2 * TOK * kGemmRowPad) +
+                                ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
+    }
+  };
+  u32x4 cv[4];
+  unsigned cs[4];
+  u32x4 xv[XV];
+  load_unit(t_begin, cv, cs);
+  load_x(t_begin, xv);
+  put_x(0, xv);
+  __syncthreads();
+  for (int t = t_begin; t < t_end; ++t) {
+    const int b = NBUF == 2 ? (t - t_begin) & 1 : 0;
+    u32x4 cvn[4];
+    unsigned csn[4];
+    load_unit(t + 1, cvn, csn);
+    if (NBUF == 2) load_x(t + 1, xv);
     if (live) {
       unsigned wn[4][4], s2[4];
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
       // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
-      const unsigned char* bh = smem + (size_t)r * kGemmRowPad + 256u * q;
+      const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)r * kGemmRowPad + 256u * q;
       const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
 #define DZ_GEMM_STEP(S)                                                                               \
   {                                                                                                   \
@@ -226,6 +253,19 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       DZ_GEMM_STEP(8) DZ_GEMM_STEP(9) DZ_GEMM_STEP(10) DZ_GEMM_STEP(11)
       DZ_GEMM_STEP(12) DZ_GEMM_STEP(13) DZ_GEMM_STEP(14) DZ_GEMM_STEP(15)
 #undef DZ_GEMM_STEP
+    }
+    if (NBUF == 2) {
+      put_x(b ^ 1, xv);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
+    } else {
+      __syncthreads();  // every wave is done with this tile's activations
+      load_x(t + 1, xv);
+      put_x(0, xv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      cv[sb] = cvn[sb];
+      cs[sb] = csn[sb];
     }
   }
   if (!live) return;

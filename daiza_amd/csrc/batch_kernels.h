@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void bt_attn_prep_kernel(const float* __restri
 
 // Causal GQA attention of token t (position pos0 + t) over cache positions [0, pos0 + t] for the
 // GRP q-heads of kv-head kvh (online softmax, attention.rs:149-199), then o·sigmoid(gate)
-// (attention.rs:202-203) -> ao[t][h·256 ..].  The 4 waves take positions p ≡ wave (mod 4) with
+// (attention.rs:202-203) -> ao[t][h·256 ..].  The 4 waves take blocks of 64 positions in turn with
 // their own running (m, l, o) and are merged at the end.  Grid (n, nkv, nch), 256 threads: with
 // nch > 1 workgroup z takes positions [z·csz, (z+1)·csz) and writes its record (m, l, o[256])
 // per q-head to rec[t][h][z] for bt_attn_merge_kernel instead.
@@ -288,62 +288,83 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
                                                       const float* __restrict__ vcache, int max_ctx, int nq,
                                                       int pos0, float* __restrict__ ao, int csz,
                                                       float* __restrict__ rec) {
-  constexpr int HD = 256;
+  constexpr int HD = 256, BP = 64;
+  __shared__ float qs[GRP][HD];
+  __shared__ float ps[4][GRP][BP];
   __shared__ float wm[4][GRP], wl[4][GRP];
   __shared__ float wo[4][GRP][HD];
   const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, nch = gridDim.z;
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const int ctx = nch > 1 ? min(pos0 + t + 1, (z + 1) * csz) : pos0 + t + 1;
   const int pbeg = nch > 1 ? z * csz : 0;
+  for (int i = (int)tid; i < GRP * HD; i += 256) qs[i / HD][i % HD] = qb[((size_t)t * nq + kvh * GRP) * HD + i];
+  __syncthreads();
+  const float* kb = kcache + (size_t)kvh * max_ctx * HD;
+  const float* vb = vcache + (size_t)kvh * max_ctx * HD;
   float m[GRP], l[GRP];
-  float4 o[GRP], q4[GRP];
+  float4 o[GRP];
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {
     m[gi] = -INFINITY;
     l[gi] = 0.f;
     o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
-    q4[gi] = *reinterpret_cast<const float4*>(qb + ((size_t)t * nq + kvh * GRP + gi) * HD + 4 * lane);
   }
-  const float* kb = kcache + (size_t)kvh * max_ctx * HD + 4 * lane;
-  const float* vb = vcache + (size_t)kvh * max_ctx * HD + 4 * lane;
-  // Each wave keeps its next KD positions (every 4th of the chunk) in flight.  Every slot is loaded
-  // unconditionally -- a position past the chunk reads the chunk's first row, never used -- so that
-  // no slot value becomes a phi (the register copies resolving one wait for the loads).
-  constexpr int KD = 4;
-  auto ld = [&](int pp, float4& k4, float4& v4) {
-    const int pc = pp < ctx ? pp : pbeg;
-    k4 = *reinterpret_cast<const float4*>(kb + (size_t)pc * HD);
-    v4 = *reinterpret_cast<const float4*>(vb + (size_t)pc * HD);
-  };
-  const int p = pbeg + (int)wave;
-  float4 kq[KD], vq[KD];
+  // Blocks of 64 positions, wave w taking blocks w, w+4, ...  Scores: lane = position, each lane
+  // walks its key row against the queries in LDS (a broadcast read), so a score costs 256 FMAs in
+  // one lane instead of a 64-lane reduction per (position, head).  Values: lane = 4 dims, walking the
+  // block's positions with their probabilities from LDS.
+  for (int b0 = pbeg + (int)wave * BP; b0 < ctx; b0 += 4 * BP) {
+    const int pp = b0 + (int)lane;
+    const bool valid = pp < ctx;
+    const float* kr = kb + (size_t)(valid ? pp : b0) * HD;
+    float sc[GRP];
 #pragma unroll
-  for (int d = 0; d < KD; ++d) ld(p + 4 * d, kq[d], vq[d]);
-  for (int base = p; base < ctx; base += 4 * KD) {
+    for (int gi = 0; gi < GRP; ++gi) sc[gi] = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < HD / 4; ++j) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * j);
 #pragma unroll
-    for (int d = 0; d < KD; ++d) {
-      const int pp = base + 4 * d;
-      if (pp < ctx) {
-        const float4 k4 = kq[d], v4 = vq[d];
-#pragma unroll
-        for (int gi = 0; gi < GRP; ++gi) {
-          float dp = q4[gi].x * k4.x;
-          dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
-          dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
-          dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
-          const float score = wave_sum(dp);
-          const float mn = fmaxf(m[gi], score);
-          const float al = expf(m[gi] - mn), be = expf(score - mn);
-          l[gi] = l[gi] * al + be;
-          o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
-          o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
-          o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
-          o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
-          m[gi] = mn;
-        }
+      for (int gi = 0; gi < GRP; ++gi) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[gi][4 * j]);
+        float d = sc[gi];
+        d = __builtin_fmaf(q4.x, k4.x, d);
+        d = __builtin_fmaf(q4.y, k4.y, d);
+        d = __builtin_fmaf(q4.z, k4.z, d);
+        sc[gi] = __builtin_fmaf(q4.w, k4.w, d);
       }
-      ld(pp + 4 * KD, kq[d], vq[d]);
     }
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      const float x = valid ? sc[gi] : -INFINITY;
+      const float mn = fmaxf(m[gi], wave_max(x));
+      const float al = expf(m[gi] - mn);
+      const float pr = valid ? expf(x - mn) : 0.f;
+      l[gi] = l[gi] * al + wave_sum(pr);
+      o[gi].x *= al;
+      o[gi].y *= al;
+      o[gi].z *= al;
+      o[gi].w *= al;
+      m[gi] = mn;
+      ps[wave][gi][lane] = pr;
+    }
+    // the other lanes' probabilities of this wave (LDS accesses of one wave complete in order)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    const int np = min(BP, ctx - b0);
+#pragma unroll 8
+    for (int pi = 0; pi < np; ++pi) {
+      const float4 v4 = *reinterpret_cast<const float4*>(vb + (size_t)(b0 + pi) * HD + 4 * lane);
+#pragma unroll
+      for (int gi = 0; gi < GRP; ++gi) {
+        const float pr = ps[wave][gi][pi];
+        o[gi].x = __builtin_fmaf(pr, v4.x, o[gi].x);
+        o[gi].y = __builtin_fmaf(pr, v4.y, o[gi].y);
+        o[gi].z = __builtin_fmaf(pr, v4.z, o[gi].z);
+        o[gi].w = __builtin_fmaf(pr, v4.w, o[gi].w);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();  // this block's reads of ps before the next block's writes
   }
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {

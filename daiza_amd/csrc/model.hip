@@ -1182,10 +1182,13 @@ static hipError_t launch_bt_attn(int grp, dim3 g, hipStream_t s, const float* qb
 
 // Position chunks of the chunk's attention: enough workgroups to fill the device when the chunk
 // has few tokens (speculative verify at long context), one chunk for a long prefill.
+// A chunk of several positions is a whole number of 256-position rounds (the kernel's 4 waves take
+// 64 each) where that keeps about the wanted number of chunks.
 static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
   int nch = (1024 + n * nkv - 1) / (n * nkv);
   nch = std::max(1, std::min(nch, std::max(1, ctx_max / 64)));
   *csz = (ctx_max + nch - 1) / nch;
+  if (nch > 1 && *csz > 256) *csz = (*csz + 128) / 256 * 256;
   return (ctx_max + *csz - 1) / *csz;
 }
 

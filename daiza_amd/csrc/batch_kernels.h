@@ -287,13 +287,29 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
                                                       const float* __restrict__ kcache,
                                                       const float* __restrict__ vcache, int max_ctx, int nq,
                                                       int pos0, float* __restrict__ ao, int csz,
-                                                      float* __restrict__ rec) {
+                                                      float* __restrict__ rec, int n_xcd, int nkv_x, int nch_x) {
   constexpr int HD = 256, BP = 64;
   __shared__ float qs[GRP][HD];
   __shared__ float ps[4][GRP][BP];
   __shared__ float wm[4][GRP], wl[4][GRP];
   __shared__ float wo[4][GRP][HD];
-  const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, nch = gridDim.z;
+  int t, kvh, z, nch;
+  if (n_xcd > 0) {
+    // 1-D grid: workgroup L runs on XCD L % 8 (round-robin dispatch); the n tokens of one
+    // (kv-head, chunk) pair get indices with the same residue, so the chunk's cache rows are fetched
+    // into one XCD's L2 and read there n times, instead of once per XCD
+    const int L = (int)blockIdx.x, u = L >> 3, pair = (u / n_xcd) * 8 + (L & 7);
+    if (pair >= nkv_x * nch_x) return;
+    t = u % n_xcd;
+    kvh = pair % nkv_x;
+    z = pair / nkv_x;
+    nch = nch_x;
+  } else {
+    t = (int)blockIdx.x;
+    kvh = (int)blockIdx.y;
+    z = (int)blockIdx.z;
+    nch = (int)gridDim.z;
+  }
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const int ctx = nch > 1 ? min(pos0 + t + 1, (z + 1) * csz) : pos0 + t + 1;
   const int pbeg = nch > 1 ? z * csz : 0;

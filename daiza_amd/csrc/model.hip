@@ -1167,17 +1167,27 @@ static hipError_t launch(K kfn, dim3 g, dim3 b, hipStream_t s, Args... args) {
   return hipGetLastError();
 }
 
-static hipError_t launch_bt_attn(int grp, dim3 g, hipStream_t s, const float* qb, const float* gate, const float* kc,
-                                 const float* vc, int max_ctx, int nq, int pos0, float* ao, int csz, float* rec) {
+// Grid (n, nkv, nch); with at least 8 (kv-head, chunk) pairs, a 1-D grid that keeps each pair's
+// tokens on one XCD (bt_attn_kernel).
+static hipError_t launch_bt_attn(int grp, int n, int nkv, int nch, hipStream_t s, const float* qb, const float* gate,
+                                 const float* kc, const float* vc, int max_ctx, int nq, int pos0, float* ao, int csz,
+                                 float* rec) {
+  const int pairs = nkv * nch;
+  const bool xcd = nch > 1 && pairs >= 8;
+  const dim3 g = xcd ? dim3((unsigned)(8 * ((pairs + 7) / 8) * n)) : dim3((unsigned)n, (unsigned)nkv, (unsigned)nch);
+  const int nx = xcd ? n : 0;
+#define DZ_ATTN(G_) \
+  launch(bt_attn_kernel<G_>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec, nx, nkv, nch)
   switch (grp) {
-    case 1: return launch(bt_attn_kernel<1>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
-    case 2: return launch(bt_attn_kernel<2>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
-    case 3: return launch(bt_attn_kernel<3>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
-    case 4: return launch(bt_attn_kernel<4>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
-    case 6: return launch(bt_attn_kernel<6>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
-    case 8: return launch(bt_attn_kernel<8>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec);
+    case 1: return DZ_ATTN(1);
+    case 2: return DZ_ATTN(2);
+    case 3: return DZ_ATTN(3);
+    case 4: return DZ_ATTN(4);
+    case 6: return DZ_ATTN(6);
+    case 8: return DZ_ATTN(8);
     default: return hipErrorInvalidValue;
   }
+#undef DZ_ATTN
 }
 
 // Position chunks of the chunk's attention: enough workgroups to fill the device when the chunk
@@ -1271,8 +1281,8 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
         if ((rc = x->bt.arec.reserve((size_t)n * c.n_head * nch * (2 + c.head_dim) * sizeof(float)))) return rc;
         rec = static_cast<float*>(x->bt.arec.ptr);
       }
-      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, dim3(nb, (unsigned)c.n_head_kv, (unsigned)nch), s, x->bt.qb,
-                                  x->bt.gate, kc, vc, (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy, csz, rec));
+      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, n, (int)c.n_head_kv, nch, s, x->bt.qb, x->bt.gate, kc, vc,
+                                  (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy, csz, rec));
       if (nch > 1)
         DZ_HIP_CHECK(launch(bt_attn_merge_kernel, dim3(nb, (unsigned)c.n_head), dim3(256), s, (const float*)rec, nch,
                             (const float*)x->bt.gate, (int)c.n_head, x->bt.gy));

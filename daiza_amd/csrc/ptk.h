@@ -122,7 +122,7 @@ struct PtkLayer {
   const float* dt_bias;
   const float* ssm_norm;
   float* conv;                 // ring [4][qkvd]
-  float* state;                // [nvh][128 j][128 i]
+  float* state;                // [nvh][128 i][128 j] (row-major S[i][j])
   const int* ring_base;
   const float* q_norm;
   const float* k_norm;

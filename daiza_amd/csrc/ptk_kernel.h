@@ -614,7 +614,7 @@ __device__ __forceinline__ bool phase_merge(const PtkPlan& P, int w, unsigned ti
 // ------------------------------------------------------------------ phase B: Gated DeltaNet step
 
 // State rows of a compute thread in the DeltaNet phase: waves 4..7 hold rows quarter*32 + (wave-4)*8
-// + (lane >> 3), columns (lane & 7)*16 .. +16 of the v-head's 128x128 state S[j][i].
+// + (lane >> 3), columns (lane & 7)*16 .. +16 of the v-head's 128x128 state S[i][j].
 __device__ __forceinline__ void dn_state_load(const PtkPlan& P, const PtkLayer& Ly, int w, unsigned tid,
                                               float (&s)[16]) {
   // every thread loads: a thread without rows reads 16 distinct words of one cache line, so that no

@@ -1205,6 +1205,12 @@ static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
 // y[n][W.rows] (=|+=) W · (optionally RMS-normalised) x[n][W.cols].
 static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int n, const float* norm_w, float* y,
                    int64_t ldy, int accumulate) {
+  if (!norm_w && n <= 16) {
+    // no RMSNorm and few tokens (verify): the product packs its tiles itself, which saves the packing
+    // launch; with many tokens every row-block group would repeat the packing of the same tiles
+    DZ_HIP_CHECK(launch_q1_gemm_raw(W, xin, ldx, n, y, ldy, accumulate, x->s, &x->bt.split));
+    return DZ_OK;
+  }
   PackedX p;
   int rc = packed_x_reserve(x->bt.pack, n, W.cols, &p);
   if (rc) return rc;

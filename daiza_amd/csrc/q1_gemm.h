@@ -40,6 +40,9 @@ struct GemmX {
   const uint16_t* xl;  // [Np][Kp] f16 bits of x/sig - hi
   const float* sig;    // [Np] power-of-two scale of each token
   int64_t Kp;          // columns padded to the tile (ntiles * 512)
+  // raw form (q1_gemm_kernel<NB, true>): x[n][K] f32 with row stride ldx, packed per tile in LDS
+  const float* xf;
+  int64_t ldx, K;
 };
 
 // The power of two that brings max|x| into [2^13, 2^14) (1 for an all-zero or non-finite row).
@@ -155,13 +158,20 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
 // Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
 // partial to y + z·zstride; an unsplit product (gridDim.z = 1) writes
 // y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xl)[n][k] for n < n_tok, row < rows.
-template <int NB>
+//
+// Raw form (RAW): the workgroup reads x[n][K] as f32 and packs each tile itself, with a power of two
+// sig(n, t) per token and tile (max |x| of the tile's 512 columns in [2^13, 2^14), as pack_sig); a
+// tile's products are scaled by it as they are added: y = Σ_t sig(n, t) · W_t (hi + lo)(n, t).
+// That skips the separate packing pass for inputs that need no RMSNorm.
+template <int NB, bool RAW = false>
 __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
                                                          int ntiles, int tps, const GemmX x, int n_tok,
                                                          float* __restrict__ y, int64_t ldy, int64_t zstride,
                                                          int accumulate) {
   constexpr int TOK = 16 * NB;
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float tile_max[TOK][2];   // raw form: per token, max |x| of each half tile
+  __shared__ float tile_sig[2][TOK];   // raw form: sig(n, t) of each activation buffer
   const unsigned tid = threadIdx.x, lane = tid & 63u;
   const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6);
   const bool live = rb < nrb;
@@ -194,23 +204,61 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       cs[sb] = scp[c];
     }
   };
+  // Raw form: chunk j of a thread is float4 column c = tid & 127 of token (tid >> 7) + 2j (the TOK
+  // tokens' 128 float4 per tile, XV = TOK / 2 of them per thread); wave w covers half (w & 1) of the
+  // columns of its tokens.
   auto load_x = [&](int t, u32x4 (&xv)[XV]) {
     const int tc = t < t_end ? t : t_end - 1;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
-      const int i = (int)tid + 256 * j;
-      const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
-      xv[j] = *reinterpret_cast<const u32x4*>((part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp +
-                                              (size_t)tc * kTileCols + 8 * c);
+      if constexpr (RAW) {
+        const int n = tok0 + (int)(tid >> 7) + 2 * j;
+        const int64_t col = (int64_t)tc * kTileCols + 4 * (tid & 127u);
+        xv[j] = n < n_tok && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
+                                       : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        const int i = (int)tid + 256 * j;
+        const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
+        xv[j] = *reinterpret_cast<const u32x4*>((part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp +
+                                                (size_t)tc * kTileCols + 8 * c);
+      }
     }
   };
   auto put_x = [&](int b, const u32x4 (&xv)[XV]) {
+    if constexpr (RAW) {
+      const unsigned half = (tid >> 6) & 1u;
 #pragma unroll
-    for (int j = 0; j < XV; ++j) {
-      const int i = (int)tid + 256 * j;
-      const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
-      *reinterpret_cast<u32x4*>(smem + (size_t)b * (2 * TOK * kGemmRowPad) +
-                                ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
+      for (int j = 0; j < XV; ++j) {
+        const float4 v = __builtin_bit_cast(float4, xv[j]);
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) tile_max[(tid >> 7) + 2 * j][half] = m;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < XV; ++j) {
+        const int n = (int)(tid >> 7) + 2 * j;
+        const float sg = pack_sig(fmaxf(tile_max[n][0], tile_max[n][1]));
+        const float rs = 1.0f / sg;  // exact: a power of two
+        const float4 v = __builtin_bit_cast(float4, xv[j]);
+        ushort4 h, l;
+        pack_split(v.x * rs, h.x, l.x);
+        pack_split(v.y * rs, h.y, l.y);
+        pack_split(v.z * rs, h.z, l.z);
+        pack_split(v.w * rs, h.w, l.w);
+        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad + 8 * (tid & 127u);
+        *reinterpret_cast<ushort4*>(row) = h;
+        *reinterpret_cast<ushort4*>(row + (size_t)TOK * kGemmRowPad) = l;
+        if ((tid & 127u) == 0) tile_sig[b][n] = sg;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < XV; ++j) {
+        const int i = (int)tid + 256 * j;
+        const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
+        *reinterpret_cast<u32x4*>(smem + (size_t)b * (2 * TOK * kGemmRowPad) +
+                                  ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
+      }
     }
   };
   u32x4 cv[4];
@@ -230,6 +278,11 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       unsigned wn[4][4], s2[4];
 #pragma unroll
       for (int sb = 0; sb < 4; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
+      f32x4 at[4][NB];  // raw form: this tile's products, scaled by sig(n, t) after the tile
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
       // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
       const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)r * kGemmRowPad + 256u * q;
       const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
@@ -243,8 +296,8 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
     _Pragma("unroll") for (int sb = 0; sb < 4; ++sb) {                                                \
       const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
       _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                             \
-        acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], acc[sb][nb], 0, 0, 0);       \
-        acc[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl_[nb], acc[sb][nb], 0, 0, 0);       \
+        at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], at[sb][nb], 0, 0, 0);         \
+        at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl_[nb], at[sb][nb], 0, 0, 0);         \
       }                                                                                               \
     }                                                                                                 \
   }
@@ -253,6 +306,19 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       DZ_GEMM_STEP(8) DZ_GEMM_STEP(9) DZ_GEMM_STEP(10) DZ_GEMM_STEP(11)
       DZ_GEMM_STEP(12) DZ_GEMM_STEP(13) DZ_GEMM_STEP(14) DZ_GEMM_STEP(15)
 #undef DZ_GEMM_STEP
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const float sg = RAW ? tile_sig[b][16 * nb + (int)r] : 1.0f;
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+          if constexpr (RAW) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[sb][nb][v] = __builtin_fmaf(sg, at[sb][nb][v], acc[sb][nb][v]);
+          } else {
+            acc[sb][nb] = at[sb][nb];
+          }
+        }
+      }
     }
     if (NBUF == 2) {
       put_x(b ^ 1, xv);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
@@ -274,7 +340,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   for (int nb = 0; nb < NB; ++nb) {
     const int n = tok0 + 16 * nb + (int)r;
     if (n >= n_tok) continue;
-    const float sg = x.sig[n];
+    const float sg = RAW ? 1.0f : x.sig[n];
     float* yr = y + (size_t)n * ldy;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {

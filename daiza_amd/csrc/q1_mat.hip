@@ -281,20 +281,36 @@ int gemm_splits(const Q1Dev& W, int n, int* tps) {
   return (nt + *tps - 1) / *tps;
 }
 
-hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
-                          hipStream_t s, Scratch* split) {
+// One product launch: the packed form (p non-null) or the raw form (x f32, row stride ldx).
+static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const float* xr, int64_t ldx, int n, float* y,
+                                     int64_t ldy, int accumulate, hipStream_t s, Scratch* split) {
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_shmem(kGemmNB));
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(q1_gemm_kernel<1>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_shmem(1));
-    if (e != hipSuccess) return e;
+    const void* ks[4] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
+                         reinterpret_cast<const void*>(q1_gemm_kernel<1, false>),
+                         reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, true>),
+                         reinterpret_cast<const void*>(q1_gemm_kernel<1, true>)};
+    const size_t sh[4] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(kGemmNB), gemm_shmem(1)};
+    for (int i = 0; i < 4; ++i) {
+      hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh[i]);
+      if (e != hipSuccess) return e;
+    }
     attr = true;
   }
-  if (W.ntiles * kTileCols != p.Kp || n > p.Np) return hipErrorInvalidValue;
-  GemmX gx{p.xh, p.xl, p.sig, p.Kp};
+  const bool raw = p == nullptr;
+  if (!raw && (W.ntiles * kTileCols != p->Kp || n > p->Np)) return hipErrorInvalidValue;
+  GemmX gx{};
+  if (raw) {
+    gx.Kp = W.ntiles * kTileCols;
+    gx.xf = xr;
+    gx.ldx = ldx;
+    gx.K = W.cols;
+  } else {
+    gx.xh = p->xh;
+    gx.xl = p->xl;
+    gx.sig = p->sig;
+    gx.Kp = p->Kp;
+  }
   int tps;
   int S = gemm_splits(W, n, &tps);
   if (S > 1 && !split) S = 1, tps = (int)W.ntiles;
@@ -307,19 +323,38 @@ hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int
     ld = W.rows;
   }
   const unsigned gx_ = (unsigned)((W.nrb + 3) / 4);
+  const dim3 g1(gx_, 1, (unsigned)S), g2(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S);
   if (n <= 16) {
-    hipLaunchKernelGGL(q1_gemm_kernel<1>, dim3(gx_, 1, (unsigned)S), dim3(256), gemm_shmem(1), s, W.data, W.rows,
-                       W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+    if (raw)
+      hipLaunchKernelGGL((q1_gemm_kernel<1, true>), g1, dim3(256), gemm_shmem(1), s, W.data, W.rows, W.nrb,
+                         (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+    else
+      hipLaunchKernelGGL((q1_gemm_kernel<1, false>), g1, dim3(256), gemm_shmem(1), s, W.data, W.rows, W.nrb,
+                         (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   } else {
-    hipLaunchKernelGGL(q1_gemm_kernel<kGemmNB>, dim3(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S),
-                       dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows, W.nrb, (int)W.ntiles, tps, gx, n, out, ld,
-                       zs, accumulate);
+    if (raw)
+      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, true>), g2, dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows,
+                         W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+    else
+      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, false>), g2, dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows,
+                         W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || S == 1) return e;
   hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((W.rows + 255) / 256), (unsigned)n), dim3(256), 0, s,
                      (const float*)out, S, zs, W.rows, n, y, ldy, accumulate);
   return hipGetLastError();
+}
+
+hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
+                          hipStream_t s, Scratch* split) {
+  return launch_q1_gemm_any(W, &p, nullptr, 0, n, y, ldy, accumulate, s, split);
+}
+
+hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,
+                              int accumulate, hipStream_t s, Scratch* split) {
+  if ((W.cols & 3) || (ldx & 3)) return hipErrorInvalidValue;  // 16-byte loads of x rows
+  return launch_q1_gemm_any(W, nullptr, x, ldx, n, y, ldy, accumulate, s, split);
 }
 
 // ------------------------------------------------------------------ matrix API state
@@ -498,8 +533,12 @@ int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumul
   float* yd = static_cast<float*>(g_y.ptr);
   DZ_HIP_CHECK(hipMemcpyAsync(xd, x, (size_t)n * K * 4, hipMemcpyHostToDevice, s));
   if (accumulate) DZ_HIP_CHECK(hipMemcpyAsync(yd, y, (size_t)n * R * 4, hipMemcpyHostToDevice, s));
-  DZ_HIP_CHECK(launch_x_pack(xd, (int64_t)K, (int64_t)K, n, nullptr, 0.f, p, s));
-  DZ_HIP_CHECK(launch_q1_gemm(m->d, p, n, yd, (int64_t)R, accumulate, s, &g_split));
+  if (n <= 16) {  // few tokens: the product packs its tiles itself (as the batched forward does)
+    DZ_HIP_CHECK(launch_q1_gemm_raw(m->d, xd, (int64_t)K, n, yd, (int64_t)R, accumulate, s, &g_split));
+  } else {
+    DZ_HIP_CHECK(launch_x_pack(xd, (int64_t)K, (int64_t)K, n, nullptr, 0.f, p, s));
+    DZ_HIP_CHECK(launch_q1_gemm(m->d, p, n, yd, (int64_t)R, accumulate, s, &g_split));
+  }
   DZ_HIP_CHECK(hipMemcpyAsync(y, yd, (size_t)n * R * 4, hipMemcpyDeviceToHost, s));
   DZ_HIP_CHECK(hipStreamSynchronize(s));
   return DZ_OK;

@@ -77,6 +77,10 @@ hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const fl
 // demand; NULL keeps it unsplit) and sums them in order.
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
                           hipStream_t s, Scratch* split);
+// The same product on f32 x[n][W.cols] (row stride ldx, both multiples of 4), each K tile packed in
+// LDS with its own power-of-two scale per token: no separate packing pass (inputs without RMSNorm).
+hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,
+                              int accumulate, hipStream_t s, Scratch* split);
 
 }  // namespace dz
 

@@ -5,6 +5,8 @@ Bar: every column within 1e-3 normwise relative error of the reference quad kern
 (quant.rs:614-740) applied to that column, and in practice ~1e-6: the weights are exact f16
 operands and the activations carry ~22 significant bits, so only the f32 accumulation order
 differs.  Closed forms pin the sign convention and the scale handling independently of the oracle.
+Cases with n <= 16 run the raw form (each K tile packed in LDS with its own scale per token), the
+others the packed form (one scale per token, packed by a separate pass).
 """
 import numpy as np
 import pytest
@@ -123,3 +125,19 @@ def test_wide_dynamic_range(dz, oracle):
     for i in range(4):
         ref = oracle.matvec(aos, rows, cols, x[i])
         assert normwise_rel(y[i], ref) < 1e-5, i
+
+
+def test_tiles_of_different_magnitude(dz, oracle):
+    # within one token, K tiles 2^20 apart: the raw form scales each tile on its own (n <= 16), the
+    # packed form (n = 17) scales the row; both stay within the bar of the reference
+    rows, cols = 128, 2048
+    aos = oracle.synth_q1_0(SEED, K_GATE, 6, rows, cols)
+    m = dz.Q1_0Matrix(aos, rows, cols)
+    for n in (2, 17):
+        x = _xs(oracle, n, cols, layer=7)
+        x[:, :512] *= 1024.0
+        x[:, 1536:] *= 1.0 / 1024.0
+        y = m.matvec_batch(x)
+        for i in range(n):
+            ref = oracle.matvec(aos, rows, cols, x[i])
+            assert normwise_rel(y[i], ref) < 1e-5, (n, i)

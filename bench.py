@@ -192,7 +192,7 @@ def bench_verify(dz, H, ctx, cfg, decode_ms_per_tok, reps=8):
         "accepted_total": acc,
         "prefill_to_ctx_s": round(fill_s, 2),
         "note": "sequential_verify_ms = k forwards of one token on this build's decode path, the reference's "
-                "verify loop (engine.rs:1255-1470); spec_verify_step_ms adds the draft logits' upload, the device-side row statistics and top-k, and the host draws",
+                "verify loop (engine.rs:1255-1470); spec_verify_step_ms adds the device-side row statistics and top-k and the host draws (the draft logits' upload overlaps the forward on a side stream)",
     }
 
 

@@ -1366,6 +1366,16 @@ static int bt_verify_commit(dz_ctx* x, int a) {
 
 // Device logits of a pending verify for the sampler (spec.hip): row 0 = the context's logits (they
 // predict draft 0), rows = the verify forward's per-position rows; its stream and scratch memory.
+// Largest chunk of one n-token forward (activations ~0.3 MB per token at the 27B shape).
+constexpr int kBatchChunk = 1024;
+
+int ctx_verify_enqueue(dz_ctx* x, const uint32_t* draft, int k) {
+  if (!x || !draft) return set_error(DZ_ERR_MODEL, "null argument");
+  if (k < 1) return set_error(DZ_ERR_TENSOR, "verify: %d drafts", k);
+  if (k > kBatchChunk) return set_error(DZ_ERR_TENSOR, "verify: %d drafts (at most %d)", k, kBatchChunk);
+  return bt_verify_forward(x, draft, k);
+}
+
 int ctx_verify_view(dz_ctx* x, const float** row0, const float** rows, hipStream_t* s, Scratch** scratch) {
   if (x->bt.pending == 0) return set_error(DZ_ERR_TENSOR, "no pending verify forward");
   *row0 = x->logits;
@@ -1381,8 +1391,6 @@ static bool batch_wanted() {
   return !(e && e[0] == '0');
 }
 
-// Largest chunk of one n-token forward (activations ~0.3 MB per token at the 27B shape).
-constexpr int kBatchChunk = 1024;
 
 static int bt_prefill(dz_ctx* x, const uint32_t* ids, int n, float* last_logits, float* per_pos) {
   const size_t V = (size_t)x->m->cfg.vocab;
@@ -1554,10 +1562,7 @@ int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_token
 }
 
 int dz_verify_forward(dz_ctx* x, const uint32_t* draft, int k, float* per_pos_logits) {
-  if (!x || !draft) return set_error(DZ_ERR_MODEL, "null argument");
-  if (k < 1) return set_error(DZ_ERR_TENSOR, "verify: %d drafts", k);
-  if (k > kBatchChunk) return set_error(DZ_ERR_TENSOR, "verify: %d drafts (at most %d)", k, kBatchChunk);
-  int rc = bt_verify_forward(x, draft, k);
+  int rc = dz::ctx_verify_enqueue(x, draft, k);
   if (rc) return rc;
   // the context's stream is non-blocking: copy on it, then wait
   if (per_pos_logits)

@@ -86,6 +86,8 @@ hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n
 
 struct dz_ctx;
 namespace dz {
+// dz_verify_forward's checks and forward, enqueued on the context's stream without the final wait.
+int ctx_verify_enqueue(dz_ctx* x, const uint32_t* draft, int k);
 // The device rows of a context's pending verify forward (see dz_verify_forward), for the sampler.
 int ctx_verify_view(dz_ctx* x, const float** row0, const float** rows, hipStream_t* s, Scratch** scratch);
 }  // namespace dz

@@ -198,6 +198,18 @@ static int check_sampling(const dz_sampling* sp) {
   return DZ_OK;
 }
 
+// The stream that uploads draft logits beside a verify forward (default priority, non-blocking) and
+// the event that marks the upload's end, created once per process.
+static int upload_stream(hipStream_t* s, hipEvent_t* e) {
+  static hipStream_t side = nullptr;
+  static hipEvent_t done = nullptr;
+  if (!side) DZ_HIP_CHECK(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+  if (!done) DZ_HIP_CHECK(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+  *s = side;
+  *e = done;
+  return DZ_OK;
+}
+
 }  // namespace dz
 
 using namespace dz;
@@ -282,7 +294,9 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
     *bonus = eos ? 0xFFFFFFFFu : b;
     return DZ_OK;
   }
-  if ((rc = dz_verify_forward(c, draft, k, nullptr))) return rc;
+  // the forward is enqueued without a wait, so that the draft logits' upload (a side stream, joined by
+  // an event before the statistics) runs while it computes
+  if ((rc = ctx_verify_enqueue(c, draft, k))) return rc;
   const float *row0, *rows;
   hipStream_t st;
   Scratch* scr;
@@ -306,7 +320,14 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
   float* tot_dev = reinterpret_cast<float*>(base + off_tot);
   SpecPart* part_dev = reinterpret_cast<SpecPart*>(base + off_part);
-  if (!greedy) DZ_HIP_CHECK(hipMemcpyAsync(dl_dev, draft_logits, (size_t)k * V * 4, hipMemcpyHostToDevice, st));
+  if (!greedy) {
+    hipStream_t side;
+    hipEvent_t up;
+    if ((rc = upload_stream(&side, &up))) return rc;
+    DZ_HIP_CHECK(hipMemcpyAsync(dl_dev, draft_logits, (size_t)k * V * 4, hipMemcpyHostToDevice, side));
+    DZ_HIP_CHECK(hipEventRecord(up, side));
+    DZ_HIP_CHECK(hipStreamWaitEvent(st, up, 0));
+  }
   DZ_HIP_CHECK(hipMemcpyAsync(tok_dev, draft, (size_t)k * 4, hipMemcpyHostToDevice, st));
   // per-row statistics over the vocabulary in nsl slices per row, then one merge per row
   hipLaunchKernelGGL(spec_stats_part_kernel, dim3((unsigned)(k + 1), (unsigned)nsl), dim3(256), 0, st, row0, rows,

@@ -47,22 +47,25 @@ __global__ __launch_bounds__(256) void bt_embed_kernel(const int* __restrict__ i
 // Causal conv over the chunk + SiLU (ssm.rs:467-518): out[t][ch] = silu(Σ_tap x[t-3+tap][ch]·w[tap][ch]),
 // fma in tap order (oldest first), x[t'] = in-proj output of token t' for t' >= 0 and the conv
 // ring's entry for the earlier tokens (the token at chunk offset t' < 0 sits in slot
-// (head0 + t') & 3, head0 = slot of token 0).  Thread per (token, channel).
+// (head0 + t') & 3, head0 = slot of token 0).  Thread per (token, channel).  keep (verify, else null)
+// receives the conv inputs themselves, keep[t][ch] = x[t][ch], from which the commit rebuilds the ring.
 __global__ __launch_bounds__(256) void bt_conv_kernel(const float* __restrict__ yin, int64_t ldin, int n,
                                                       const float* __restrict__ ring, int head0,
                                                       const float* __restrict__ conv_w, int64_t qkvd,
-                                                      float* __restrict__ cout) {
+                                                      float* __restrict__ cout, float* __restrict__ keep) {
   const int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int t = blockIdx.y;
   if (ch >= qkvd || t >= n) return;
-  float o = 0.f;
+  float o = 0.f, xt = 0.f;
 #pragma unroll
   for (int tap = 0; tap < 4; ++tap) {
     const int tt = t - 3 + tap;
     const float xv = tt >= 0 ? yin[(size_t)tt * ldin + ch] : ring[(size_t)((head0 + tt) & 3) * qkvd + ch];
     o = __builtin_fmaf(xv, conv_w[(size_t)tap * qkvd + ch], o);
+    if (tap == 3) xt = xv;
   }
   cout[(size_t)t * qkvd + ch] = siluf_(o);
+  if (keep) keep[(size_t)t * qkvd + ch] = xt;
 }
 
 // Conv ring after tokens [0, t1) of a chunk: the inputs of tokens [t0, t1) (t0 = max(0, t1 - 4))

@@ -1251,13 +1251,13 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
       float* ring = x->conv + (size_t)si * 4 * qkvd;
       const int head0 = (x->ring_base[(size_t)si] + p0) & 3;
       const unsigned gch = (unsigned)((qkvd + 255) / 256);
+      // verify keeps the chunk's conv inputs (bt.rx) for the commit; a kept forward updates the ring now
       DZ_HIP_CHECK(launch(bt_conv_kernel, dim3(gch, nb), dim3(256), s, (const float*)x->bt.yin, ld_in, n,
-                          (const float*)ring, head0, (const float*)l.conv_w, qkvd, x->bt.cout));
+                          (const float*)ring, head0, (const float*)l.conv_w, qkvd, x->bt.cout,
+                          verify ? x->bt.rx[(size_t)si] : nullptr));
       DnRecord rec{nullptr, nullptr, nullptr};
       if (verify) {
         rec = x->bt.rec[(size_t)si];
-        DZ_HIP_CHECK(hipMemcpy2DAsync(x->bt.rx[(size_t)si], (size_t)qkvd * 4, x->bt.yin, (size_t)ld_in * 4,
-                                      (size_t)qkvd * 4, (size_t)n, hipMemcpyDeviceToDevice, s));
       } else {
         DZ_HIP_CHECK(launch(bt_ring_kernel, dim3(gch), dim3(256), s, (const float*)x->bt.yin, ld_in, std::max(0, n - 4),
                             n, ring, head0, qkvd));

@@ -453,4 +453,21 @@ __global__ __launch_bounds__(256) void bt_swiglu_kernel(const float* __restrict_
   s[(size_t)t * F + i] = siluf_(row[i]) * row[F + i];
 }
 
+// The same from the partials of a split gate/up product (part[z][t][2F], zstride apart): each sum in
+// split order, as gemm_split_reduce_kernel forms it, then silu(gate) · up.
+__global__ __launch_bounds__(256) void bt_split_swiglu_kernel(const float* __restrict__ part, int splits,
+                                                              int64_t zstride, int64_t F, int n,
+                                                              float* __restrict__ s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (i >= F || t >= n) return;
+  const size_t off = (size_t)t * 2 * F + i;
+  float g = part[off], u = part[off + F];
+  for (int z = 1; z < splits; ++z) {
+    g += part[(size_t)z * zstride + off];
+    u += part[(size_t)z * zstride + off + F];
+  }
+  s[(size_t)t * F + i] = siluf_(g) * u;
+}
+
 }  // namespace dz

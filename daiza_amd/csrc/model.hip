@@ -1204,7 +1204,7 @@ static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
 
 // y[n][W.rows] (=|+=) W · (optionally RMS-normalised) x[n][W.cols].
 static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int n, const float* norm_w, float* y,
-                   int64_t ldy, int accumulate) {
+                   int64_t ldy, int accumulate, GemmDefer* defer = nullptr) {
   if (!norm_w && n <= 16) {
     // no RMSNorm and few tokens (verify): the product packs its tiles itself, which saves the packing
     // launch; with many tokens every row-block group would repeat the packing of the same tiles
@@ -1215,7 +1215,7 @@ static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int
   int rc = packed_x_reserve(x->bt.pack, n, W.cols, &p);
   if (rc) return rc;
   DZ_HIP_CHECK(launch_x_pack(xin, ldx, W.cols, n, norm_w, x->m->cfg.rms_eps, p, x->s));
-  DZ_HIP_CHECK(launch_q1_gemm(W, p, n, y, ldy, accumulate, x->s, &x->bt.split));
+  DZ_HIP_CHECK(launch_q1_gemm(W, p, n, y, ldy, accumulate, x->s, &x->bt.split, defer));
   return DZ_OK;
 }
 
@@ -1295,9 +1295,15 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
       if ((rc = bt_gemm(x, l.out_proj, x->bt.gy, qd, n, nullptr, x->bt.h, H, 1))) return rc;
     }
     // MLP (mlp.rs:28-47): h += W_down (silu(W_gate n) * W_up n), n = rmsnorm(h, post_attention_norm)
-    if ((rc = bt_gemm(x, l.gate_up, x->bt.h, H, n, l.post_norm, x->bt.ygu, 2 * F, 0))) return rc;
-    DZ_HIP_CHECK(launch(bt_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s, (const float*)x->bt.ygu,
-                        F, n, x->bt.sw));
+    // a split gate/up product (few tokens) goes from its partials straight to the SwiGLU
+    GemmDefer gd;
+    if ((rc = bt_gemm(x, l.gate_up, x->bt.h, H, n, l.post_norm, x->bt.ygu, 2 * F, 0, &gd))) return rc;
+    if (gd.splits > 1)
+      DZ_HIP_CHECK(launch(bt_split_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s, gd.part,
+                          gd.splits, gd.zstride, F, n, x->bt.sw));
+    else
+      DZ_HIP_CHECK(launch(bt_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s,
+                          (const float*)x->bt.ygu, F, n, x->bt.sw));
     if ((rc = bt_gemm(x, l.down, x->bt.sw, F, n, nullptr, x->bt.h, H, 1))) return rc;
   }
   // output norm + lm_head for the last out_rows tokens

@@ -283,7 +283,8 @@ int gemm_splits(const Q1Dev& W, int n, int* tps) {
 
 // One product launch: the packed form (p non-null) or the raw form (x f32, row stride ldx).
 static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const float* xr, int64_t ldx, int n, float* y,
-                                     int64_t ldy, int accumulate, hipStream_t s, Scratch* split) {
+                                     int64_t ldy, int accumulate, hipStream_t s, Scratch* split,
+                                     GemmDefer* defer = nullptr) {
   static bool attr = false;
   if (!attr) {
     const void* ks[4] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
@@ -340,15 +341,16 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
                          W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || S == 1) return e;
+  if (defer) *defer = GemmDefer{out, S, zs};
+  if (e != hipSuccess || S == 1 || defer) return e;
   hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((W.rows + 255) / 256), (unsigned)n), dim3(256), 0, s,
                      (const float*)out, S, zs, W.rows, n, y, ldy, accumulate);
   return hipGetLastError();
 }
 
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
-                          hipStream_t s, Scratch* split) {
-  return launch_q1_gemm_any(W, &p, nullptr, 0, n, y, ldy, accumulate, s, split);
+                          hipStream_t s, Scratch* split, GemmDefer* defer) {
+  return launch_q1_gemm_any(W, &p, nullptr, 0, n, y, ldy, accumulate, s, split, defer);
 }
 
 hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,

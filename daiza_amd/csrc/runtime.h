@@ -74,9 +74,16 @@ hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const fl
                          hipStream_t s);
 // y[n][rows] (row stride ldy) =|+= p · Wᵀ; W.cols must match the packed K.  A product with too
 // few workgroups to fill the device splits its K tiles into partials held in `split` (grown on
-// demand; NULL keeps it unsplit) and sums them in order.
+// demand; NULL keeps it unsplit) and sums them in order.  With `defer` set, a split product leaves
+// the sum to the caller: defer receives the partials ([splits][n][W.rows], zstride apart) and
+// splits > 1; an unsplit one writes y as usual and reports splits = 1.
+struct GemmDefer {
+  const float* part = nullptr;
+  int splits = 1;
+  int64_t zstride = 0;
+};
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
-                          hipStream_t s, Scratch* split);
+                          hipStream_t s, Scratch* split, GemmDefer* defer = nullptr);
 // The same product on f32 x[n][W.cols] (row stride ldx, both multiples of 4), each K tile packed in
 // LDS with its own power-of-two scale per token: no separate packing pass (inputs without RMSNorm).
 hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,

@@ -8,12 +8,14 @@ untimed ones.  One step = one token through the whole stack (forward_single_toke
 Prints one JSON line.  `roofline` is the dominant kernel of the timed decode, the persistent token
 kernel (one cooperative launch runs all timed tokens), timed with HIP events on the context's
 stream: algorithmic bytes per launch (every token's Q1_0 weights, KV-cache reads and appends,
-DeltaNet state read and write, conv ring, embedding row, logits) over the launch's duration.
-`roofline_gemv` is the Q1_0 LUT GEMV alone at the config-1 shape (17408 x 5120, 32 distinct
-matrices, more than the 256 MB Infinity Cache), timed per launch.  `config5` times speculative
-verify (k = 8 drafts at context 8192) after a batched prefill to that context.
-`cpu_baseline` is the CPU oracle (oracle/, a C restatement of the reference's multithreaded AVX2
-path) on a bounded sample of the same workload.
+DeltaNet state read and write, conv ring, embedding row, logits) over the launch's duration; its
+`traffic` is the HBM bytes per token of a profiled launch (profiles/decode_config4_pmc.txt) times
+the timed launch's tokens.  `roofline_gemv` is a complete y = W x at the config-1 shape (17408 x
+5120, 32 distinct matrices, more than the 256 MB Infinity Cache), timed per call.  `layer_steps`
+times one mixer layer-step of configs 2 and 3 (at context 4096 and 32768).  `config5` times
+speculative verify (k = 8 drafts at context 8192) after a batched prefill to
+that context.  `cpu_baseline` is the CPU oracle (oracle/, a C restatement of the reference's
+multithreaded AVX2 path) decoding a bounded sample from the GPU context's post-prefill state.
 """
 import argparse
 import ctypes
@@ -120,15 +122,15 @@ def bench_copy(H, nbytes, reps=32):
     return {"bytes": nbytes, "us": us, "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
-def measured_traffic(name):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary under profiles/ (FETCH_SIZE
-    and WRITE_SIZE, each scaled by the same counter on a copy of known size), or None when that
-    summary is absent."""
+def measured_traffic(name, key="traffic_bytes_per_launch"):
+    """HBM bytes from a committed rocprofv3 --pmc summary under profiles/ (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the same counter on a copy of known size): the value of the line
+    `key:`, or None when the summary or the line is absent."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key + ":"):
             return int(float(line.split(":", 1)[1]))
     return None
 
@@ -197,10 +199,11 @@ def bench_verify(dz, H, ctx, cfg, decode_ms_per_tok, reps=8):
 
 
 def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
-    """HIP-event timing of the LUT GEMV (config-1 shape) over a timed region of nmat*reps
-    back-to-back launches on the library's stream, rotating nmat distinct matrices (more bytes
-    than the 256 MB Infinity Cache).  Per-launch time = region / launches; it includes each
-    launch's dispatch gap, so it reads a little above the profiler's kernel duration."""
+    """HIP-event timing of a complete y = W x at the config-1 shape (dz_q1_0_matvec_dev: the split-K
+    LUT GEMV and the tile sum that forms y) over a timed region of nmat*reps back-to-back calls on one
+    stream, rotating nmat distinct matrices (more bytes than the 256 MB Infinity Cache).  Per-call
+    time = region / calls; it includes the dispatch gaps, so it reads a little above the profiler's
+    kernel durations."""
     # config-1 distribution: Bernoulli(0.5) sign bits, scale = f16(|N(0,1)| * 0.02), x ~ N(0,1)
     rng = np.random.default_rng(SEED)
     blk = np.empty((rows, cols // 128, 18), np.uint8)
@@ -210,23 +213,27 @@ def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
     mats = [dz.Q1_0Matrix(aos, rows, cols) for _ in range(nmat)]
     x = rng.standard_normal(cols).astype(np.float32)
     L = dz.lib()
-    ld = L.dz_q1_0_partials_ld(mats[0]._h)
-    nt = L.dz_q1_0_ntiles(mats[0]._h)
     dx, dy = ctypes.c_void_p(), ctypes.c_void_p()
     H.hipMalloc(ctypes.byref(dx), cols * 4)
-    H.hipMalloc(ctypes.byref(dy), ld * nt * 4)
+    H.hipMalloc(ctypes.byref(dy), rows * 4)
     H.hipMemcpy(dx, x.ctypes.data, cols * 4, 1)
     s = ctypes.c_void_p()
     H.hipStreamCreate(ctypes.byref(s))
-    for m in mats:  # warm-up
-        assert L.dz_q1_0_gemv_partials(m._h, dx, dy, s) == 0
+    for m in mats:  # warm-up (also sizes the library's partial buffer)
+        assert L.dz_q1_0_matvec_dev(m._h, dx, dy, 0, s) == 0
     H.hipStreamSynchronize(s)
+    # the result of the timed path against the oracle (one matrix, same x)
+    import oracle
+    y = np.empty(rows, np.float32)
+    H.hipMemcpy(y.ctypes.data, dy, rows * 4, 2)
+    yo = oracle.matvec(aos, rows, cols, x)
+    rel = float(np.max(np.abs(y - yo)) / np.max(np.abs(yo)))
     n = nmat * reps
     ev = Events(H, 2)
     g = Gate(H, s)
     H.hipEventRecord(ev.ev[0], s)
     for i in range(n):
-        L.dz_q1_0_gemv_partials(mats[i % nmat]._h, dx, dy, s)
+        L.dz_q1_0_matvec_dev(mats[i % nmat]._h, dx, dy, 0, s)
     H.hipEventRecord(ev.ev[1], s)
     H.hipEventSynchronize(ev.ev[1])
     g.free()
@@ -239,22 +246,111 @@ def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
     H.hipFree(dx)
     H.hipFree(dy)
     return {"avg_launch_us": avg_us, "launches": n, "algo_bytes": algo,
-            "achieved_gbs": algo / (avg_us * 1e-6) / 1e9}
+            "achieved_gbs": algo / (avg_us * 1e-6) / 1e9, "max_rel_err_vs_oracle": rel}
 
 
-def cpu_baseline(cfg_cls, budget_s=20.0):
-    """Oracle (C restatement of the reference AVX2 path) decode on the host cores."""
+def layer_step_bytes(cfg, kind, ctx_len=0):
+    """Algorithmic HBM bytes of one mixer layer-step (BASELINE configs 2 and 3): the Q1_0 weights of
+    the in- and out-projections, plus for a DeltaNet layer the recurrent state read and written and
+    the conv ring (3 history rows read, 1 written) with its weights, for an attention layer the K/V
+    rows read over the context (the new position included) and the K/V append."""
+    blk = lambda r, c: r * (c // 128) * 18
+    H, hd = cfg.hidden, cfg.ssm_state
+    if kind == "deltanet":
+        inner, qkvd = cfg.ssm_v_heads * hd, cfg.qkv_dim
+        w = blk(qkvd + inner + 2 * cfg.ssm_v_heads, H) + blk(H, inner)
+        return w + 2 * cfg.ssm_v_heads * hd * hd * 4 + 4 * qkvd * 4 + 4 * qkvd * 4
+    qd, kvd = cfg.n_head * cfg.head_dim, cfg.n_head_kv * cfg.head_dim
+    w = blk(2 * qd + 2 * kvd, H) + blk(H, qd)
+    return w + 2 * kvd * 4 * (ctx_len + 1) + 2 * kvd * 4
+
+
+def bench_layers(dz, H, steps=40):
+    """BASELINE configs 2 and 3 as isolated layer-steps: dz_ctx_mixer_step_dev (one mixer of one
+    layer, h += mixer(rmsnorm(h)), weights, state and h resident in HBM) timed with HIP events on the
+    context's stream over `steps` back-to-back steps.  Config 2: a 27B-shape Gated DeltaNet layer
+    with N(0, 0.02) state and N(0, 0.1) conv history; config 3: a 27B-shape attention layer over an
+    N(0,1) cache at context 4096 and 32768."""
+    out = {}
+    for name, L in (("config2_deltanet", 0), ("config3_attention_ctx4096", 4096),
+                    ("config3_attention_ctx32768", 32768)):
+        attn = L > 0
+        cfg = dz.Config.bonsai27b(max_ctx=L + steps + 8)
+        cfg.n_layers, cfg.vocab, cfg.full_attn_interval = 1, 1024, 1 if attn else 4
+        model = dz.Model.synthetic(cfg, SEED + 2)
+        ctx = dz.Context(model)
+        rng = np.random.default_rng(L + 1)
+        if attn:
+            k = rng.standard_normal((cfg.n_head_kv, L, cfg.head_dim), dtype=np.float32)
+            ctx.set_kv(0, k, k)
+            del k
+            ctx.set_pos(L)
+        else:
+            st = (rng.standard_normal((cfg.ssm_v_heads, cfg.ssm_state, cfg.ssm_state)) * 0.02).astype(np.float32)
+            conv = (rng.standard_normal((4, cfg.qkv_dim)) * 0.1).astype(np.float32)
+            ctx.set_ssm_state(0, st, conv, 0)
+        h = rng.standard_normal(cfg.hidden).astype(np.float32)
+        dh = ctypes.c_void_p()
+        H.hipMalloc(ctypes.byref(dh), cfg.hidden * 4)
+        H.hipMemcpy(dh, h.ctypes.data, cfg.hidden * 4, 1)
+        Lb = dz.lib()
+        stream = ctypes.c_void_p(ctx.stream())
+        for _ in range(3):  # warm-up
+            assert Lb.dz_ctx_mixer_step_dev(ctx._h, 0, dh, dh) == 0
+        H.hipStreamSynchronize(stream)
+        p0 = ctx.pos
+        ev = Events(H, 2)
+        g = Gate(H, stream, n=4)
+        H.hipEventRecord(ev.ev[0], stream)
+        for _ in range(steps):
+            Lb.dz_ctx_mixer_step_dev(ctx._h, 0, dh, dh)
+        H.hipEventRecord(ev.ev[1], stream)
+        H.hipEventSynchronize(ev.ev[1])
+        g.free()
+        us = 1e3 * ev.elapsed_ms(0, 1) / steps
+        ev.destroy()
+        kind = "attention" if attn else "deltanet"
+        algo = sum(layer_step_bytes(cfg, kind, p0 + i) for i in range(steps)) / steps
+        out[name] = {"us_per_step": round(us, 2), "algo_bytes_per_step": int(algo),
+                     "achieved_gbs": round(algo / (us * 1e-6) / 1e9, 1),
+                     "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_GBS, 4),
+                     "context": p0 if attn else None}
+        log("%s: %.2f us per layer-step, %.1f GB/s" % (name, us, out[name]["achieved_gbs"]))
+        H.hipFree(dh)
+        ctx.close()
+        model.close()
+    return out
+
+
+def snapshot_state(ctx, cfg):
+    """Host copies of every layer's state of a context (DeltaNet state, conv ring and head; K/V of
+    the cached positions), for the CPU baseline to start from the GPU's prefill."""
+    snap = {"pos": ctx.pos, "ssm": {}, "kv": {}}
+    for l in range(cfg.n_layers):
+        if (l + 1) % cfg.full_attn_interval:
+            snap["ssm"][l] = ctx.get_ssm_state(l)
+        else:
+            snap["kv"][l] = ctx.get_kv(l, ctx.pos)
+    return snap
+
+
+def cpu_baseline(cfg_cls, snap, first, budget_s=20.0):
+    """Oracle (C restatement of the reference AVX2 path: quad LUT kernel, work-stealing 128-row
+    chunks) greedy decode on the host cores, from the GPU context's state after the same
+    1024-token prefill (copied in: the oracle's own token-by-token prefill would take minutes)."""
     import oracle
     # the GPU box grants 16 host CPUs per GPU
     threads = min(os.cpu_count() or 1, int(os.environ.get("DZ_CPU_THREADS", 16)))
-    cfg = cfg_cls.bonsai27b(max_ctx=256)
+    cfg = cfg_cls.bonsai27b(max_ctx=snap["pos"] + 80)
     t0 = time.time()
     om = oracle.Model(cfg, SEED, nthreads=threads)
     gen_s = time.time() - t0
-    rng = np.random.default_rng(1)
-    ids = rng.integers(0, cfg.vocab, 8)
-    for t in ids:  # short prefill (sequential single-token forwards)
-        tok, _ = om.forward(int(t), want_logits=False)
+    om.set_pos(snap["pos"])
+    for l, (st, conv, head) in snap["ssm"].items():
+        om.set_ssm_state(l, st, conv, head)
+    for l, (k, v) in snap["kv"].items():
+        om.set_kv(l, k, v)
+    tok = first
     n = 0
     t0 = time.time()
     while True:
@@ -273,18 +369,16 @@ def cpu_baseline(cfg_cls, budget_s=20.0):
     except OSError:
         pass
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "oracle greedy decode of %d tokens after an 8-token prefill, full 27B shape, %d threads on "
-                      "%s (%d logical CPUs visible; model generation %.1f s excluded)"
-                      % (n, threads, model, os.cpu_count() or 0, gen_s)}
-
-
-_KEEP = []  # objects of --only trace, alive until interpreter exit
+            "sample": "oracle greedy decode of %d tokens at context %d-%d (the GPU context's state after the same "
+                      "%d-token prefill, copied in), full 27B shape, %d threads on %s (%d logical CPUs visible; "
+                      "model generation %.1f s excluded)"
+                      % (n, snap["pos"], snap["pos"] + n, snap["pos"], threads, model, os.cpu_count() or 0, gen_s)}
 
 
 def trace_decode(dz, args):
     """--only trace: the prefill and one decode launch through library calls alone, timed by the host
-    clock, for rocprofv3 passes (the profiler loses its output when this script's own HIP objects
-    exist, or when the context is freed under it, so both are left to process exit)."""
+    clock, for rocprofv3 passes.  Everything is closed before return; with --maps the process's
+    memory map is written first (to symbolize an exit-time stack)."""
     cfg = dz.Config.bonsai27b(max_ctx=args.prefill + args.warmup + args.steps + 8)
     model = dz.Model.synthetic(cfg, SEED)
     ctx = dz.Context(model)
@@ -297,7 +391,11 @@ def trace_decode(dz, args):
     ctx.decode_greedy(int(toks[-1]), args.steps)
     dt = time.perf_counter() - t0
     print("[trace] decode %d tokens in one launch: %.2f tok/s (host clock)" % (args.steps, args.steps / dt), flush=True)
-    return model, ctx
+    if args.maps:
+        with open("/proc/self/maps") as f, open(args.maps, "w") as o:
+            o.write(f.read())
+    ctx.close()
+    model.close()
 
 
 def main():
@@ -308,9 +406,11 @@ def main():
     ap.add_argument("--prefill", type=int, default=PREFILL)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "verify", "trace"], default="all",
+    ap.add_argument("--maps", default="", help="--only trace: write /proc/self/maps to this file")
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "verify", "layers", "trace"], default="all",
                     help="gemv: only the config-1 GEMV and the copy reference; decode: only the prefill, the "
-                         "timed decode and a 256 MiB copy reference; verify: only the config-5 verify; trace: the "
+                         "timed decode and a 256 MiB copy reference; verify: only the config-5 verify; layers: "
+                         "only the config-2/3 layer-steps; trace: the "
                          "prefill and decode through library calls alone, timed by the host clock (for "
                          "rocprofv3 passes, which lose their output when the script's own HIP objects exist)")
     args = ap.parse_args()
@@ -321,12 +421,15 @@ def main():
 
     import daiza_amd as dz
     if args.only == "trace":
-        _KEEP.extend(trace_decode(dz, args))
+        trace_decode(dz, args)
         return 0
     H = hip()
     L = dz.lib()
     if L.dz_device_init(0) != 0:
         raise SystemExit("dz_device_init: " + L.dz_last_error().decode())
+    if args.only == "layers":
+        bench_layers(dz, H)
+        return 0
     if args.only == "gemv":
         g = bench_gemv(dz, H)
         cp = bench_copy(H, g["algo_bytes"])
@@ -361,6 +464,7 @@ def main():
     prefill_s = time.time() - t0
     log("prefill %d tokens in %.2f s" % (args.prefill, prefill_s))
     first = int(np.argmax(last))
+    snap = None if args.no_cpu or args.only != "all" else snapshot_state(ctx, cfg)
 
     stream = ctypes.c_void_p(ctx.stream())
     ev = Events(H, 2)
@@ -383,7 +487,9 @@ def main():
     pos_timed = args.prefill + args.warmup
     algo = decode_bytes(cfg, wbytes, pos_timed, args.steps)
     ptk_gbs = algo / (ms * 1e-3) / 1e9
-    ptk_traffic = measured_traffic("decode_config4_pmc.txt")
+    # HBM bytes of the timed launch: the profiled launch's bytes per token times this launch's tokens
+    per_tok = measured_traffic("decode_config4_pmc.txt", "traffic_bytes_per_token")
+    ptk_traffic = per_tok * args.steps if per_tok else None
     if args.only == "decode":
         cp = bench_copy(H, 256 << 20, reps=4)
         log("token kernel: %.1f GB/s algorithmic over %.1f ms (%d B per launch); copy of %d B: %.1f GB/s"
@@ -398,6 +504,9 @@ def main():
     v = bench_verify(dz, H, ctx, cfg, ms / args.steps)
     log("config 5: verify forward %.2f ms, spec step %.2f ms (sequential %.2f ms) at context %d"
         % (v["verify_forward_ms"], v["spec_verify_step_ms"], v["sequential_verify_ms"], v["context"]))
+    ctx.close()
+    model.close()
+    layers = bench_layers(dz, H)
     out = {
         "metric": METRIC,
         "value": round(tps, 2),
@@ -439,25 +548,25 @@ def main():
             "copy_ceiling_gbs": round(cp["gbs"], 1),
         },
         "roofline_gemv": {
-            "kernel": "gemv_lut_kernel (Q1_0 LUT GEMV, config 1 17408x5120, split-K partials)",
+            "kernel": "dz_q1_0_matvec_dev (Q1_0 LUT GEMV, config 1 17408x5120: complete y = W x)",
             "bound": "hbm",
             "achieved": round(g["achieved_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["achieved_gbs"] / PEAK_GBS, 4),
-            "traffic": measured_traffic("gemv_config1_pmc.txt"),
+            "traffic": measured_traffic("gemv_config1_pmc.txt", "traffic_bytes_per_call"),
             "avg_launch_us": round(g["avg_launch_us"], 3),
+            "max_rel_err_vs_oracle": g["max_rel_err_vs_oracle"],
             "launches_timed": g["launches"],
             "algo_bytes_per_launch": g["algo_bytes"],
         },
         "config5": v,
+        "layer_steps": layers,
         "cpu_baseline": None,
     }
-    ctx.close()
-    model.close()
     if not args.no_cpu:
         log("cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(dz.Config, args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline(dz.Config, snap, first, args.cpu_budget)
     print(json.dumps(out))
     return 0
 

@@ -123,6 +123,8 @@ _MODEL_PROTOS = {
     "dz_forward_token": ([_vp, ctypes.c_uint32, _f32p, _u32p], ctypes.c_int),
     "dz_forward_batch": ([_vp, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p], ctypes.c_int),
     "dz_decode_greedy": ([_vp, ctypes.c_uint32, ctypes.c_int, _u32p], ctypes.c_int),
+    "dz_decode_greedy_eos": ([_vp, ctypes.c_uint32, ctypes.c_int, ctypes.c_int32, _u32p, ctypes.POINTER(ctypes.c_int)],
+                             ctypes.c_int),
     "dz_ctx_logits": ([_vp, _f32p], ctypes.c_int),
     "dz_ctx_set_ssm_state": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.c_int], ctypes.c_int),
     "dz_ctx_get_ssm_state": ([_vp, ctypes.c_int, _f32p, _f32p, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
@@ -132,6 +134,7 @@ _MODEL_PROTOS = {
     "dz_kv_truncate": ([_vp, ctypes.c_int], ctypes.c_int),
     "dz_ctx_set_pos": ([_vp, ctypes.c_int], ctypes.c_int),
     "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
+    "dz_ctx_mixer_step_dev": ([_vp, ctypes.c_int, _vp, _vp], ctypes.c_int),
     "dz_ctx_stream": ([_vp], _vp),
     "dz_ctx_token_kernel": ([_vp], ctypes.c_int),
     "dz_ctx_vocab": ([_vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
@@ -244,6 +247,14 @@ class Q1_0Matrix:
         return out
 
 
+class Tensor(ctypes.Structure):
+    """dz_tensor: one GGUF-named host tensor (type 0 = F32, 1 = F16, 41 = Q1_0)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("data", _vp), ("n_bytes", ctypes.c_size_t)]
+
+
+GGUF_F32, GGUF_F16, GGUF_Q1_0 = 0, 1, 41
+
+
 class Model:
     """Device-resident weights (LoadedWeights, weights.rs:1308-1379)."""
 
@@ -253,8 +264,21 @@ class Model:
         if tensors is None:
             _check(lib().dz_model_create_synth(ctypes.byref(cfg), int(seed), ctypes.byref(h)))
         else:
-            raise DaizaError(DZ_ERR_UNSUPPORTED, "named-tensor loading is exposed through the C ABI only")
+            # tensors: {GGUF name: (type, array)}; the arrays are borrowed for the call only
+            keep = []
+            arr = (Tensor * len(tensors))()
+            for i, (name, (ty, a)) in enumerate(tensors.items()):
+                a = np.ascontiguousarray(a)
+                keep.append(a)
+                arr[i] = Tensor(name.encode(), int(ty), a.ctypes.data, a.nbytes)
+            _check(lib().dz_model_create(ctypes.byref(cfg), arr, len(tensors), ctypes.byref(h)))
+            del keep
         self._h = h
+
+    @classmethod
+    def from_tensors(cls, cfg, tensors):
+        """Weights from GGUF-named host tensors (LoadedWeights::load_all, weights.rs:1308-1379)."""
+        return cls(cfg, tensors=tensors)
 
     @classmethod
     def synthetic(cls, cfg, seed):
@@ -398,9 +422,23 @@ class Context:
         return per if per_pos_logits else last
 
     def decode_greedy(self, first_token, n):
+        """n greedy forwards on the device; the pick after each (engine.rs:850-871 without the EOS stop)."""
         out = np.empty(n, np.uint32)
         _check(lib().dz_decode_greedy(self._h, int(first_token), int(n), out.ctypes.data_as(_u32p)))
         return out
+
+    def decode_greedy_eos(self, first_token, n, eos_id):
+        """The greedy loop with its EOS stop (engine.rs:850-871): picks after each forward run; the last
+        is eos_id when the loop stopped on it (that token is not forwarded)."""
+        out = np.empty(max(n, 1), np.uint32)
+        done = ctypes.c_int()
+        _check(lib().dz_decode_greedy_eos(self._h, int(first_token), int(n), int(eos_id), out.ctypes.data_as(_u32p),
+                                          ctypes.byref(done)))
+        return out[:done.value].copy()
+
+    def kv_truncate(self, n):
+        """KvCache::truncate (kv_cache.rs:119-130): keeps n cached positions, pos = n; conv rings stay."""
+        _check(lib().dz_kv_truncate(self._h, int(n)))
 
     def logits(self):
         out = np.empty(self.cfg.vocab, np.float32)

@@ -72,6 +72,10 @@ struct dz_ctx {
   int* ring_base_dev = nullptr;
   int gmax = 64;
   int pos_host = 0;            // mirror of TokState::pos_next
+  // Set when a token-kernel launch gave up on a bounded wait: the launch may have stored part of a
+  // token's state (DeltaNet rows, KV, conv rows) without the position moving, so every forward is
+  // refused until dz_ctx_reset (or a full-state restore) makes the state consistent again.
+  bool poisoned = false;
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   // persistent token kernel (used by forward_token / forward_batch / decode_greedy when enabled)
@@ -719,6 +723,7 @@ static int ctx_zero_state(dz_ctx* x) {
   DZ_HIP_CHECK(hipMemcpyAsync(x->st, &st, sizeof st, hipMemcpyHostToDevice, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
   x->pos_host = 0;
+  x->poisoned = false;
   return DZ_OK;
 }
 
@@ -778,6 +783,27 @@ static int ctx_peek_argmax(dz_ctx* x) {
   sa.commit = 0;
   hipLaunchKernelGGL(select_token_kernel, dim3(1), dim3(1024), 0, x->s, sa);
   DZ_HIP_CHECK(hipGetLastError());
+  return DZ_OK;
+}
+
+static int ctx_set_pos_dev(dz_ctx* x, int pos);
+
+// Moves the position to pos while every DeltaNet layer's conv-ring head stays where it is: heads are
+// stored relative to the position ((ring_base + pos) & 3), so each base is rebased by the move.
+// SsmState::conv_head (cache/ssm_state.rs:10-39) is independent of the KV length, and neither
+// KvCache::truncate (kv_cache.rs:119-130) nor a position change touches it.
+static int ctx_move_pos(dz_ctx* x, int pos) {
+  const int old = x->pos_host;
+  for (size_t i = 0; i < x->ring_base.size(); ++i) x->ring_base[i] = ((x->ring_base[i] + old - pos) % 4 + 4) % 4;
+  if (!x->ring_base.empty())
+    DZ_HIP_CHECK(hipMemcpy(x->ring_base_dev, x->ring_base.data(), x->ring_base.size() * 4, hipMemcpyHostToDevice));
+  return ctx_set_pos_dev(x, pos);
+}
+
+// Refuses work on a context whose last token-kernel launch gave up part-way.
+static int ctx_usable(const dz_ctx* x) {
+  if (x->poisoned)
+    return set_error(DZ_ERR_DEVICE, "context state is inconsistent after a failed launch: call dz_ctx_reset");
   return DZ_OK;
 }
 
@@ -1007,7 +1033,9 @@ static int ptk_prepare(dz_ctx* x) {
 // ids (already in x->feed), the rest the greedy pick.  toklog[pos + i] receives token i and
 // toklog[pos + n] the greedy pick after the last one; logits of the last token land in x->logits,
 // and with per_pos every token's logits in ptk.logits_all[i] (n <= ptk.chunk).
-static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0) {
+// With eos >= 0 a greedy pick equal to eos ends the launch before that token is forwarded; *n_done
+// (if given) receives the number of tokens forwarded and the position advances by that many.
+static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0, int eos = -1, int* n_done = nullptr) {
   const PtkPlan& P = x->ptk.plan;
   if (x->pos_host + n > x->m->cfg.max_ctx)
     return set_error(DZ_ERR_TENSOR, "context full: pos %d + %d > max_ctx %d", x->pos_host, n, x->m->cfg.max_ctx);
@@ -1027,8 +1055,15 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0)
   r.pos0 = x->pos_host;
   r.tag0 = (unsigned)(1 + x->ptk.gti * (uint64_t)P.ppt);
   r.want_logits = 1;
+  r.eos = eos;
   r.err.flag = x->ptk.err;
+  // DAIZA_PTK_SPIN=<n> lowers the bound of every wait in the launch (a wait that gives up ends the
+  // launch with DZ_ERR_DEVICE); for tests of the failure path, which must stay on the host's side.
   r.err.spin_limit = 1 << 21;
+  if (const char* sl = getenv("DAIZA_PTK_SPIN")) {
+    const long v = strtol(sl, nullptr, 10);
+    if (v > 0 && v < (1 << 21)) r.err.spin_limit = (int)v;
+  }
   // DAIZA_PTK_TRACE=<file>: append per-phase times of every workgroup to <file> (binary: int32
   // n_tok, ppt, G, slots, then n_tok*ppt*G*slots uint64 s_memrealtime ticks of 10 ns)
   const char* trace_path = getenv("DAIZA_PTK_TRACE");
@@ -1060,9 +1095,16 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0)
   }
   if (err[0]) {
     DZ_HIP_CHECK(hipMemset(x->ptk.err, 0, 16));
+    x->poisoned = true;
     return set_error(DZ_ERR_DEVICE, "token kernel: wait timed out (code %d, phase tag %u, workgroup %d)", err[0],
                      (unsigned)err[1], err[2]);
   }
+  if (err[3] < 0 || err[3] > n) {
+    x->poisoned = true;
+    return set_error(DZ_ERR_DEVICE, "token kernel: %d of %d tokens reported", err[3], n);
+  }
+  n = err[3];
+  if (n_done) *n_done = n;
   x->pos_host += n;
   // keep TokState consistent for the graph-path kernels (mixer steps)
   int pp[2] = {x->pos_host - 1, x->pos_host};
@@ -1379,6 +1421,7 @@ int ctx_verify_enqueue(dz_ctx* x, const uint32_t* draft, int k) {
   if (!x || !draft) return set_error(DZ_ERR_MODEL, "null argument");
   if (k < 1) return set_error(DZ_ERR_TENSOR, "verify: %d drafts", k);
   if (k > kBatchChunk) return set_error(DZ_ERR_TENSOR, "verify: %d drafts (at most %d)", k, kBatchChunk);
+  if (int rc0 = ctx_usable(x)) return rc0;
   return bt_verify_forward(x, draft, k);
 }
 
@@ -1485,6 +1528,7 @@ int dz_ctx_token_kernel(const dz_ctx* x) { return x && x->ptk.on ? 1 : 0; }
 
 int dz_forward_token(dz_ctx* x, uint32_t token, float* logits, uint32_t* argmax) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (int rc0 = ctx_usable(x)) return rc0;
   x->bt.pending = 0;
   if (x->ptk.on) {
     int rc = ptk_feed(x, &token, 1);
@@ -1515,6 +1559,7 @@ int dz_forward_token(dz_ctx* x, uint32_t token, float* logits, uint32_t* argmax)
 int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float* last_logits, float* per_pos) {
   if (!x || (!ids && n)) return set_error(DZ_ERR_MODEL, "null argument");
   if (n < 1) return set_error(DZ_ERR_TENSOR, "forward_batch: empty batch");
+  if (int rc0 = ctx_usable(x)) return rc0;
   if (start_pos != x->pos_host)
     return set_error(DZ_ERR_TENSOR, "forward_batch: start_pos %d != context position %d", start_pos, x->pos_host);
   if (x->pos_host + n > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "forward_batch: context full");
@@ -1549,6 +1594,7 @@ int dz_forward_batch(dz_ctx* x, const uint32_t* ids, int n, int start_pos, float
 
 int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_tokens) {
   if (!x || !out_tokens) return set_error(DZ_ERR_MODEL, "null argument");
+  if (int rc0 = ctx_usable(x)) return rc0;
   if (n < 1) return DZ_OK;
   x->bt.pending = 0;
   const int p0 = x->pos_host;
@@ -1567,6 +1613,37 @@ int dz_decode_greedy(dz_ctx* x, uint32_t first_token, int n, uint32_t* out_token
   return DZ_OK;
 }
 
+int dz_decode_greedy_eos(dz_ctx* x, uint32_t first_token, int n, int32_t eos_id, uint32_t* out_tokens,
+                         int* n_forwarded) {
+  if (!x || !out_tokens || !n_forwarded) return set_error(DZ_ERR_MODEL, "null argument");
+  *n_forwarded = 0;
+  if (int rc0 = ctx_usable(x)) return rc0;
+  if (n < 1 || (eos_id >= 0 && first_token == (uint32_t)eos_id)) return DZ_OK;
+  x->bt.pending = 0;
+  const int p0 = x->pos_host;
+  if (x->ptk.on) {
+    int done = 0;
+    int rc = ptk_feed(x, &first_token, 1);
+    if (rc || (rc = ptk_run(x, n, 1, false, 0, eos_id < 0 ? -1 : eos_id, &done))) return rc;
+    if (done) DZ_HIP_CHECK(hipMemcpy(out_tokens, x->toklog + p0 + 1, (size_t)done * 4, hipMemcpyDeviceToHost));
+    *n_forwarded = done;
+    return DZ_OK;
+  }
+  // graph path: one token per replay, the pick read back and checked on the host
+  int rc = ctx_feed(x, &first_token, 1);
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i) {
+    if ((rc = ctx_run(x, 1)) || (rc = ctx_peek_argmax(x))) return rc;
+    int t;
+    DZ_HIP_CHECK(hipMemcpyAsync(&t, x->toklog + x->pos_host, 4, hipMemcpyDeviceToHost, x->s));
+    DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+    out_tokens[i] = (uint32_t)t;
+    *n_forwarded = i + 1;
+    if (eos_id >= 0 && t == eos_id) break;
+  }
+  return DZ_OK;
+}
+
 int dz_verify_forward(dz_ctx* x, const uint32_t* draft, int k, float* per_pos_logits) {
   int rc = dz::ctx_verify_enqueue(x, draft, k);
   if (rc) return rc;
@@ -1580,6 +1657,7 @@ int dz_verify_forward(dz_ctx* x, const uint32_t* draft, int k, float* per_pos_lo
 
 int dz_verify_commit(dz_ctx* x, int n_accept) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (int rc0 = ctx_usable(x)) return rc0;
   if (x->bt.pending == 0 && n_accept == 0) return DZ_OK;
   if (x->bt.pending == 0) return set_error(DZ_ERR_TENSOR, "verify commit without a verify forward");
   return bt_verify_commit(x, n_accept);
@@ -1684,23 +1762,61 @@ int dz_kv_truncate(dz_ctx* x, int len) {
   x->bt.pending = 0;
   if (len >= x->pos_host) return DZ_OK;  // KvCache::truncate keeps longer requests as no-ops
   if (len < 0) return set_error(DZ_ERR_TENSOR, "truncate to %d", len);
-  return ctx_set_pos_dev(x, len);
+  return ctx_move_pos(x, len);
 }
 
 int dz_ctx_set_pos(dz_ctx* x, int pos) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
   x->bt.pending = 0;
   if (pos < 0 || pos >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "pos %d out of [0, max_ctx)", pos);
-  // ring heads are stored relative to pos: keep each layer's physical head unchanged
-  const int old = x->pos_host;
-  for (size_t i = 0; i < x->ring_base.size(); ++i) x->ring_base[i] = ((x->ring_base[i] + old - pos) % 4 + 4) % 4;
-  if (!x->ring_base.empty())
-    DZ_HIP_CHECK(hipMemcpy(x->ring_base_dev, x->ring_base.data(), x->ring_base.size() * 4, hipMemcpyHostToDevice));
-  return ctx_set_pos_dev(x, pos);
+  return ctx_move_pos(x, pos);
+}
+
+}  // extern "C"
+
+namespace dz {
+// TokState.pos = pos (the token being run), pos_next = pos + 1, enqueued on the stream.
+__global__ void set_tok_pos_kernel(TokState* st, int pos) {
+  if (threadIdx.x == 0) {
+    st->pos = pos;
+    st->pos_next = pos + 1;
+  }
+}
+}  // namespace dz
+
+extern "C" {
+
+int dz_ctx_mixer_step_dev(dz_ctx* x, int layer, const float* h_dev, float* h_out_dev) {
+  if (!x || !h_dev || !h_out_dev) return set_error(DZ_ERR_MODEL, "null argument");
+  if (int rc0 = ctx_usable(x)) return rc0;
+  if (layer < 0 || layer >= x->m->cfg.n_layers) return set_error(DZ_ERR_TENSOR, "layer %d out of range", layer);
+  if (x->pos_host >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "context full");
+  const dz_config& c = x->m->cfg;
+  int64_t ld_in, ld_h, ld_gu;
+  int th, to, tf;
+  ctx_dims(x->m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
+  const int P = x->pos_host;
+  x->bt.pending = 0;
+  hipLaunchKernelGGL(set_tok_pos_kernel, dim3(1), dim3(64), 0, x->s, x->st, P);
+  DZ_HIP_CHECK(hipGetLastError());
+  DZ_HIP_CHECK(hipMemcpyAsync(x->h[1], h_dev, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice, x->s));
+  int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s);
+  if (rc) return rc;
+  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden};
+  rc = with_np_bucket(fa.np, [&](auto B) -> int {
+    hipLaunchKernelGGL(final_reduce_kernel<decltype(B)::value>, dim3((unsigned)th), dim3(512), 0, x->s, fa);
+    DZ_HIP_CHECK(hipGetLastError());
+    return DZ_OK;
+  });
+  if (rc) return rc;
+  DZ_HIP_CHECK(hipMemcpyAsync(h_out_dev, x->h_fin, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice, x->s));
+  x->pos_host = P + 1;
+  return DZ_OK;
 }
 
 int dz_ctx_mixer_step(dz_ctx* x, int layer, float* h) {
   if (!x || !h) return set_error(DZ_ERR_MODEL, "null argument");
+  if (int rc0 = ctx_usable(x)) return rc0;
   if (layer < 0 || layer >= x->m->cfg.n_layers) return set_error(DZ_ERR_TENSOR, "layer %d out of range", layer);
   if (x->pos_host >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "context full");
   const dz_config& c = x->m->cfg;

@@ -64,7 +64,7 @@ __device__ __forceinline__ int flag_ld(const int* p) {
 }
 
 struct PtkErr {
-  int* flag;  // first failure: code, phase tag, workgroup (0 = none)
+  int* flag;  // first failure: code, phase tag, workgroup (0 = none); [3]: tokens forwarded
   int spin_limit;
 };
 
@@ -185,7 +185,8 @@ struct PtkRun {
   int pos0;                    // position of the first token
   unsigned tag0;               // tag base of the first token (token i: tag0 + i*ppt)
   int want_logits;             // 1: write logits (last token; all tokens when logits_all is set)
-  PtkErr err;
+  int eos;                     // >= 0: a greedy pick equal to eos ends the launch unforwarded
+  PtkErr err;                  // err.flag[3] receives the number of tokens forwarded
   u64* trace;                  // optional [n_tok][ppt][G][kPtkTraceSlots] times (s_memrealtime), else null
 };
 

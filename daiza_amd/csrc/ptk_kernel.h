@@ -373,9 +373,8 @@ __device__ __forceinline__ int s_pick(const PtkPlan& P, unsigned lane, const u64
 
 __device__ __forceinline__ bool s_select(const PtkPlan& P, const PtkRun& r, int i, int w, unsigned lane, u64* hemb,
                                          const u64* cand_v, const u64* cand_i, unsigned tag_prev, unsigned tag,
-                                         int pos) {
+                                         int pos, int& tok) {
   bool ok = true;
-  int tok;
   if (i < r.n_feed) {
     tok = __builtin_amdgcn_readfirstlane(glb(r.feed)[i]);
   } else {
@@ -1092,7 +1091,9 @@ __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const 
   if constexpr (!SYNC) {
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    const bool last = i == r.n_tok - 1;
+    // the context's logits: the last token's, or every token's when an EOS pick may end the launch
+    // early (the logits of the last token forwarded, as the reference leaves them)
+    const bool last = i == r.n_tok - 1 || r.eos >= 0;
 #pragma unroll
     for (int m = 0; m < U_LM; ++m) {
       const int rb = rb0 + (int)cw + kCW * m;
@@ -1175,16 +1176,35 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   // `ok` carries the sync wave's outcome from its poll phases to the next workgroup barrier
   bool ok = true;
   int dn_seq = 0;  // DeltaNet phases passed (the compute waves' conv-input arrivals count 3 per phase)
+  bool stopped = false;
+  int n_done = r.n_tok;
   for (int i = 0; i < r.n_tok; ++i) {
     const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
     const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);
     const int pos = r.pos0 + i;
     u64* tokreg = ll_region(P0, par, P0.n_layers);
     const u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
+    int tok = 0;
     if constexpr (SYNC) {
       ok = s_select(P0, r, i, w0, threadIdx.x, tokreg, prev_tok + cand_off, prev_tok + cand_off + G,
-                    tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos);
+                    tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos, tok);
       ptk_mark(r, P0, i, 0, w0, threadIdx.x, 0);
+    }
+    // EOS stop (engine.rs:850-871: a sampled eos_token_id ends the loop before it is forwarded).  Every
+    // workgroup picks the same token from the same candidates, so all of them stop at the same step;
+    // the sync wave hands its decision to the compute waves through LDS.  toklog[pos] already holds
+    // the eos id.
+    if (r.eos >= 0) {
+      int* stopw = lds_ptr<int>(smem, kLdsFlag + 8);
+      if constexpr (SYNC) {
+        if (threadIdx.x == 0) *stopw = (i >= r.n_feed && tok == r.eos) ? 1 : 0;
+      }
+      lds_barrier();
+      if (*stopw) {
+        stopped = true;
+        n_done = i;
+        break;
+      }
     }
     const u64* h_in = tokreg;
     unsigned tag_h = tb;
@@ -1319,9 +1339,13 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
       return;
     if constexpr (SYNC) ptk_mark(r, P0, i, P0.ph_l, w0, threadIdx.x, 0);
   }
+  // tokens forwarded by this launch (fewer than n_tok after an EOS stop), for the host
+  if constexpr (SYNC) {
+    if (w0 == 0 && threadIdx.x == 0) __hip_atomic_store(glb(e.flag) + 3, n_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   // greedy pick after the last token, published as toklog[pos0 + n_tok] (workgroup 0)
   if constexpr (SYNC) {
-    if (w0 == 0) {
+    if (w0 == 0 && !stopped) {
       const int i = r.n_tok;
       const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
       const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);

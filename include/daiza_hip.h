@@ -135,7 +135,10 @@ int dz_model_create_synth(const dz_config* cfg, uint64_t seed, dz_model** out);
 int dz_model_free(dz_model* m);
 int dz_model_weight_bytes(const dz_model* m, uint64_t* q1_bytes);
 
-/* Context = ModelState + ForwardContext (forward.rs:32-131): KV caches, SSM states, position. */
+/* Context = ModelState + ForwardContext (forward.rs:32-131): KV caches, SSM states, position.
+ * If a forward fails with DZ_ERR_DEVICE because a device-side wait gave up, the launch may have
+ * updated part of the state; the context then refuses every forward with DZ_ERR_DEVICE until
+ * dz_ctx_reset.  (The reference's forward cannot fail part-way; this has no counterpart there.) */
 int dz_ctx_create(dz_model* m, dz_ctx** out);
 int dz_ctx_free(dz_ctx* c);
 int dz_ctx_reset(dz_ctx* c);          /* ModelState::reset (forward.rs:66-76) */
@@ -163,6 +166,17 @@ int dz_forward_batch(dz_ctx* c, const uint32_t* ids, int n, int start_pos,
  * Mirrors the greedy loop of Engine::generate_inner (engine.rs:850-871) without the EOS stop.
  */
 int dz_decode_greedy(dz_ctx* c, uint32_t first_token, int n, uint32_t* out_tokens);
+
+/*
+ * The greedy loop of Engine::generate_inner (engine.rs:850-871) with its EOS stop: like
+ * dz_decode_greedy, but a pick equal to eos_id (>= 0; Config::eos_token_id, config.rs:69, is 248046)
+ * ends the loop before that token is forwarded.  *n_forwarded receives the number of forwards run
+ * (0 when first_token is eos_id); out_tokens[i] (i < *n_forwarded) is the pick after forward i, so the
+ * loop stopped on EOS exactly when out_tokens[*n_forwarded - 1] == eos_id.  The position advances by
+ * *n_forwarded and the context's logits are those of the last forward.
+ */
+int dz_decode_greedy_eos(dz_ctx* c, uint32_t first_token, int n, int32_t eos_id, uint32_t* out_tokens,
+                         int* n_forwarded);
 
 /* Last computed logits (vocab f32) of the context. */
 int dz_ctx_logits(dz_ctx* c, float* logits);
@@ -237,6 +251,11 @@ int dz_ctx_set_pos(dz_ctx* c, int pos);
  * context position (BASELINE configs 2 and 3).
  */
 int dz_ctx_mixer_step(dz_ctx* c, int layer, float* h);
+
+/* dz_ctx_mixer_step on device vectors h_dev[hidden] -> h_out_dev[hidden] (may be the same buffer),
+ * enqueued on the context's stream without a host synchronisation (for timing one layer-step with
+ * the weights, state and input resident in HBM).  Advances the position like dz_ctx_mixer_step. */
+int dz_ctx_mixer_step_dev(dz_ctx* c, int layer, const float* h_dev, float* h_out_dev);
 
 /* The context's HIP stream (hipStream_t), for callers that time or order work around it. */
 void* dz_ctx_stream(dz_ctx* c);

@@ -84,6 +84,7 @@ def lib():
         L.or_ctx_pos.restype = ctypes.c_int
         L.or_ctx_pos.argtypes = [ctypes.c_void_p]
         L.or_ctx_set_pos.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.or_kv_truncate.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.or_model_embd_row.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
         L.or_forward_token.restype = ctypes.c_int
         L.or_forward_token.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
@@ -238,6 +239,10 @@ class Model:
 
     def set_pos(self, p):
         lib().or_ctx_set_pos(self._c, p)
+
+    def kv_truncate(self, n):
+        """KvCache::truncate on every attention layer (kv_cache.rs:119-130), pos = n."""
+        lib().or_kv_truncate(self._c, int(n))
 
     def forward(self, token, want_logits=True):
         logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None

@@ -956,6 +956,14 @@ void or_ctx_free(or_ctx* x) {
 int or_ctx_pos(or_ctx* x) { return x->pos; }
 void or_ctx_set_pos(or_ctx* x, int pos) { x->pos = pos; }
 
+/* KvCache::truncate (kv_cache.rs:119-130) on every attention layer, then pos = len: a longer len
+ * leaves a cache as it is; the DeltaNet states and conv rings (SsmState) are not touched. */
+void or_kv_truncate(or_ctx* x, int len) {
+  for (int i = 0; i < x->m->cfg.n_layers; ++i)
+    if (x->m->L[i].is_attn && len < x->kv_len[i]) x->kv_len[i] = len;
+  x->pos = len;
+}
+
 static void mv(or_ctx* x, const qmat* w, const float* in, float* out, int acc) {
   or_matvec(w->q, w->rows, w->cols, in, out, acc, x->m->nthreads);
 }

@@ -86,6 +86,8 @@ or_ctx* or_ctx_new(or_model* m);
 void or_ctx_free(or_ctx* c);
 int or_ctx_pos(or_ctx* c);
 void or_ctx_set_pos(or_ctx* c, int pos);
+/* KvCache::truncate (kv_cache.rs:119-130) on every attention layer, pos = len; SSM state untouched. */
+void or_kv_truncate(or_ctx* c, int len);
 /* forward_single_token (forward.rs:204-375); logits may be NULL; returns argmax */
 void or_model_embd_row(or_model* m, uint32_t token, float* out);
 int or_forward_token(or_ctx* c, uint32_t token, float* logits);

@@ -101,6 +101,9 @@ def lib():
     L.dz_q1_0_partials_ld.argtypes = [_vp]
     L.dz_q1_0_partials_ld.restype = ctypes.c_size_t
     L.dz_q1_0_ntiles.argtypes = [_vp]
+    L.dz_q1_0_matvec_dev_noalloc.argtypes = [_vp, _vp, _vp, ctypes.c_int, _vp]
+    L.dz_q1_0_noalloc_max_partials.argtypes = []
+    L.dz_q1_0_noalloc_max_partials.restype = ctypes.c_size_t
     for name, args in _MODEL_PROTOS.items():
         fn = getattr(L, name, None)
         if fn is not None:
@@ -153,6 +156,7 @@ EXPORTED_SYMBOLS = [
     "dz_config_bonsai27b", "dz_last_error", "dz_device_init",
     "dz_q1_0_upload", "dz_q1_0_free", "dz_q1_0_shape", "dz_q1_0_matvec", "dz_q1_0_matvec_multi", "dz_q1_0_matvec_batch",
     "dz_q1_0_matvec_dev", "dz_q1_0_dequant_rows", "dz_q1_0_gemv_partials", "dz_q1_0_partials_ld", "dz_q1_0_ntiles",
+    "dz_q1_0_matvec_dev_noalloc", "dz_q1_0_noalloc_max_partials",
 ] + list(k for k in _MODEL_PROTOS if k != "dz_config_bonsai27b")
 
 

@@ -32,6 +32,15 @@ static int g_device = -1;
 static hipStream_t g_stream = nullptr;
 static std::mutex g_mu;
 
+// Workspace of dz_q1_0_matvec_dev_noalloc: the split-K partials of one product, for callers that
+// cannot allocate.  Each device that runs the library holds its own copy until the process ends.
+// In host code `scratch` only names the symbol; its device address (per device) is looked up once
+// at set-up and kept in g_scratch_dev, which is what kernels receive.
+constexpr size_t kNoAllocScratchFloats = (size_t)4 << 20;  // 16 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+constexpr int kMaxDevices = 16;
+static float* g_scratch_dev[kMaxDevices] = {};
+
 int ensure_device() {
   std::lock_guard<std::mutex> lk(g_mu);
   if (g_device >= 0) {
@@ -46,6 +55,12 @@ int ensure_device() {
     return set_error(DZ_ERR_DEVICE, "device 0 is %s; this library is built for gfx950 only", prop.gcnArchName);
   DZ_HIP_CHECK(hipSetDevice(0));
   DZ_HIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  // the no-alloc workspace of this device (device 0 is current)
+  void* sp = nullptr;
+  hipError_t e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || sp == nullptr)
+    return set_error(DZ_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  g_scratch_dev[0] = static_cast<float*>(sp);
   g_device = 0;
   return DZ_OK;
 }
@@ -363,8 +378,9 @@ hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n
 
 static Scratch g_x, g_y, g_part, g_pack, g_split;
 
+// ws: the partials' workspace (ws_floats of them), or null for the library's growing buffer.
 static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* const* y_dev, int accumulate,
-                       hipStream_t s) {
+                       hipStream_t s, float* ws = nullptr, size_t ws_floats = 0) {
   int prc = prepare_gemv_kernels();
   if (prc) return prc;
   const Q1Dev* ds[8];
@@ -372,9 +388,16 @@ static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* co
   GemvPlan p;
   int rc = plan_gemv(ds, n, 1, &p);
   if (rc) return rc;
-  rc = g_part.reserve((size_t)p.g.n_tg * p.ld * sizeof(float));
-  if (rc) return rc;
-  float* part = static_cast<float*>(g_part.ptr);
+  const size_t need = (size_t)p.g.n_tg * (size_t)p.ld;
+  float* part = ws;
+  if (ws) {
+    if (need > ws_floats)
+      return set_error(DZ_ERR_UNSUPPORTED, "matvec_dev_noalloc: %zu partial sums exceed the workspace of %zu", need,
+                       ws_floats);
+  } else {
+    if ((rc = g_part.reserve(need * sizeof(float)))) return rc;
+    part = static_cast<float*>(g_part.ptr);
+  }
   PlainSrc src{x_dev, mats[0]->d.cols};
   PartialDst dst{part, p.ld};
   DZ_HIP_CHECK(launch_gemv(p, src, dst, s));
@@ -398,7 +421,9 @@ const char* dz_last_error(void) { return g_err; }
 
 int dz_device_init(int device) {
   if (device != 0) return set_error(DZ_ERR_UNSUPPORTED, "only device 0 is supported");
-  return ensure_device();
+  int rc = ensure_device();
+  if (rc) return rc;
+  return prepare_gemv_kernels();  // kernel attributes once here, not on a first call of any entry point
 }
 
 void dz_config_bonsai27b(dz_config* c, int32_t max_ctx) {
@@ -458,6 +483,21 @@ int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumula
   float* ys[1] = {y_dev};
   return matvec_impl(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
 }
+
+int dz_q1_0_matvec_dev_noalloc(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream) {
+  if (!m || !x_dev || !y_dev) return set_error(DZ_ERR_TENSOR, "matvec_dev_noalloc: null pointer");
+  int dev = -1;
+  DZ_HIP_CHECK(hipGetDevice(&dev));
+  // set-up (stream, workspace address) happens in dz_device_init, never here: this entry allocates nothing
+  if (g_device < 0 || dev < 0 || dev >= kMaxDevices || g_scratch_dev[dev] == nullptr)
+    return set_error(DZ_ERR_DEVICE, "matvec_dev_noalloc: call dz_device_init first");
+  dz_mat* ms[1] = {m};
+  float* ys[1] = {y_dev};
+  return matvec_impl(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream(), g_scratch_dev[dev],
+                     kNoAllocScratchFloats);
+}
+
+size_t dz_q1_0_noalloc_max_partials(void) { return kNoAllocScratchFloats; }
 
 int dz_q1_0_gemv_partials(dz_mat* m, const float* x_dev, float* part_dev, void* stream) {
   if (!m || !x_dev || !part_dev) return set_error(DZ_ERR_TENSOR, "gemv_partials: null pointer");

@@ -98,6 +98,16 @@ int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumul
  * without a host synchronisation.  The token loop uses the fused kernels instead. */
 int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);
 
+/* dz_q1_0_matvec_dev that allocates nothing, for callers that cannot call hipMalloc (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation); no counterpart in the
+ * reference.  The split-K partial sums go to a fixed per-device workspace of
+ * dz_q1_0_noalloc_max_partials() floats (16 MiB, held until the process ends): a matrix needs
+ * ceil(cols/512) * (rows rounded up to 64) of them, and a larger one is refused with
+ * DZ_ERR_UNSUPPORTED.  dz_device_init must have run.  Every call on a device shares its workspace,
+ * so calls that overlap on one device (several streams or threads) race. */
+int dz_q1_0_matvec_dev_noalloc(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);
+size_t dz_q1_0_noalloc_max_partials(void);
+
 /* Split-K form on device pointers: writes part_dev[t][r] for K tiles t = 0..ceil(cols/512)-1 and
  * rows r < dz_q1_0_partials_ld(m) (row count padded to 64), so that y[r] = sum_t part[t][r] in
  * tile order.  For callers that fuse the tile sum into their next kernel, as the token loop does

@@ -117,6 +117,15 @@ _MODEL_PROTOS = {
     "dz_config_bonsai27b": ([_vp, ctypes.c_int32], None),
     "dz_model_create": ([_vp, _vp, ctypes.c_int, ctypes.POINTER(_vp)], ctypes.c_int),
     "dz_model_create_synth": ([_vp, ctypes.c_uint64, ctypes.POINTER(_vp)], ctypes.c_int),
+    "dz_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], ctypes.c_int),
+    "dz_gguf_close": ([_vp], ctypes.c_int),
+    "dz_gguf_n_tensors": ([_vp], ctypes.c_int),
+    "dz_gguf_tensor_info": ([_vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int32),
+                             ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_uint64),
+                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "dz_gguf_tensor_data": ([_vp, ctypes.c_int], _vp),
+    "dz_gguf_config": ([_vp, ctypes.c_int32, _vp, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
+    "dz_model_create_gguf": ([_vp, _vp, ctypes.POINTER(_vp)], ctypes.c_int),
     "dz_model_free": ([_vp], ctypes.c_int),
     "dz_model_weight_bytes": ([_vp, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "dz_ctx_create": ([_vp, ctypes.POINTER(_vp)], ctypes.c_int),
@@ -304,6 +313,61 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+class GgufFile:
+    """A GGUF v3 file mapped read-only (GgufFile::open, gguf/parser.rs:40-119)."""
+
+    def __init__(self, path):
+        h = _vp()
+        _check(lib().dz_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().dz_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """[(name, type, dims in GGUF order, absolute offset, n_bytes)] in file order."""
+        out = []
+        for i in range(lib().dz_gguf_n_tensors(self._h)):
+            name, ty, nd = ctypes.c_char_p(), ctypes.c_int32(), ctypes.c_int32()
+            dims = (ctypes.c_uint64 * 4)()
+            off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+            _check(lib().dz_gguf_tensor_info(self._h, i, ctypes.byref(name), ctypes.byref(ty), ctypes.byref(nd), dims,
+                                             ctypes.byref(off), ctypes.byref(nb)))
+            out.append((name.value.decode(), ty.value, tuple(dims[:nd.value]), off.value, nb.value))
+        return out
+
+    def tensor_bytes(self, i):
+        p = lib().dz_gguf_tensor_data(self._h, i)
+        if not p:
+            return None
+        n = self.tensors()[i][4]
+        return np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(p)).copy()
+
+    def config(self, max_ctx=4096):
+        """Config::from_metadata (model/config.rs:76-160); returns (Config, eos_token_id)."""
+        c = Config()
+        eos = ctypes.c_int32()
+        _check(lib().dz_gguf_config(self._h, int(max_ctx), ctypes.byref(c), ctypes.byref(eos)))
+        return c, eos.value
+
+    def model(self, cfg):
+        """LoadedWeights::load_all (weights.rs:1308-1379) on the device."""
+        m = Model.__new__(Model)
+        m.cfg = cfg
+        h = _vp()
+        _check(lib().dz_model_create_gguf(self._h, ctypes.byref(cfg), ctypes.byref(h)))
+        m._h = h
+        return m
 
 
 class SamplingParams(ctypes.Structure):

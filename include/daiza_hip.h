@@ -140,6 +140,29 @@ typedef struct dz_tensor {
 
 int dz_model_create(const dz_config* cfg, const dz_tensor* tensors, int n_tensors, dz_model** out);
 
+/* ---- GGUF files (Daiza-engine/src/gguf) ----
+ * dz_gguf_open: GgufFile::open (gguf/parser.rs:40-119): maps the file read-only and parses the v3
+ * header, the metadata table (metadata.rs) and the tensor table (tensor_info.rs:41-201; dims in GGUF
+ * order, dims[0] = columns; Q1_0 is type 41); the data section starts at the next multiple of
+ * general.alignment (default 32).  The tensors stay slices of the mapping until dz_gguf_close.
+ * dz_gguf_tensor_info: *offset is the absolute file offset of the data, *n_bytes 0 for a type this
+ * path does not use (only F32, F16, BF16 and Q1_0 are sized).  dz_gguf_tensor_data: the data in
+ * the mapping, or NULL. */
+typedef struct dz_gguf dz_gguf;
+int dz_gguf_open(const char* path, dz_gguf** out);
+int dz_gguf_close(dz_gguf* g);
+int dz_gguf_n_tensors(const dz_gguf* g);
+int dz_gguf_tensor_info(const dz_gguf* g, int i, const char** name, int32_t* type, int32_t* n_dims, uint64_t* dims,
+                        uint64_t* offset, uint64_t* n_bytes);
+const void* dz_gguf_tensor_data(const dz_gguf* g, int i);
+/* Config::from_metadata (model/config.rs:76-160): the Bonsai-27B defaults overridden by every
+ * qwen35.* key present (architecture must be "qwen35"); embd_f16 from token_embd.weight's type;
+ * *eos_token_id (may be NULL) from tokenizer.ggml.eos_token_id (default 248046). */
+int dz_gguf_config(const dz_gguf* g, int32_t max_ctx, dz_config* cfg, int32_t* eos_token_id);
+/* LoadedWeights::load_all (model/weights.rs:1308-1379): the file's tensors by name through
+ * dz_model_create (the file stays open only for the call). */
+int dz_model_create_gguf(const dz_gguf* g, const dz_config* cfg, dz_model** out);
+
 /* Synthetic model with the generator of daiza_synth.h (BASELINE.json config 4 when cfg is Bonsai-27B). */
 int dz_model_create_synth(const dz_config* cfg, uint64_t seed, dz_model** out);
 int dz_model_free(dz_model* m);

@@ -200,3 +200,30 @@ def test_failed_wait_poisons_context(dz, oracle, monkeypatch):
         am, lg = ctx.forward_single_token(t)
         oam, olg = om.forward(t)
         assert normwise_rel(lg, olg) < 1e-3 and am == oam
+
+
+@pytest.mark.parametrize("embd_f16", [1, 0])
+def test_model_from_gguf_file(dz, oracle, tmp_path, embd_f16):
+    """A GGUF file of the synthetic model (tests/gguf_writer.py) through GgufFile::open,
+    Config::from_metadata and LoadedWeights::load_all (dz_gguf_open, dz_gguf_config,
+    dz_model_create_gguf): the same logits as dz_model_create_synth bit for bit, and as the oracle."""
+    from gguf_writer import model_metadata, model_tensors, write_gguf
+    cfg = dz.Config.small(n_layers=4, max_ctx=32, embd_f16=embd_f16)
+    om = oracle.Model(cfg, SEED)
+    path = str(tmp_path / "model.gguf")
+    write_gguf(path, model_metadata(cfg) + [("general.alignment", 10, 64)],
+               model_tensors(named_tensors(oracle, om, cfg, SEED), cfg), alignment=64)
+    g = dz.GgufFile(path)
+    gcfg, eos = g.config(max_ctx=32)
+    for name, _ in dz.Config._fields_:
+        assert getattr(gcfg, name) == pytest.approx(getattr(cfg, name)), name
+    m_file = g.model(gcfg)
+    g.close()
+    m_synth = dz.Model.synthetic(cfg, SEED)
+    c_file, c_synth = dz.Context(m_file), dz.Context(m_synth)
+    for t in (5, 2047, 0, 731):
+        a1, l1 = c_file.forward_single_token(t)
+        a2, l2 = c_synth.forward_single_token(t)
+        ao, lo = om.forward(t)
+        assert np.array_equal(l1, l2), t
+        assert normwise_rel(l1, lo) < 1e-3 and a1 == a2 == ao, t

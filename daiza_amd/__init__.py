@@ -125,6 +125,7 @@ _MODEL_PROTOS = {
                              ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "dz_gguf_tensor_data": ([_vp, ctypes.c_int], _vp),
     "dz_gguf_config": ([_vp, ctypes.c_int32, _vp, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int),
+    "dz_gguf_context_length": ([_vp, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "dz_model_create_gguf": ([_vp, _vp, ctypes.POINTER(_vp)], ctypes.c_int),
     "dz_model_free": ([_vp], ctypes.c_int),
     "dz_model_weight_bytes": ([_vp, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
@@ -148,6 +149,12 @@ _MODEL_PROTOS = {
     "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
     "dz_ctx_mixer_step_dev": ([_vp, ctypes.c_int, _vp, _vp], ctypes.c_int),
     "dz_ctx_stream": ([_vp], _vp),
+    "dz_session_cfg_hash": ([_vp, ctypes.c_uint64], ctypes.c_uint64),
+    "dz_ctx_save": ([_vp, ctypes.c_char_p, ctypes.c_uint64, _u32p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_char_p],
+                    ctypes.c_int),
+    "dz_ctx_load": ([_vp, ctypes.c_char_p, ctypes.c_uint64, _u32p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64),
+                     ctypes.POINTER(ctypes.c_int32), ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+                    ctypes.c_int),
     "dz_ctx_token_kernel": ([_vp], ctypes.c_int),
     "dz_ctx_vocab": ([_vp, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "dz_verify_forward": ([_vp, _u32p, ctypes.c_int, _f32p], ctypes.c_int),
@@ -360,6 +367,12 @@ class GgufFile:
         _check(lib().dz_gguf_config(self._h, int(max_ctx), ctypes.byref(c), ctypes.byref(eos)))
         return c, eos.value
 
+    def context_length(self):
+        """Config::context_length (model/config.rs:52, 92-93), hashed into DZSS session files."""
+        v = ctypes.c_uint64()
+        _check(lib().dz_gguf_context_length(self._h, ctypes.byref(v)))
+        return v.value
+
     def model(self, cfg):
         """LoadedWeights::load_all (weights.rs:1308-1379) on the device."""
         m = Model.__new__(Model)
@@ -414,6 +427,14 @@ def sample_bonus(target, draft, params, rng):
     _check(lib().dz_sample_bonus(_f(t), _f(d), t.size, ctypes.byref(params), ctypes.byref(rng.state),
                                  ctypes.byref(out)))
     return out.value
+
+
+CONTEXT_LENGTH = 262144  # qwen35.context_length of Bonsai-27B (Config::context_length), hashed into DZSS files
+
+
+def session_cfg_hash(cfg, context_length=CONTEXT_LENGTH):
+    """cfg_hash of session_persist.rs:52-66 for this configuration."""
+    return lib().dz_session_cfg_hash(ctypes.byref(cfg), int(context_length))
 
 
 class Context:
@@ -507,6 +528,25 @@ class Context:
     def kv_truncate(self, n):
         """KvCache::truncate (kv_cache.rs:119-130): keeps n cached positions, pos = n; conv rings stay."""
         _check(lib().dz_kv_truncate(self._h, int(n)))
+
+    def save(self, path, history=(), think_enabled=False, system_prompt=None, context_length=CONTEXT_LENGTH):
+        """Session::save_to_disk (session_persist.rs:70-146): the DZSS v1 file of this context's state,
+        with the session fields the caller holds (history tokens, think flag, system prompt)."""
+        h = np.ascontiguousarray(history, np.uint32)
+        sp = None if system_prompt is None else system_prompt.encode()
+        _check(lib().dz_ctx_save(self._h, os.fsencode(path), int(context_length), h.ctypes.data_as(_u32p), h.size,
+                                 int(bool(think_enabled)), sp))
+
+    def load(self, path, context_length=CONTEXT_LENGTH, history_cap=1 << 20, prompt_cap=1 << 16):
+        """Session::load_from_disk (session_persist.rs:188-312) into this context; returns
+        (history tokens, think_enabled, system prompt or None)."""
+        hist = np.empty(history_cap, np.uint32)
+        nh, think, plen = ctypes.c_uint64(), ctypes.c_int32(), ctypes.c_uint64()
+        buf = ctypes.create_string_buffer(prompt_cap)
+        _check(lib().dz_ctx_load(self._h, os.fsencode(path), int(context_length), hist.ctypes.data_as(_u32p), history_cap,
+                                 ctypes.byref(nh), ctypes.byref(think), buf, prompt_cap, ctypes.byref(plen)))
+        has_sys = open(path, "rb").read(38)[37] != 0
+        return hist[:nh.value].copy(), bool(think.value), (buf.raw[:plen.value].decode(errors="replace") if has_sys else None)
 
     def logits(self):
         out = np.empty(self.cfg.vocab, np.float32)

@@ -274,6 +274,17 @@ int dz_gguf_config(const dz_gguf* g, int32_t max_ctx, dz_config* cfg, int32_t* e
   return DZ_OK;
 }
 
+// Config::context_length (config.rs:52, 92-93): qwen35.context_length read with Metadata::get_u64,
+// so only a u64 or i64 value replaces the default 262144.  It sizes nothing on this path; DZSS
+// session files hash it.
+int dz_gguf_context_length(const dz_gguf* g, uint64_t* out) {
+  if (!g || !out) return set_error(DZ_ERR_MODEL, "null argument");
+  *out = 262144;
+  auto f = g->kv.find("qwen35.context_length");
+  if (f != g->kv.end() && (f->second.type == kU64 || f->second.type == kI64)) *out = f->second.u;
+  return DZ_OK;
+}
+
 // LoadedWeights::load_all (weights.rs:1308-1379): every tensor of the file, by name, to
 // dz_model_create, which checks the names, types and sizes the model needs.
 int dz_model_create_gguf(const dz_gguf* g, const dz_config* cfg, dz_model** out) {

@@ -1522,6 +1522,12 @@ int dz_ctx_reset(dz_ctx* x) {
 
 int dz_ctx_pos(const dz_ctx* x) { return x ? x->pos_host : -1; }
 
+}  // extern "C"
+
+const dz_config* dz::ctx_config(const dz_ctx* x) { return &x->m->cfg; }
+
+extern "C" {
+
 void* dz_ctx_stream(dz_ctx* x) { return x ? (void*)x->s : nullptr; }
 
 int dz_ctx_token_kernel(const dz_ctx* x) { return x && x->ptk.on ? 1 : 0; }

@@ -49,6 +49,9 @@ hipError_t launch_gemv(const GemvPlan& p, const Src& src, const Dst& dst, hipStr
 // Raises the dynamic-LDS limit of every GEMV instantiation the library launches (idempotent).
 int prepare_gemv_kernels();
 
+// The model config of a context (model.hip).
+const dz_config* ctx_config(const dz_ctx* x);
+
 // Sum of the tile-group partials into each segment's output: y = [y +] sum_tg part[tg][row].
 struct ReduceSeg {
   float* y;

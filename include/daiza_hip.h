@@ -159,6 +159,9 @@ const void* dz_gguf_tensor_data(const dz_gguf* g, int i);
  * qwen35.* key present (architecture must be "qwen35"); embd_f16 from token_embd.weight's type;
  * *eos_token_id (may be NULL) from tokenizer.ggml.eos_token_id (default 248046). */
 int dz_gguf_config(const dz_gguf* g, int32_t max_ctx, dz_config* cfg, int32_t* eos_token_id);
+/* Config::context_length (model/config.rs:52, 92-93): qwen35.context_length when stored as a 64-bit
+ * integer (Metadata::get_u64), else 262144.  Sizes nothing here; the DZSS cfg_hash includes it. */
+int dz_gguf_context_length(const dz_gguf* g, uint64_t* out);
 /* LoadedWeights::load_all (model/weights.rs:1308-1379): the file's tensors by name through
  * dz_model_create (the file stays open only for the call). */
 int dz_model_create_gguf(const dz_gguf* g, const dz_config* cfg, dz_model** out);
@@ -289,6 +292,29 @@ int dz_ctx_mixer_step(dz_ctx* c, int layer, float* h);
  * enqueued on the context's stream without a host synchronisation (for timing one layer-step with
  * the weights, state and input resident in HBM).  Advances the position like dz_ctx_mixer_step. */
 int dz_ctx_mixer_step_dev(dz_ctx* c, int layer, const float* h_dev, float* h_out_dev);
+
+/* ---- session snapshots: DZSS v1 (Daiza-runtime/src/session_persist.rs:47-312) ----
+ * dz_ctx_save writes the context's state as Session::save_to_disk does: a 128-byte header ("DZSS",
+ * version 1, cfg_hash, pos, history length, block count, think flag, system-prompt flag), the history
+ * tokens, then per layer the KV cache (kind 0: per_token, len, K and V as [seq][kv head][dim]) or the
+ * DeltaNet state (kind 1: S[v head][i][j], the conv ring [conv_kernel][qkv_dim], conv_head), then the
+ * system prompt if one is given.  History, think flag and system prompt belong to the reference's
+ * Session, not to the context: the caller passes them (system_prompt NULL = none).
+ * dz_ctx_load checks magic, version, cfg_hash and block count, reads the whole file, and only then
+ * replaces the context's state (reset, position, every layer), so a refused file leaves the context
+ * as it was; a successful load also clears a failed launch's refusal.  history / system_prompt may be
+ * NULL; with a buffer too small (history_cap tokens, prompt_cap bytes including the terminating 0)
+ * it fails with DZ_ERR_TENSOR before touching the context.
+ * context_length is Config::context_length (262144 for Bonsai-27B, qwen35.context_length), one of
+ * the fields of the reference's cfg_hash; dz_session_cfg_hash is that hash (Rust's DefaultHasher,
+ * SipHash-1-3 with zero keys, over block_count, hidden, head_count, head_count_kv, head_dim,
+ * full_attention_interval, ssm_state_size, ssm_time_step_rank, ssm_conv_kernel, context_length). */
+uint64_t dz_session_cfg_hash(const dz_config* cfg, uint64_t context_length);
+int dz_ctx_save(dz_ctx* c, const char* path, uint64_t context_length, const uint32_t* history, uint64_t n_history,
+                int32_t think_enabled, const char* system_prompt);
+int dz_ctx_load(dz_ctx* c, const char* path, uint64_t context_length, uint32_t* history, uint64_t history_cap,
+                uint64_t* n_history, int32_t* think_enabled, char* system_prompt, uint64_t prompt_cap,
+                uint64_t* prompt_len);
 
 /* The context's HIP stream (hipStream_t), for callers that time or order work around it. */
 void* dz_ctx_stream(dz_ctx* c);

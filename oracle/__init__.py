@@ -85,6 +85,8 @@ def lib():
         L.or_ctx_pos.argtypes = [ctypes.c_void_p]
         L.or_ctx_set_pos.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.or_kv_truncate.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.or_siphash.restype = ctypes.c_uint64
+        L.or_siphash.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, u8p, ctypes.c_size_t]
         L.or_model_embd_row.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
         L.or_forward_token.restype = ctypes.c_int
         L.or_forward_token.argtypes = [ctypes.c_void_p, ctypes.c_uint32, f32p]
@@ -131,6 +133,11 @@ def _f(a):
 
 def _u8(a):
     return a.ctypes.data_as(u8p)
+
+
+def siphash(c, d, k0, k1, msg):
+    m = np.frombuffer(bytes(msg), np.uint8).copy() if len(msg) else np.zeros(1, np.uint8)
+    return lib().or_siphash(c, d, k0, k1, _u8(m), len(msg))
 
 
 def f16_to_f32(bits):

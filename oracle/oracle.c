@@ -9,7 +9,8 @@
  * Citations are to /root/reference/Daiza-engine/src/... unless the path says otherwise.
  *
  * Pinning (tests/test_oracle_cpu.py): every function is checked against known answers, closed
- * forms, float64 brute force or the independent float64 restatement tests/npref.py.  Parity
+ * forms, float64 brute force or the independent float64 restatement tests/npref.py; or_siphash
+ * against the published SipHash-2-4 vectors (tests/test_session_cpu.py).  Parity
  * unpinned (matched within tolerance only; only running the reference could fix the bits):
  * sigmoid_ps / silu_ps (vendor-specific _mm256_rcp_ps) and libm expf/logf/powf/sinf/cosf, which
  * the reference takes from its platform's libm and this file from glibc.
@@ -1190,4 +1191,38 @@ void or_synth_normal_f32(uint64_t seed, int kind, int layer, uint64_t i0, uint64
 uint16_t or_f32_to_f16(float v) { return dz_f32_to_f16(v); }
 void or_synth_embd_row_f16(uint64_t seed, uint32_t token, uint64_t hidden, uint16_t* out) {
   dz_synth_embd_row_f16(dz_key(seed, DZ_K_EMBD, (uint32_t)-1), token, hidden, out);
+}
+
+/* ---- SipHash (Aumasson and Bernstein, "SipHash: a fast short-input PRF", 2012) ----
+ * c compression rounds per 8-byte word, d finalisation rounds; little-endian words; the last word
+ * carries the message length mod 256 in its top byte.  SipHash-2-4 is the published function (pinned
+ * by its test vectors); the reference's cfg_hash (Daiza-runtime/src/session_persist.rs:52-66) is
+ * Rust's DefaultHasher, SipHash-1-3 with keys 0 and 0, over ten usize fields as 8-byte LE words. */
+static uint64_t or_rotl(uint64_t x, int b) { return (x << b) | (x >> (64 - b)); }
+#define OR_SIPROUND                                                                  \
+  do {                                                                               \
+    v0 += v1; v1 = or_rotl(v1, 13); v1 ^= v0; v0 = or_rotl(v0, 32);                  \
+    v2 += v3; v3 = or_rotl(v3, 16); v3 ^= v2;                                        \
+    v0 += v3; v3 = or_rotl(v3, 21); v3 ^= v0;                                        \
+    v2 += v1; v1 = or_rotl(v1, 17); v1 ^= v2; v2 = or_rotl(v2, 32);                  \
+  } while (0)
+uint64_t or_siphash(int c, int d, uint64_t k0, uint64_t k1, const uint8_t* m, size_t n) {
+  uint64_t v0 = 0x736f6d6570736575ull ^ k0, v1 = 0x646f72616e646f6dull ^ k1;
+  uint64_t v2 = 0x6c7967656e657261ull ^ k0, v3 = 0x7465646279746573ull ^ k1;
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    uint64_t w = 0;
+    for (int b = 0; b < 8; ++b) w |= (uint64_t)m[i + b] << (8 * b);
+    v3 ^= w;
+    for (int r = 0; r < c; ++r) OR_SIPROUND;
+    v0 ^= w;
+  }
+  uint64_t w = ((uint64_t)n & 0xFF) << 56;
+  for (int b = 0; i + b < n; ++b) w |= (uint64_t)m[i + b] << (8 * b);
+  v3 ^= w;
+  for (int r = 0; r < c; ++r) OR_SIPROUND;
+  v0 ^= w;
+  v2 ^= 0xFF;
+  for (int r = 0; r < d; ++r) OR_SIPROUND;
+  return v0 ^ v1 ^ v2 ^ v3;
 }

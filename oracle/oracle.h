@@ -99,6 +99,9 @@ void or_set_kv(or_ctx* c, int layer, const float* k, const float* v, int len);
 int or_kv_len(or_ctx* c, int layer);
 void or_get_kv(or_ctx* c, int layer, float* k, float* v, int len);
 
+/* SipHash with c compression and d finalisation rounds (session_persist.rs:52-66 uses c=1, d=3). */
+uint64_t or_siphash(int c, int d, uint64_t k0, uint64_t k1, const uint8_t* m, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,7 +60,7 @@ struct dz_ctx {
   float* h[2] = {nullptr, nullptr};
   float* ss[2] = {nullptr, nullptr};
   float *p_in = nullptr, *p_o = nullptr, *p_gu = nullptr, *p_down = nullptr;
-  float *y = nullptr, *zs = nullptr, *apart = nullptr;
+  float *y = nullptr, *zs = nullptr, *apart = nullptr, *attn_u = nullptr;
   float *h_fin = nullptr, *ss_fin = nullptr, *logits = nullptr, *am_val = nullptr;
   int* am_idx = nullptr;
   int n_am = 0;
@@ -70,7 +70,7 @@ struct dz_ctx {
   float* rope = nullptr;       // [max_ctx][rope_dim]
   std::vector<int> ring_base;  // per SSM layer
   int* ring_base_dev = nullptr;
-  int gmax = 64;
+  int gmax = 128;  // graph path: attention chunks per kv head (<= 128, attn_merge_kernel's bound)
   int pos_host = 0;            // mirror of TokState::pos_next
   // Set when a token-kernel launch gave up on a bounded wait: the launch may have stored part of a
   // token's state (DeltaNet rows, KV, conv rows) without the position moving, so every forward is
@@ -568,13 +568,18 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
     a.nq = c.n_head;
     a.nkv = c.n_head_kv;
     if ((rc = launch_attention(c.n_head / c.n_head_kv, dim3((unsigned)(c.n_head_kv * x->gmax)), a, s))) return rc;
+    // merge the chunks and gate once, then the out-projection reads the result as a plain vector
+    AttnMergeArgs ma{x->apart, x->gmax, c.head_dim, x->st, x->p_in, nin, ld_l, ss_mid, th, H, c.rms_eps, x->attn_u};
     rc = with_np_bucket(nin, [&](auto B) -> int {
-      AttnOutSrc<decltype(B)::value> src{x->apart, x->gmax, c.head_dim, (int64_t)c.n_head * c.head_dim, x->st,
-                                         x->p_in, nin, ld_l, ss_mid, th, H, c.rms_eps};
-      PartialDst dst{x->p_o, ld_h};
-      return gemv(l.out_proj, 1, src, dst, s);
+      hipLaunchKernelGGL(attn_merge_kernel<decltype(B)::value>, dim3((unsigned)(c.n_head * (c.head_dim / 64))),
+                         dim3(256), 0, s, ma);
+      DZ_HIP_CHECK(hipGetLastError());
+      return DZ_OK;
     });
     if (rc) return rc;
+    PlainSrc src{x->attn_u, (int64_t)c.n_head * c.head_dim};
+    PartialDst dst{x->p_o, ld_h};
+    if ((rc = gemv(l.out_proj, 1, src, dst, s))) return rc;
   }
   return DZ_OK;
 }
@@ -654,8 +659,7 @@ int dz::prepare_gemv_kernels() {
       constexpr int NB = decltype(B)::value;
       int r;
       if ((r = set_gemv_attr<ResidSrc<NB>, PartialDst>())) return r;
-      if ((r = set_gemv_attr<SwigluSrc<NB>, PartialDst>())) return r;
-      return set_gemv_attr<AttnOutSrc<NB>, PartialDst>();
+      return set_gemv_attr<SwigluSrc<NB>, PartialDst>();
     });
     if (rc) return rc;
   }
@@ -1490,6 +1494,7 @@ int dz_ctx_create(dz_model* m, dz_ctx** out) {
       (rc = alloc_t(A, &x->p_gu, (size_t)th * ld_gu)) || (rc = alloc_t(A, &x->p_down, (size_t)tf * ld_h)) ||
       (rc = alloc_t(A, &x->y, (size_t)inner)) || (rc = alloc_t(A, &x->zs, (size_t)inner)) ||
       (rc = alloc_t(A, &x->apart, (size_t)c.n_head * x->gmax * (2 + c.head_dim))) ||
+      (rc = alloc_t(A, &x->attn_u, (size_t)c.n_head * c.head_dim)) ||
       (rc = alloc_t(A, &x->h_fin, (size_t)ld_h)) || (rc = alloc_t(A, &x->ss_fin, (size_t)th)) ||
       (rc = alloc_t(A, &x->logits, (size_t)m->lm_head.nrb * kRowBlock)) ||
       (rc = alloc_t(A, &x->am_val, (size_t)x->n_am)) || (rc = alloc_t(A, &x->am_idx, (size_t)x->n_am)) ||

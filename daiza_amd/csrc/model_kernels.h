@@ -214,52 +214,86 @@ struct GatedYSrc {
   }
 };
 
-// LUT input of the attention out-projection: combine the split-K softmax partials of the head
-// and gate with sigmoid (attention.rs:189-203).  Partial record: [m, l, o[head_dim]].
-template <int NP>
-struct AttnOutSrc {
+// Positions per chunk of the graph path's attention at context ctx with at most gmax chunks per kv
+// head: at least 64, four waves of one 16-position tile each.
+__device__ __forceinline__ int attn_chunk(int ctx, int gmax) {
+  const int c = (ctx + gmax - 1) / gmax;
+  return c < 64 ? 64 : c;
+}
+
+// The attention output of one token: combine the split-K softmax partials of each q-head and gate
+// with sigmoid (attention.rs:189-203), once, into u[n_head * hd] for the out-projection.  Partial
+// record: [m, l, o[hd]] per (head, chunk).  Workgroup (head, 64 dims), four waves: wave w sums
+// chunks [32w, 32w + 32) in chunk order with weights exp(m_g - M), M the maximum over all chunks
+// (every wave forms it from the (m, l) of all chunks); the four partial sums are then added in wave
+// order.  Every load is issued at the start: the o values do not depend on M.
+struct AttnMergeArgs {
   const float* apart;  // [n_head][gmax][2 + hd]
-  int gmax;
+  int gmax;            // <= 128
   int hd;
-  int64_t K;          // n_head * hd
   const TokState* st;
-  const float* p_in;  // qkv partials (gate half of each q-head)
+  const float* p_in;  // in-projection partials (gate half of each q-head)
   int np;
   int64_t ldp;
   const float* ss;
   int nss;
   int64_t H;
   float eps;
-  __device__ __forceinline__ void stage(float* xs, float*, int t, unsigned tid, int nt, int64_t) const {
-    const int ctx = st->pos + 1;
-    int chunk = (ctx + gmax - 1) / gmax;
-    if (chunk < 16) chunk = 16;
-    const int geff = (ctx + chunk - 1) / chunk;
-    const float inv = inv_rms_from(ss, nss, H, eps);
-    {  // one thread per tile column (nt == kTileCols)
-      const int i = (int)tid;
-      const int64_t col = (int64_t)t * kTileCols + i;
-      float u = 0.f;
-      if (col < K) {
-        const int h = (int)(col / hd), d = (int)(col % hd);
-        const float* rec = apart + (size_t)h * gmax * (2 + hd);
-        float M = -INFINITY;
-        for (int g = 0; g < geff; ++g) M = fmaxf(M, rec[(size_t)g * (2 + hd)]);
-        float l = 0.f, o = 0.f;
-        for (int g = 0; g < geff; ++g) {
-          const float* r = rec + (size_t)g * (2 + hd);
-          const float e = expf(r[0] - M);
-          l = __builtin_fmaf(r[1], e, l);
-          o = __builtin_fmaf(r[2 + d], e, o);
-        }
-        const int64_t grow = (int64_t)h * 2 * hd + hd + d;
-        const float gate = sum_strided<NP>(p_in, ldp, np, grow) * inv;
-        u = (o * (1.0f / l)) * sigmoidf_(gate);
-      }
-      xs[i] = u;
+  float* u;  // [n_head * hd]
+};
+
+template <int NP>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnMergeArgs a) {
+  __shared__ float wl[4][128][2];
+  __shared__ float part[4][2][64];
+  const unsigned tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const int dq = a.hd / 64;
+  const int h = blockIdx.x / dq, d = (blockIdx.x % dq) * 64 + (int)lane;
+  const int ctx = a.st->pos + 1;
+  const int chunk = attn_chunk(ctx, a.gmax);
+  const int geff = (ctx + chunk - 1) / chunk;
+  const size_t rs = (size_t)(2 + a.hd);
+  const float* rec = a.apart + (size_t)h * a.gmax * rs;
+  const int g0 = 32 * (int)w;
+  float o[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) o[k] = g0 + k < geff ? rec[(g0 + k) * rs + 2 + d] : 0.f;
+  float gate = 0.f;
+  if (w == 0) gate = sum_strided<NP>(a.p_in, a.ldp, a.np, (int64_t)h * 2 * a.hd + a.hd + d);
+  float mg[2], lg[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int g = (int)lane + 64 * k;
+    mg[k] = g < geff ? rec[g * rs] : -INFINITY;
+    lg[k] = g < geff ? rec[g * rs + 1] : 0.f;
+  }
+  const float M = wave_max(fmaxf(mg[0], mg[1]));
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int g = (int)lane + 64 * k;
+    wl[w][g][0] = g < geff ? expf(mg[k] - M) : 0.f;
+    wl[w][g][1] = lg[k];
+  }
+  __builtin_amdgcn_wave_barrier();
+  float L = 0.f, O = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    if (g0 + k < geff) {
+      const float e = wl[w][g0 + k][0];
+      L = __builtin_fmaf(wl[w][g0 + k][1], e, L);
+      O = __builtin_fmaf(o[k], e, O);
     }
   }
-};
+  part[w][0][lane] = L;
+  part[w][1][lane] = O;
+  __syncthreads();
+  if (w == 0) {
+    const float Lt = ((part[0][0][lane] + part[1][0][lane]) + part[2][0][lane]) + part[3][0][lane];
+    const float Ot = ((part[0][1][lane] + part[1][1][lane]) + part[2][1][lane]) + part[3][1][lane];
+    const float inv = inv_rms_from(a.ss, a.nss, a.H, a.eps);
+    a.u[(size_t)h * a.hd + d] = (Ot * (1.0f / Lt)) * sigmoidf_(gate * inv);
+  }
+}
 
 // LUT input (h * inv_rms) * w with h already final (output norm before lm_head, forward.rs:332).
 struct NormedSrc {
@@ -600,15 +634,45 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   __shared__ float red[GRP + 1][4];
   __shared__ float wm[4][GRP], wl[4][GRP];
   __shared__ float wo[4][GRP][HD];
+  __shared__ float ew[4][GRP][16];
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const int kvh = blockIdx.x / a.gmax, g = blockIdx.x % a.gmax;
   const int P = a.st->pos, ctx = P + 1;
-  int chunk = (ctx + a.gmax - 1) / a.gmax;
-  if (chunk < 16) chunk = 16;
+  const int chunk = attn_chunk(ctx, a.gmax);
   const int geff = (ctx + chunk - 1) / chunk;
   if (g >= geff) return;
   const int p0 = g * chunk, p1 = min(ctx, p0 + chunk);
   const bool has_new = p1 == ctx;
+  // K rows and V rows of the cache, global loads only (so that waiting on LDS reads never waits on
+  // them).  Tiles of 16 positions, wave w takes tiles w, w + 4, ...; the first tile's rows load
+  // before the prologue unless the tile holds the new position, whose rows this workgroup stores
+  // below (and reads after the barrier that follows).
+  const float* kb = a.kcache + (size_t)kvh * a.max_ctx * HD;
+  const float* vb = a.vcache + (size_t)kvh * a.max_ctx * HD;
+  const int pj = (int)(lane >> 2), qtr = (int)(lane & 3u);
+  constexpr int kT = 16;
+  const int ntile = (p1 - p0 + kT - 1) / kT;
+  float4 kk[16], vv[kT];
+  auto load_k = [&](int t) {
+    const int tp0 = p0 + kT * t;
+    const int row = tp0 + pj < p1 ? tp0 + pj : tp0;
+    const float4* kr = reinterpret_cast<const float4*>(kb + (size_t)row * HD) + qtr;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) kk[u] = kr[4 * u];  // the quad reads 64 contiguous bytes per step
+  };
+  auto load_v = [&](int t) {
+    const int tp0 = p0 + kT * t;
+    const int npos = min(kT, p1 - tp0);
+#pragma unroll
+    for (int j = 0; j < kT; ++j)
+      vv[j] = j < npos ? *reinterpret_cast<const float4*>(vb + (size_t)(tp0 + j) * HD + 4 * lane)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  const bool pre = (int)wave < ntile && p0 + kT * ((int)wave + 1) <= P;
+  if (pre) {
+    load_k((int)wave);
+    load_v((int)wave);
+  }
   const float inv = inv_rms_from(a.ss, a.nss, a.H, a.eps);
   const int half = a.rope_dim / 2;
   const float* cs = a.rope + (size_t)P * a.rope_dim;
@@ -686,57 +750,83 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   }
   __syncthreads();
 
-  // online softmax over this wave's positions; lane holds dims 4*lane .. 4*lane+3
+  // Online softmax over this wave's tiles.  Scores: the four lanes 4j .. 4j+3 hold position tp0 + j,
+  // lane 4j+r the float4 columns r, r+4, ..., r+60 of its K row; they dot them with the same
+  // columns of q (from LDS) and add the four within the quad; one softmax update per tile.
+  // Values: lane j holds dims 4j .. 4j+3 and sums the tile's V rows weighted by the exp-scores,
+  // read back from LDS.  The next tile's K rows load during this tile's softmax and values, its V
+  // rows during the next tile's scores.  l is kept per position lane (quarter 0) until the end.
   float m[GRP], l[GRP];
-  float4 o[GRP], q4[GRP];
+  float4 o[GRP];
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {
     m[gi] = -INFINITY;
     l[gi] = 0.f;
     o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
-    q4[gi] = *reinterpret_cast<const float4*>(&qs[gi][4 * lane]);
   }
-  const float* kb = a.kcache + (size_t)kvh * a.max_ctx * HD;
-  const float* vb = a.vcache + (size_t)kvh * a.max_ctx * HD;
-  auto loadkv = [&](int p, float4& k4, float4& v4) {
-    if (p == P) {
-      k4 = *reinterpret_cast<const float4*>(&kn[4 * lane]);
-      v4 = *reinterpret_cast<const float4*>(&vn[4 * lane]);
-    } else {
-      k4 = *reinterpret_cast<const float4*>(kb + (size_t)p * HD + 4 * lane);
-      v4 = *reinterpret_cast<const float4*>(vb + (size_t)p * HD + 4 * lane);
-    }
-  };
-  // software pipeline: positions p, p+4 and p+8 of this wave are in flight together
-  int p = p0 + (int)wave;
-  float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), va = ka, kb1 = ka, vb1 = ka;
-  if (p < p1) loadkv(p, ka, va);
-  if (p + 4 < p1) loadkv(p + 4, kb1, vb1);
-  for (; p < p1; p += 4) {
-    float4 kc = ka, vc = va;
-    if (p + 8 < p1) loadkv(p + 8, kc, vc);
-    const float4 k4 = ka, v4 = va;
-    ka = kb1;
-    va = vb1;
-    kb1 = kc;
-    vb1 = vc;
+  float(*es)[16] = ew[wave];
+  if ((int)wave < ntile && !pre) {
+    load_k((int)wave);
+    load_v((int)wave);
+  }
+  for (int t = (int)wave; t < ntile; t += 4) {
+    const int tp0 = p0 + kT * t;
+    const int npos = min(kT, p1 - tp0);
+    const bool valid = pj < npos;
+    float sc[GRP];
 #pragma unroll
     for (int gi = 0; gi < GRP; ++gi) {
-      float dp = q4[gi].x * k4.x;
-      dp = __builtin_fmaf(q4[gi].y, k4.y, dp);
-      dp = __builtin_fmaf(q4[gi].z, k4.z, dp);
-      dp = __builtin_fmaf(q4[gi].w, k4.w, dp);
-      const float score = wave_sum(dp);
-      const float mn = fmaxf(m[gi], score);
-      const float al = expf(m[gi] - mn), be = expf(score - mn);
-      l[gi] = l[gi] * al + be;
-      o[gi].x = __builtin_fmaf(be, v4.x, o[gi].x * al);
-      o[gi].y = __builtin_fmaf(be, v4.y, o[gi].y * al);
-      o[gi].z = __builtin_fmaf(be, v4.z, o[gi].z * al);
-      o[gi].w = __builtin_fmaf(be, v4.w, o[gi].w * al);
-      m[gi] = mn;
+      float d = 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float4 q = *reinterpret_cast<const float4*>(&qs[gi][16 * u + 4 * qtr]);
+        d = __builtin_fmaf(q.x, kk[u].x, d);
+        d = __builtin_fmaf(q.y, kk[u].y, d);
+        d = __builtin_fmaf(q.z, kk[u].z, d);
+        d = __builtin_fmaf(q.w, kk[u].w, d);
+      }
+      d = dpp_add<0xB1>(d);  // quad_perm [1,0,3,2]
+      sc[gi] = dpp_add<0x4E>(d);  // quad_perm [2,3,0,1]: every lane of the quad has the sum
     }
+    if (t + 4 < ntile) load_k(t + 4);
+#pragma unroll
+    for (int gi = 0; gi < GRP; ++gi) {
+      const float sv = valid ? sc[gi] : -INFINITY;
+      const float mn = fmaxf(m[gi], wave_max(sv));
+      const float al = expf(m[gi] - mn);
+      const float e = valid ? expf(sv - mn) : 0.f;
+      l[gi] = __builtin_fmaf(l[gi], al, qtr == 0 ? e : 0.f);
+      o[gi].x *= al;
+      o[gi].y *= al;
+      o[gi].z *= al;
+      o[gi].w *= al;
+      m[gi] = mn;
+      if (qtr == 0) es[gi][pj] = e;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j4 = 0; j4 < kT; j4 += 4) {
+      if (j4 < npos) {
+#pragma unroll
+        for (int gi = 0; gi < GRP; ++gi) {
+          const float4 e4 = *reinterpret_cast<const float4*>(&es[gi][j4]);
+          const float ee[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float4 v = vv[j4 + r];
+            o[gi].x = __builtin_fmaf(ee[r], v.x, o[gi].x);
+            o[gi].y = __builtin_fmaf(ee[r], v.y, o[gi].y);
+            o[gi].z = __builtin_fmaf(ee[r], v.z, o[gi].z);
+            o[gi].w = __builtin_fmaf(ee[r], v.w, o[gi].w);
+          }
+        }
+      }
+    }
+    if (t + 4 < ntile) load_v(t + 4);
+    __builtin_amdgcn_wave_barrier();
   }
+#pragma unroll
+  for (int gi = 0; gi < GRP; ++gi) l[gi] = wave_sum(l[gi]);
 #pragma unroll
   for (int gi = 0; gi < GRP; ++gi) {
     if (lane == 0) {

@@ -113,7 +113,7 @@ def test_deltanet_step(dz, oracle, full):
             h = ho
 
 
-@pytest.mark.parametrize("ctxlen", [1, 100, 4096, 32768])
+@pytest.mark.parametrize("ctxlen", [1, 100, 300, 4096, 5000, 32768])
 def test_attention_step(dz, oracle, ctxlen):
     # one gated attention step over an N(0,1) KV cache of length ctxlen
     cfg = dz.Config.bonsai27b(max_ctx=ctxlen + 8)

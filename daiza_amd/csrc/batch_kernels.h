@@ -462,11 +462,7 @@ __global__ __launch_bounds__(256) void bt_split_swiglu_kernel(const float* __res
   const int t = blockIdx.y;
   if (i >= F || t >= n) return;
   const size_t off = (size_t)t * 2 * F + i;
-  float g = part[off], u = part[off + F];
-  for (int z = 1; z < splits; ++z) {
-    g += part[(size_t)z * zstride + off];
-    u += part[(size_t)z * zstride + off + F];
-  }
+  const float g = ordered_sum(part + off, zstride, splits), u = ordered_sum(part + off + F, zstride, splits);
   s[(size_t)t * F + i] = siluf_(g) * u;
 }
 

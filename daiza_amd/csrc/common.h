@@ -58,6 +58,26 @@ struct Q1Dev {
   int64_t ntiles = 0;          // K tiles (cols padded to 512)
 };
 
+// p[0] + p[s] + p[2s] + ... + p[(n-1)s] (n >= 1), added in index order, with the loads issued 16 at a
+// time: a loop of dependent adds with a run-time count otherwise waits one memory round trip per term.
+__device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_t stride, int n) {
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) v[k] = k < n ? p[(size_t)k * stride] : 0.f;
+  float acc = v[0];
+#pragma unroll
+  for (int k = 1; k < 16; ++k)
+    if (k < n) acc += v[k];
+  for (int b = 16; b < n; b += 16) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = b + k < n ? p[(size_t)(b + k) * stride] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (b + k < n) acc += v[k];
+  }
+  return acc;
+}
+
 }  // namespace dz
 
 #define DZ_HIP_CHECK(expr)                                                     \

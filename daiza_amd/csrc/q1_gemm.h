@@ -365,8 +365,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
   const int n = blockIdx.y;
   if (row >= rows || n >= n_tok) return;
   const size_t off = (size_t)n * rows + row;
-  float v = part[off];
-  for (int z = 1; z < splits; ++z) v += part[(size_t)z * zstride + off];
+  const float v = ordered_sum(part + off, zstride, splits);
   float* yr = y + (size_t)n * ldy + row;
   *yr = accumulate ? *yr + v : v;
 }

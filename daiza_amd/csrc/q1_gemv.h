@@ -128,9 +128,11 @@ __device__ __forceinline__ void build_lut(float* __restrict__ lut, const float* 
   constexpr int KB = (PER == 64) ? 6 : (PER == 32) ? 5 : (PER == 16) ? 4 : 7;
   static_assert(PER == (1 << KB), "threads per workgroup must be 128, 256, 512 or 1024");
   const unsigned p = tid & 63, hi = tid >> 6;
-  float x[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) x[j] = xs[8 * p + j];
+  // the position's 8 inputs as two 16-byte reads: eight 4-byte reads xs[8p + j] would put the 64
+  // lanes on 4 of the 32 banks (a 16-way conflict per read, serialised across the workgroup's waves)
+  const float4 xa = *reinterpret_cast<const float4*>(xs + 8 * p);
+  const float4 xb = *reinterpret_cast<const float4*>(xs + 8 * p + 4);
+  const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
   float C = 0.f;
 #pragma unroll
   for (int j = KB; j < 8; ++j) C += ((hi >> (j - KB)) & 1u) ? x[j] : -x[j];

@@ -175,8 +175,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const ReduceArgs a)
   while (s + 1 < a.nseg && v >= a.seg[s + 1].vrow_begin) ++s;
   const int64_t r = v - a.seg[s].vrow_begin;
   if (r < 0 || r >= a.seg[s].rows) return;
-  float acc = a.part[v];
-  for (int tg = 1; tg < a.n_tg; ++tg) acc += a.part[(size_t)tg * a.ld + v];
+  const float acc = ordered_sum(a.part + v, a.ld, a.n_tg);
   float* y = a.seg[s].y + r;
   *y = a.accumulate ? *y + acc : acc;
 }

@@ -149,6 +149,7 @@ _MODEL_PROTOS = {
     "dz_ctx_mixer_step": ([_vp, ctypes.c_int, _f32p], ctypes.c_int),
     "dz_ctx_mixer_step_dev": ([_vp, ctypes.c_int, _vp, _vp], ctypes.c_int),
     "dz_ctx_stream": ([_vp], _vp),
+    "dz_ctx_copy_state": ([_vp, _vp], ctypes.c_int),
     "dz_session_cfg_hash": ([_vp, ctypes.c_uint64], ctypes.c_uint64),
     "dz_ctx_save": ([_vp, ctypes.c_char_p, ctypes.c_uint64, _u32p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_char_p],
                     ctypes.c_int),
@@ -528,6 +529,11 @@ class Context:
     def kv_truncate(self, n):
         """KvCache::truncate (kv_cache.rs:119-130): keeps n cached positions, pos = n; conv rings stay."""
         _check(lib().dz_kv_truncate(self._h, int(n)))
+
+    def copy_state_from(self, src):
+        """ModelState::clone onto this context (dz_ctx_copy_state): checkpoint into a spare context,
+        restore by copying back."""
+        _check(lib().dz_ctx_copy_state(self._h, src._h))
 
     def save(self, path, history=(), think_enabled=False, system_prompt=None, context_length=CONTEXT_LENGTH):
         """Session::save_to_disk (session_persist.rs:70-146): the DZSS v1 file of this context's state,

@@ -1783,6 +1783,57 @@ int dz_ctx_set_pos(dz_ctx* x, int pos) {
   return ctx_move_pos(x, pos);
 }
 
+// ModelState::clone (forward.rs:31-77, derive(Clone); session_persist.rs:159 clones it for the
+// background save) onto another context: dst takes src's position, DeltaNet states, conv rings and
+// ring heads, the cached K/V rows [0, pos), the token log, and the last forward's logits and argmax
+// candidates.  The two contexts may belong to different models of the same shape (max_ctx may
+// differ if src's position fits dst's).
+int dz_ctx_copy_state(dz_ctx* dst, const dz_ctx* src) {
+  if (!dst || !src) return set_error(DZ_ERR_MODEL, "null context");
+  if (dst == src) return DZ_OK;
+  const dz_config &a = dst->m->cfg, &b = src->m->cfg;
+  const bool same = a.n_layers == b.n_layers && a.hidden == b.hidden && a.ffn == b.ffn && a.vocab == b.vocab &&
+                    a.n_head == b.n_head && a.n_head_kv == b.n_head_kv && a.head_dim == b.head_dim &&
+                    a.rope_dim == b.rope_dim && a.rope_base == b.rope_base && a.rms_eps == b.rms_eps &&
+                    a.full_attn_interval == b.full_attn_interval && a.ssm_conv_kernel == b.ssm_conv_kernel &&
+                    a.ssm_state == b.ssm_state && a.ssm_k_heads == b.ssm_k_heads && a.ssm_v_heads == b.ssm_v_heads;
+  if (!same) return set_error(DZ_ERR_MODEL, "copy_state: the contexts' model shapes differ");
+  const int pos = src->pos_host;
+  if (pos > a.max_ctx) return set_error(DZ_ERR_TENSOR, "copy_state: position %d exceeds max_ctx %d", pos, a.max_ctx);
+  DZ_HIP_CHECK(hipStreamSynchronize(src->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(dst->s));
+  dst->bt.pending = 0;
+  const int64_t hd = a.ssm_state, qkvd = (2 * (int64_t)a.ssm_k_heads + a.ssm_v_heads) * hd;
+  hipStream_t s = dst->s;
+  const int n_ssm = dst->m->n_ssm, n_attn = dst->m->n_attn;
+  if (n_ssm) {
+    DZ_HIP_CHECK(hipMemcpyAsync(dst->ssm_state, src->ssm_state, (size_t)n_ssm * a.ssm_v_heads * hd * hd * 4,
+                                hipMemcpyDeviceToDevice, s));
+    DZ_HIP_CHECK(hipMemcpyAsync(dst->conv, src->conv, (size_t)n_ssm * 4 * qkvd * 4, hipMemcpyDeviceToDevice, s));
+    DZ_HIP_CHECK(hipMemcpyAsync(dst->ring_base_dev, src->ring_base_dev, (size_t)n_ssm * 4, hipMemcpyDeviceToDevice, s));
+  }
+  if (n_attn && pos) {
+    // rows [0, pos) of every (layer, K|V, kv head) block; each context strides by its own max_ctx
+    const size_t row = (size_t)a.head_dim * 4;
+    DZ_HIP_CHECK(hipMemcpy2DAsync(dst->kv, (size_t)a.max_ctx * row, src->kv, (size_t)b.max_ctx * row, (size_t)pos * row,
+                                  (size_t)n_attn * 2 * a.n_head_kv, hipMemcpyDeviceToDevice, s));
+  }
+  DZ_HIP_CHECK(hipMemcpyAsync(dst->toklog, src->toklog, (size_t)(pos + 1) * 4, hipMemcpyDeviceToDevice, s));
+  DZ_HIP_CHECK(hipMemcpyAsync(dst->logits, src->logits, (size_t)a.vocab * 4, hipMemcpyDeviceToDevice, s));
+  DZ_HIP_CHECK(hipMemcpyAsync(dst->am_val, src->am_val, (size_t)dst->n_am * 4, hipMemcpyDeviceToDevice, s));
+  DZ_HIP_CHECK(hipMemcpyAsync(dst->am_idx, src->am_idx, (size_t)dst->n_am * 4, hipMemcpyDeviceToDevice, s));
+  TokState st;
+  DZ_HIP_CHECK(hipMemcpy(&st, src->st, sizeof st, hipMemcpyDeviceToHost));
+  st.feed_len = 0;  // host-fed ids belong to a call in progress, not to the state
+  st.feed_idx = 0;
+  DZ_HIP_CHECK(hipMemcpyAsync(dst->st, &st, sizeof st, hipMemcpyHostToDevice, s));
+  DZ_HIP_CHECK(hipStreamSynchronize(s));
+  dst->ring_base = src->ring_base;
+  dst->pos_host = pos;
+  dst->poisoned = src->poisoned;
+  return DZ_OK;
+}
+
 }  // extern "C"
 
 namespace dz {

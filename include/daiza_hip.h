@@ -316,6 +316,17 @@ int dz_ctx_load(dz_ctx* c, const char* path, uint64_t context_length, uint32_t* 
                 uint64_t* n_history, int32_t* think_enabled, char* system_prompt, uint64_t prompt_cap,
                 uint64_t* prompt_len);
 
+/*
+ * ModelState::clone (Daiza-engine/src/model/forward.rs:31-77, derive(Clone); the reference clones it
+ * for Session::save_to_disk_async, Daiza-runtime/src/session_persist.rs:153-186) between contexts:
+ * dst takes src's position, DeltaNet states, conv rings, cached K/V rows [0, pos), token log and the
+ * last forward's logits; src is unchanged.  This is the checkpoint/restore of a context: copy into a
+ * spare context of the same model to checkpoint, copy back to restore.  The models must have the same
+ * shape (DZ_ERR_MODEL otherwise); src's position must fit dst's max_ctx (DZ_ERR_TENSOR).  A pending
+ * dz_verify_forward on dst is dropped; src's refusal after a failed launch is copied with its state.
+ */
+int dz_ctx_copy_state(dz_ctx* dst, const dz_ctx* src);
+
 /* The context's HIP stream (hipStream_t), for callers that time or order work around it. */
 void* dz_ctx_stream(dz_ctx* c);
 

@@ -1,7 +1,8 @@
 """GPU tests of the boundary's state handling: the real-weights entry (dz_model_create with GGUF
 names, both token-embedding formats), the argmax tie rule across lm_head workgroups, KV truncation
-(KvCache::truncate keeps every conv ring where it is), the greedy loop's EOS stop, and the refusal of
-a context whose launch gave up part-way.  Oracle: oracle/oracle.c (the reference's algorithm).
+(KvCache::truncate keeps every conv ring where it is), the greedy loop's EOS stop, the refusal of a
+context whose launch gave up part-way, and state copies between contexts (checkpoint / restore).
+Oracle: oracle/oracle.c (the reference's algorithm).
 """
 import numpy as np
 import pytest
@@ -227,3 +228,86 @@ def test_model_from_gguf_file(dz, oracle, tmp_path, embd_f16):
         ao, lo = om.forward(t)
         assert np.array_equal(l1, l2), t
         assert normwise_rel(l1, lo) < 1e-3 and a1 == a2 == ao, t
+
+
+def test_copy_state_checkpoint_restore(dz, oracle, launch_path):
+    """ModelState::clone through dz_ctx_copy_state: a checkpoint taken into a spare context after a
+    prefill and 4 greedy tokens; the original runs 5 more tokens, is restored from the checkpoint and
+    runs the same 5 again with bit-identical logits; the checkpoint's own continuation agrees, and the
+    oracle given the same tokens agrees within 1e-3."""
+    cfg = dz.Config.small(n_layers=8, max_ctx=96)
+    m = dz.Model.synthetic(cfg, SEED + 5)
+    a = dz.Context(m)
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, cfg.vocab, 10)]
+    lg = a.forward_batch(np.array(prompt, np.uint32))
+    first = int(np.argmax(lg))
+    toks = [int(t) for t in a.decode_greedy(first, 4)]
+    slot = dz.Context(m)
+    slot.forward_batch(np.array([1, 2, 3], np.uint32))  # some other state, replaced by the copy
+    slot.copy_state_from(a)
+    assert slot.pos == a.pos == 14
+    assert np.array_equal(slot.logits(), a.logits())
+    for l in range(cfg.n_layers):
+        if cfg.is_full_attention(l):
+            ka, va = a.get_kv(l, a.pos)
+            ks, vs = slot.get_kv(l, slot.pos)
+            assert np.array_equal(ka, ks) and np.array_equal(va, vs)
+        else:
+            sa, ca, ha = a.get_ssm_state(l)
+            ss, cs, hs = slot.get_ssm_state(l)
+            assert np.array_equal(sa, ss) and np.array_equal(ca, cs) and ha == hs
+
+    def run(ctx, n=5):
+        out, t = [], toks[-1]
+        for _ in range(n):
+            t, lgt = ctx.forward_single_token(t)
+            out.append(lgt)
+        return out
+
+    cont = run(a)
+    a.copy_state_from(slot)  # restore
+    assert a.pos == 14
+    again = run(a)
+    from_slot = run(slot)
+    for i in range(5):
+        assert np.array_equal(again[i], cont[i]) and np.array_equal(from_slot[i], cont[i]), i
+    om = oracle.Model(cfg, SEED + 5)
+    for t in prompt + [first] + toks[:-1]:
+        om.forward(t)
+    _, olg = om.forward(toks[-1])
+    assert normwise_rel(cont[0], olg) < 1e-3
+
+
+def test_copy_state_across_shapes_and_paths(dz, oracle, monkeypatch):
+    """A copy into a context with a larger max_ctx, from the token kernel to the per-kernel graph
+    path, continues like the source; copies between different model shapes, or of a position that
+    does not fit the destination, are refused and leave the destination unchanged."""
+    cfg = dz.Config.small(n_layers=4, max_ctx=64)
+    m = dz.Model.synthetic(cfg, SEED + 6)
+    a = dz.Context(m)
+    assert a.token_kernel
+    a.forward_batch(np.array([7, 8, 9, 10, 11], np.uint32))
+    big = dz.Config.small(n_layers=4, max_ctx=128)
+    monkeypatch.setenv("DAIZA_PTK", "0")
+    mb = dz.Model.synthetic(big, SEED + 6)  # the same weights, a longer cache
+    b = dz.Context(mb)
+    monkeypatch.delenv("DAIZA_PTK")
+    assert not b.token_kernel
+    b.copy_state_from(a)
+    assert b.pos == 5
+    ta, la = a.forward_single_token(12)
+    tb, lb = b.forward_single_token(12)
+    assert ta == tb and normwise_rel(lb, la) < 1e-5
+    # refusals
+    other = dz.Context(dz.Model.synthetic(dz.Config.small(n_layers=8, max_ctx=64), SEED))
+    with pytest.raises(dz.DaizaError) as e:
+        other.copy_state_from(a)
+    assert e.value.code == dz.DZ_ERR_MODEL
+    small = dz.Context(dz.Model.synthetic(dz.Config.small(n_layers=4, max_ctx=8), SEED))
+    small.forward_single_token(3)
+    long_ctx = dz.Context(m)
+    long_ctx.forward_batch(np.arange(20, dtype=np.uint32))
+    with pytest.raises(dz.DaizaError) as e:
+        small.copy_state_from(long_ctx)
+    assert e.value.code == dz.DZ_ERR_TENSOR
+    assert small.pos == 1

@@ -494,7 +494,7 @@ static int launch_attention(int grp, dim3 grid, const AttnArgs& a, hipStream_t s
 // DeltaNet or attention kernel, then the out-projection GEMV into p_o.  `h_mid` receives the
 // materialised layer input with its tile sums of squares in `ss_mid`.
 static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* parts, int np, int64_t ldp, float* h_mid,
-                         float* ss_mid, hipStream_t s) {
+                         float* ss_mid, hipStream_t s, int pos = -1) {
   dz_model* m = x->m;
   const dz_config& c = m->cfg;
   LayerDev& l = m->L[li];
@@ -515,6 +515,7 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
   if (!l.attn) {
     DeltaArgs a;
     a.st = x->st;
+    a.pos = pos;
     a.p_in = x->p_in;
     a.np = nin;
     a.ldp = ld_l;
@@ -548,6 +549,7 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
   } else {
     AttnArgs a;
     a.st = x->st;
+    a.pos = pos;
     a.p_in = x->p_in;
     a.np = nin;
     a.ldp = ld_l;
@@ -569,7 +571,7 @@ static int enqueue_mixer(dz_ctx* x, int li, const float* h_in, const float* part
     a.nkv = c.n_head_kv;
     if ((rc = launch_attention(c.n_head / c.n_head_kv, dim3((unsigned)(c.n_head_kv * x->gmax)), a, s))) return rc;
     // merge the chunks and gate once, then the out-projection reads the result as a plain vector
-    AttnMergeArgs ma{x->apart, x->gmax, c.head_dim, x->st, x->p_in, nin, ld_l, ss_mid, th, H, c.rms_eps, x->attn_u};
+    AttnMergeArgs ma{x->apart, x->gmax, c.head_dim, x->st, pos, x->p_in, nin, ld_l, ss_mid, th, H, c.rms_eps, x->attn_u};
     rc = with_np_bucket(nin, [&](auto B) -> int {
       hipLaunchKernelGGL(attn_merge_kernel<decltype(B)::value>, dim3((unsigned)(c.n_head * (c.head_dim / 64))),
                          dim3(256), 0, s, ma);
@@ -1834,19 +1836,6 @@ int dz_ctx_copy_state(dz_ctx* dst, const dz_ctx* src) {
   return DZ_OK;
 }
 
-}  // extern "C"
-
-namespace dz {
-// TokState.pos = pos (the token being run), pos_next = pos + 1, enqueued on the stream.
-__global__ void set_tok_pos_kernel(TokState* st, int pos) {
-  if (threadIdx.x == 0) {
-    st->pos = pos;
-    st->pos_next = pos + 1;
-  }
-}
-}  // namespace dz
-
-extern "C" {
 
 int dz_ctx_mixer_step_dev(dz_ctx* x, int layer, const float* h_dev, float* h_out_dev) {
   if (!x || !h_dev || !h_out_dev) return set_error(DZ_ERR_MODEL, "null argument");
@@ -1859,19 +1848,18 @@ int dz_ctx_mixer_step_dev(dz_ctx* x, int layer, const float* h_dev, float* h_out
   ctx_dims(x->m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
   const int P = x->pos_host;
   x->bt.pending = 0;
-  hipLaunchKernelGGL(set_tok_pos_kernel, dim3(1), dim3(64), 0, x->s, x->st, P);
-  DZ_HIP_CHECK(hipGetLastError());
-  DZ_HIP_CHECK(hipMemcpyAsync(x->h[1], h_dev, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice, x->s));
-  int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s);
+  // the kernels take the position as an argument and read the caller's h directly; the residual
+  // kernel writes the caller's output (which may be h itself: every read of h is in the first kernel)
+  // and leaves TokState at this token (pos P, pos_next P + 1)
+  int rc = enqueue_mixer(x, layer, h_dev, nullptr, 0, ld_h, x->h[0], x->ss[0], x->s, P);
   if (rc) return rc;
-  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden};
+  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, h_out_dev, x->ss_fin, c.hidden, x->st, P};
   rc = with_np_bucket(fa.np, [&](auto B) -> int {
     hipLaunchKernelGGL(final_reduce_kernel<decltype(B)::value>, dim3((unsigned)th), dim3(512), 0, x->s, fa);
     DZ_HIP_CHECK(hipGetLastError());
     return DZ_OK;
   });
   if (rc) return rc;
-  DZ_HIP_CHECK(hipMemcpyAsync(h_out_dev, x->h_fin, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice, x->s));
   x->pos_host = P + 1;
   return DZ_OK;
 }
@@ -1886,13 +1874,11 @@ int dz_ctx_mixer_step(dz_ctx* x, int layer, float* h) {
   int th, to, tf;
   ctx_dims(x->m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
   const int P = x->pos_host;
-  // this token's position: TokState.pos = P, pos_next = P + 1
-  int pp[1] = {P};
-  DZ_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos), pp, 4, hipMemcpyHostToDevice, x->s));
   DZ_HIP_CHECK(hipMemcpyAsync(x->h[1], h, (size_t)c.hidden * 4, hipMemcpyHostToDevice, x->s));
-  int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s);
+  int rc = enqueue_mixer(x, layer, x->h[1], nullptr, 0, ld_h, x->h[0], x->ss[0], x->s, P);
   if (rc) return rc;
-  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden};
+  // the residual kernel leaves TokState at this token (pos P, pos_next P + 1)
+  FinalArgs fa{x->h[0], x->p_o, (int)x->m->L[layer].out_proj.ntiles, ld_h, x->h_fin, x->ss_fin, c.hidden, x->st, P};
   rc = with_np_bucket(fa.np, [&](auto B) -> int {
     hipLaunchKernelGGL(final_reduce_kernel<decltype(B)::value>, dim3((unsigned)th), dim3(512), 0, x->s, fa);
     DZ_HIP_CHECK(hipGetLastError());

@@ -232,6 +232,7 @@ struct AttnMergeArgs {
   int gmax;            // <= 128
   int hd;
   const TokState* st;
+  int pos;            // this token's position, or -1: TokState.pos
   const float* p_in;  // in-projection partials (gate half of each q-head)
   int np;
   int64_t ldp;
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnMergeArgs a) 
   const unsigned tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   const int dq = a.hd / 64;
   const int h = blockIdx.x / dq, d = (blockIdx.x % dq) * 64 + (int)lane;
-  const int ctx = a.st->pos + 1;
+  const int ctx = (a.pos >= 0 ? a.pos : a.st->pos) + 1;
   const int chunk = attn_chunk(ctx, a.gmax);
   const int geff = (ctx + chunk - 1) / chunk;
   const size_t rs = (size_t)(2 + a.hd);
@@ -453,6 +454,7 @@ __global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) 
 
 struct DeltaArgs {
   const TokState* st;
+  int pos;            // this token's position, or -1: TokState.pos (replays of the captured token graph)
   const float* p_in;  // in-proj partials [np][ldp]: rows [qkv | z | alpha | beta]
   int np;
   int64_t ldp;
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
   const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % a.nkh;
   const int i_loc = tid & 31, js = tid >> 5;
   const int i = quarter * 32 + i_loc;
-  const int pos = a.st->pos;
+  const int pos = a.pos >= 0 ? a.pos : a.st->pos;
   const int hb = (*a.ring_base_ptr + pos) & 3;  // ring head before this token = slot of the new value
   const int64_t kdim = (int64_t)a.nkh * HD;
   const int64_t qkvd = a.qkvd;
@@ -601,6 +603,7 @@ __global__ __launch_bounds__(256) void deltanet_kernel(const DeltaArgs a) {
 
 struct AttnArgs {
   const TokState* st;
+  int pos;            // this token's position, or -1: TokState.pos (replays of the captured token graph)
   const float* p_in;  // qkv partials: rows [q+gate interleaved per head (n_head*2*hd) | k | v]
   int np;
   int64_t ldp;
@@ -637,7 +640,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const AttnArgs a) {
   __shared__ float ew[4][GRP][16];
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const int kvh = blockIdx.x / a.gmax, g = blockIdx.x % a.gmax;
-  const int P = a.st->pos, ctx = P + 1;
+  const int P = a.pos >= 0 ? a.pos : a.st->pos, ctx = P + 1;
   const int chunk = attn_chunk(ctx, a.gmax);
   const int geff = (ctx + chunk - 1) / chunk;
   if (g >= geff) return;
@@ -865,6 +868,8 @@ struct FinalArgs {
   float* h_out;
   float* ss_out;
   int64_t H;
+  TokState* st = nullptr;  // when set, TokState.pos / pos_next become pos / pos + 1 (a direct mixer step)
+  int pos = 0;
 };
 
 template <int NP>
@@ -881,6 +886,10 @@ __global__ __launch_bounds__(512) void final_reduce_kernel(const FinalArgs a) {
   }
   const float s = block_sum(v * v, red, tid, 512);
   if (tid == 0) a.ss_out[t] = s;
+  if (a.st && t == 0 && tid == 0) {
+    a.st->pos = a.pos;
+    a.st->pos_next = a.pos + 1;
+  }
 }
 
 }  // namespace dz

@@ -241,6 +241,112 @@ __global__ __launch_bounds__(NWAVES * 64) void gemv_lut_kernel(const GemvGrid g,
     if (ok[m]) dst.store(tg, rb[m], lane, acc[m]);
 }
 
+// Output of one stacked matrix: rows [vrow_begin, vrow_begin + rows) of the virtual row space.
+struct ReduceSeg {
+  float* y;
+  int64_t vrow_begin;  // first virtual row of the segment
+  int64_t rows;        // logical rows
+};
+
+// ---- one-launch y = W x: split-K partials and their tile sum in the same kernel ----
+//
+// Workgroup (chunk, tile t) of the grid above with one tile per workgroup and one row-block per
+// wave: the same staging, table and lookups as gemv_lut_kernel.  The tile's partial of every row
+// goes out as a 64-bit word {f32 value, 32-bit call tag}, written through to the device coherence
+// point.  The workgroup of the chunk's last tile then forms the chunk's rows (thread = row, the row
+// whose partial it computed itself), y[row] = [y[row] +] sum_t part[t][row] in tile order (the
+// order of partial_reduce_kernel), polling each word until it carries this call's tag: readiness
+// travels with the data, so no fence, counter or barrier is involved.  The summing workgroup waits
+// only for workgroups of lower index; the host launches this kernel only when the whole grid is
+// resident at once, so all of them run.  A poll that never completes (bounded) leaves NaN in the row.
+struct FusedGemvArgs {
+  GemvGrid g;                  // tpw == 1, rbw == NWAVES
+  const float* x;
+  int64_t K;
+  unsigned long long* part;    // [n_tg][ld] tagged words
+  int64_t ld;
+  unsigned tag;                // this call's tag (never 0: the buffer starts zeroed)
+  int accumulate;
+  int spin_limit;
+  ReduceSeg seg[8];            // output of each stacked matrix
+};
+
+template <int NWAVES>
+__global__ __launch_bounds__(NWAVES * 64) void gemv_fused_kernel(const FusedGemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* lut = reinterpret_cast<float*>(smem);
+  float* xs = reinterpret_cast<float*>(smem + kLutBytes + 64);
+  constexpr int NT = NWAVES * 64;
+  static_assert(NT == kTileCols, "staging runs one thread per tile column");
+  typedef __attribute__((address_space(1))) unsigned long long gu64;
+  const GemvGrid& g = a.g;
+  const unsigned tid = threadIdx.x, lane = tid & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = (int)(blockIdx.x % (unsigned)g.n_tg);
+  const int64_t chunk = blockIdx.x / (unsigned)g.n_tg;
+  // the tile's inputs are staged before the weights are requested: the CU returns loads in issue
+  // order, and inputs queued behind the weights would hold the table back until the weights arrive
+  const int64_t col = (int64_t)t * kTileCols + tid;
+  xs[tid] = col < a.K ? a.x[col] : 0.f;
+  lds_barrier();
+  const int64_t rb = chunk * NWAVES + wave;
+  const bool ok = rb < g.total_rb;
+  UnitRegs cur;
+  if (ok) load_unit(unit_ptr(g, rb, t), lane, cur);
+  unsigned c[16];
+  make_pos_consts(lane, c);
+  build_lut<NT>(lut, xs, tid);
+  lds_barrier();
+  const float acc = ok ? unit_dot(cur, c) : 0.f;
+  if (ok)
+    __hip_atomic_store((gu64*)(a.part + (size_t)t * a.ld + rb * kRowBlock + lane),
+                       ((unsigned long long)a.tag << 32) | (unsigned long long)__float_as_uint(acc), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  if (t != g.n_tg - 1) return;
+  // the chunk's rows: thread tid sums row chunk*NT + tid over the tiles
+  const int64_t v = chunk * NT + tid;
+  if (v >= g.total_rb * kRowBlock) return;
+  const gu64* p = (const gu64*)(a.part + v);
+  float sum = 0.f;
+  bool good = true;
+  for (int b = 0; b < g.n_tg && good; b += 16) {
+    unsigned long long w[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int tt = b + k;
+      // this thread's own partial (the last tile) is in a register
+      w[k] = tt < g.n_tg - 1 ? __hip_atomic_load(p + (size_t)tt * a.ld, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : ((unsigned long long)a.tag << 32) | (unsigned long long)__float_as_uint(acc);
+    }
+    for (int spin = 0;; ++spin) {
+      bool all = true;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) all &= (unsigned)(w[k] >> 32) == a.tag;
+      if (all) break;
+      if (spin >= a.spin_limit) {
+        good = false;
+        break;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if ((unsigned)(w[k] >> 32) != a.tag)
+          w[k] = __hip_atomic_load(p + (size_t)(b + k) * a.ld, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float pv = __uint_as_float((unsigned)w[k]);
+      if (b + k == 0) sum = pv;
+      else if (b + k < g.n_tg) sum += pv;
+    }
+  }
+  int s = 0;
+  while (s + 1 < g.nseg && v >= a.seg[s + 1].vrow_begin) ++s;
+  const int64_t r = v - a.seg[s].vrow_begin;
+  if (r >= a.seg[s].rows) return;
+  float* y = a.seg[s].y + r;
+  *y = !good ? __builtin_nanf("") : (a.accumulate ? *y + sum : sum);
+}
+
 // ---- common sources / destinations ----
 
 struct PlainSrc {  // x[K] in device memory, zero beyond K

@@ -397,16 +397,71 @@ static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* co
     if ((rc = g_part.reserve(need * sizeof(float)))) return rc;
     part = static_cast<float*>(g_part.ptr);
   }
-  PlainSrc src{x_dev, mats[0]->d.cols};
-  PartialDst dst{part, p.ld};
-  DZ_HIP_CHECK(launch_gemv(p, src, dst, s));
   ReduceSeg segs[8];
   for (int i = 0; i < n; ++i) {
     segs[i].y = y_dev[i];
     segs[i].vrow_begin = p.g.seg[i].rb_begin * kRowBlock;
     segs[i].rows = mats[i]->d.rows;
   }
+  PlainSrc src{x_dev, mats[0]->d.cols};
+  PartialDst dst{part, p.ld};
+  DZ_HIP_CHECK(launch_gemv(p, src, dst, s));
   DZ_HIP_CHECK(launch_partial_reduce(part, p.ld, p.g.n_tg, segs, n, accumulate, s));
+  return DZ_OK;
+}
+
+// The tagged partials of the one-launch product (gemv_fused_kernel).  The buffer starts zeroed and
+// tags grow by one per call; it is cleared again before a tag would wrap.
+static Scratch g_tpart;
+static unsigned g_tag = 0;
+static int g_fused_cap = -1;  // workgroups of gemv_fused_kernel resident at once on the device
+
+// y = W x in one launch when the whole grid is resident at once (its summing workgroups wait for
+// workgroups of lower index); otherwise the split-K kernel and the tile-sum kernel.
+static int matvec_fused(dz_mat* const* mats, int n, const float* x_dev, float* const* y_dev, int accumulate,
+                        hipStream_t s) {
+  constexpr size_t shmem = (size_t)kLutBytes + 64 + kTileCols * 4;
+  const void* kfn = (const void*)gemv_fused_kernel<kGemvWaves>;
+  if (g_fused_cap < 0) {
+    DZ_HIP_CHECK(hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+    int dev = 0, occ = 0;
+    hipDeviceProp_t prop;
+    DZ_HIP_CHECK(hipGetDevice(&dev));
+    DZ_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+    DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kGemvWaves * 64, shmem));
+    g_fused_cap = occ * prop.multiProcessorCount;
+  }
+  const Q1Dev* ds[8];
+  for (int i = 0; i < n; ++i) ds[i] = &mats[i]->d;
+  GemvPlan p;
+  int rc = plan_gemv(ds, n, 1, &p);
+  if (rc) return rc;
+  if ((int64_t)p.nwg > g_fused_cap) return matvec_impl(mats, n, x_dev, y_dev, accumulate, s);
+  std::lock_guard<std::mutex> lk(g_mu);
+  const size_t words = (size_t)p.g.n_tg * (size_t)p.ld;
+  const size_t pb = g_tpart.bytes;
+  if ((rc = g_tpart.reserve(words * 8))) return rc;
+  if (g_tpart.bytes != pb || g_tag == 0xFFFFFFFFu) {
+    DZ_HIP_CHECK(hipMemsetAsync(g_tpart.ptr, 0, g_tpart.bytes, s));
+    g_tag = 0;
+  }
+  FusedGemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.g = p.g;
+  a.x = x_dev;
+  a.K = mats[0]->d.cols;
+  a.part = static_cast<unsigned long long*>(g_tpart.ptr);
+  a.ld = p.ld;
+  a.tag = ++g_tag;
+  a.accumulate = accumulate;
+  a.spin_limit = 1 << 20;
+  for (int i = 0; i < n; ++i) {
+    a.seg[i].y = y_dev[i];
+    a.seg[i].vrow_begin = p.g.seg[i].rb_begin * kRowBlock;
+    a.seg[i].rows = mats[i]->d.rows;
+  }
+  hipLaunchKernelGGL(gemv_fused_kernel<kGemvWaves>, dim3(p.nwg), dim3(kGemvWaves * 64), shmem, s, a);
+  DZ_HIP_CHECK(hipGetLastError());
   return DZ_OK;
 }
 
@@ -480,7 +535,7 @@ int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumula
   if (rc) return rc;
   dz_mat* ms[1] = {m};
   float* ys[1] = {y_dev};
-  return matvec_impl(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
+  return matvec_fused(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
 }
 
 int dz_q1_0_matvec_dev_noalloc(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream) {
@@ -542,7 +597,7 @@ static int matvec_host(dz_mat* const* mats, int n, const float* x, float* const*
       DZ_HIP_CHECK(hipMemcpyAsync(ydev[i], ys[i], (size_t)mats[i]->d.rows * 4, hipMemcpyHostToDevice, s));
     off += (size_t)mats[i]->d.rows;
   }
-  rc = matvec_impl(mats, n, static_cast<const float*>(g_x.ptr), ydev, accumulate, s);
+  rc = matvec_fused(mats, n, static_cast<const float*>(g_x.ptr), ydev, accumulate, s);
   if (rc) return rc;
   for (int i = 0; i < n; ++i)
     DZ_HIP_CHECK(hipMemcpyAsync(ys[i], ydev[i], (size_t)mats[i]->d.rows * 4, hipMemcpyDeviceToHost, s));

@@ -53,11 +53,6 @@ int prepare_gemv_kernels();
 const dz_config* ctx_config(const dz_ctx* x);
 
 // Sum of the tile-group partials into each segment's output: y = [y +] sum_tg part[tg][row].
-struct ReduceSeg {
-  float* y;
-  int64_t vrow_begin;  // first virtual row of the segment
-  int64_t rows;        // logical rows
-};
 hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const ReduceSeg* segs, int nseg,
                                  int accumulate, hipStream_t s);
 

@@ -279,130 +279,151 @@ __global__ __launch_bounds__(256) void bt_attn_prep_kernel(const float* __restri
   }
 }
 
-// Causal GQA attention of token t (position pos0 + t) over cache positions [0, pos0 + t] for the
-// GRP q-heads of kv-head kvh (online softmax, attention.rs:149-199), then o·sigmoid(gate)
-// (attention.rs:202-203) -> ao[t][h·256 ..].  The 4 waves take blocks of 64 positions in turn with
-// their own running (m, l, o) and are merged at the end.  Grid (n, nkv, nch), 256 threads: with
-// nch > 1 workgroup z takes positions [z·csz, (z+1)·csz) and writes its record (m, l, o[256])
-// per q-head to rec[t][h][z] for bt_attn_merge_kernel instead.
-template <int GRP>
+// Causal GQA attention of tokens t0 .. t0+TPW-1 (positions pos0 + t) over cache positions
+// [0, pos0 + t] for the GRP q-heads of kv-head kvh (online softmax, attention.rs:149-199), then
+// o·sigmoid(gate) (attention.rs:202-203) -> ao[t][h·256 ..].  The TPW tokens of a workgroup share
+// every cache row it reads (R = TPW·GRP query rows).  The 4 waves take blocks of 64 positions in turn
+// with their own running (m, l, o) per row and are merged at the end.  Grid (ceil(n/TPW), nkv, nch),
+// 256 threads: with nch > 1 workgroup z takes positions [z·csz, (z+1)·csz) and writes its record
+// (m, l, o[256]) per (token, q-head) to rec[t][h][z] for bt_attn_merge_kernel instead.
+template <int GRP, int TPW>
 __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ qb, const float* __restrict__ gate,
                                                       const float* __restrict__ kcache,
                                                       const float* __restrict__ vcache, int max_ctx, int nq,
-                                                      int pos0, float* __restrict__ ao, int csz,
+                                                      int pos0, int n, float* __restrict__ ao, int csz,
                                                       float* __restrict__ rec, int n_xcd, int nkv_x, int nch_x) {
-  constexpr int HD = 256, BP = 64;
-  __shared__ float qs[GRP][HD];
-  __shared__ float ps[4][GRP][BP];
-  __shared__ float wm[4][GRP], wl[4][GRP];
-  __shared__ float wo[4][GRP][HD];
-  int t, kvh, z, nch;
+  constexpr int HD = 256, BP = 64, R = TPW * GRP;
+  // the query rows and block probabilities during the walk; the waves' (o) for the final merge after
+  // it, in the same memory
+  constexpr int kWalk = (R * HD + 4 * R * BP) * 4, kMerge = 4 * R * HD * 4;
+  __shared__ __align__(16) unsigned char buf[kWalk > kMerge ? kWalk : kMerge];
+  __shared__ float wm[4][R], wl[4][R];
+  float(*qs)[HD] = reinterpret_cast<float(*)[HD]>(buf);
+  float(*ps)[R][BP] = reinterpret_cast<float(*)[R][BP]>(buf + R * HD * 4);
+  float(*wo)[R][HD] = reinterpret_cast<float(*)[R][HD]>(buf);
+  int tg, kvh, z, nch;
   if (n_xcd > 0) {
-    // 1-D grid: workgroup L runs on XCD L % 8 (round-robin dispatch); the n tokens of one
+    // 1-D grid: workgroup L runs on XCD L % 8 (round-robin dispatch); the token groups of one
     // (kv-head, chunk) pair get indices with the same residue, so the chunk's cache rows are fetched
-    // into one XCD's L2 and read there n times, instead of once per XCD
+    // into one XCD's L2 and read there once per group, instead of once per XCD
     const int L = (int)blockIdx.x, u = L >> 3, pair = (u / n_xcd) * 8 + (L & 7);
     if (pair >= nkv_x * nch_x) return;
-    t = u % n_xcd;
+    tg = u % n_xcd;
     kvh = pair % nkv_x;
     z = pair / nkv_x;
     nch = nch_x;
   } else {
-    t = (int)blockIdx.x;
+    tg = (int)blockIdx.x;
     kvh = (int)blockIdx.y;
     z = (int)blockIdx.z;
     nch = (int)gridDim.z;
   }
+  const int t0 = tg * TPW, nt = min(TPW, n - t0);
   const unsigned tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const int ctx = nch > 1 ? min(pos0 + t + 1, (z + 1) * csz) : pos0 + t + 1;
   const int pbeg = nch > 1 ? z * csz : 0;
-  for (int i = (int)tid; i < GRP * HD; i += 256) qs[i / HD][i % HD] = qb[((size_t)t * nq + kvh * GRP) * HD + i];
+  const int pend = nch > 1 ? (z + 1) * csz : 0x7FFFFFFF;
+  int ctxt[TPW];  // positions visible to each token within this chunk: [pbeg, ctxt)
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) ctxt[tt] = tt < nt ? min(pos0 + t0 + tt + 1, pend) : pbeg;
+  const int ctx = ctxt[nt - 1];  // the group's last token sees the most
+  for (int i = (int)tid; i < R * HD; i += 256) {
+    const int r = i / HD, tt = r / GRP, gi = r % GRP;
+    qs[r][i % HD] = tt < nt ? qb[((size_t)(t0 + tt) * nq + kvh * GRP + gi) * HD + i % HD] : 0.f;
+  }
   __syncthreads();
   const float* kb = kcache + (size_t)kvh * max_ctx * HD;
   const float* vb = vcache + (size_t)kvh * max_ctx * HD;
-  float m[GRP], l[GRP];
-  float4 o[GRP];
+  float m[R], l[R];
+  float4 o[R];
 #pragma unroll
-  for (int gi = 0; gi < GRP; ++gi) {
-    m[gi] = -INFINITY;
-    l[gi] = 0.f;
-    o[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+    o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // Blocks of 64 positions, wave w taking blocks w, w+4, ...  Scores: lane = position, each lane
-  // walks its key row against the queries in LDS (a broadcast read), so a score costs 256 FMAs in
-  // one lane instead of a 64-lane reduction per (position, head).  Values: lane = 4 dims, walking the
-  // block's positions with their probabilities from LDS.
+  // walks its key row against the query rows in LDS (a broadcast read), so a score costs 256 FMAs in
+  // one lane instead of a 64-lane reduction per (position, row).  (Four lanes per position, each
+  // reading a quarter of the row so that a load touches 16 rows instead of 64, measured slower here:
+  // 119 against 83 us per layer at context 8192.)  Values: lane = 4 dims, walking the block's
+  // positions with their probabilities from LDS.
   for (int b0 = pbeg + (int)wave * BP; b0 < ctx; b0 += 4 * BP) {
     const int pp = b0 + (int)lane;
-    const bool valid = pp < ctx;
-    const float* kr = kb + (size_t)(valid ? pp : b0) * HD;
-    float sc[GRP];
+    const float* kr = kb + (size_t)(pp < ctx ? pp : b0) * HD;
+    float sc[R];
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) sc[gi] = 0.f;
-#pragma unroll 8
+    for (int r = 0; r < R; ++r) sc[r] = 0.f;
+#pragma unroll 4
     for (int j = 0; j < HD / 4; ++j) {
       const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * j);
 #pragma unroll
-      for (int gi = 0; gi < GRP; ++gi) {
-        const float4 q4 = *reinterpret_cast<const float4*>(&qs[gi][4 * j]);
-        float d = sc[gi];
+      for (int r = 0; r < R; ++r) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[r][4 * j]);
+        float d = sc[r];
         d = __builtin_fmaf(q4.x, k4.x, d);
         d = __builtin_fmaf(q4.y, k4.y, d);
         d = __builtin_fmaf(q4.z, k4.z, d);
-        sc[gi] = __builtin_fmaf(q4.w, k4.w, d);
+        sc[r] = __builtin_fmaf(q4.w, k4.w, d);
       }
     }
 #pragma unroll
-    for (int gi = 0; gi < GRP; ++gi) {
-      const float x = valid ? sc[gi] : -INFINITY;
-      const float mn = fmaxf(m[gi], wave_max(x));
-      const float al = expf(m[gi] - mn);
+    for (int r = 0; r < R; ++r) {
+      const bool valid = pp < ctxt[r / GRP];
+      const float x = valid ? sc[r] : -INFINITY;
+      const float mn = fmaxf(m[r], wave_max(x));
+      // a row with no visible position yet keeps m = -inf: its factors are 0 and 1 by definition
+      const float al = mn == -INFINITY ? 1.0f : expf(m[r] - mn);
       const float pr = valid ? expf(x - mn) : 0.f;
-      l[gi] = l[gi] * al + wave_sum(pr);
-      o[gi].x *= al;
-      o[gi].y *= al;
-      o[gi].z *= al;
-      o[gi].w *= al;
-      m[gi] = mn;
-      ps[wave][gi][lane] = pr;
+      l[r] = l[r] * al + wave_sum(pr);
+      o[r].x *= al;
+      o[r].y *= al;
+      o[r].z *= al;
+      o[r].w *= al;
+      m[r] = mn;
+      ps[wave][r][lane] = pr;
     }
     // the other lanes' probabilities of this wave (LDS accesses of one wave complete in order)
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
     const int np = min(BP, ctx - b0);
-#pragma unroll 8
+#pragma unroll 4
     for (int pi = 0; pi < np; ++pi) {
       const float4 v4 = *reinterpret_cast<const float4*>(vb + (size_t)(b0 + pi) * HD + 4 * lane);
 #pragma unroll
-      for (int gi = 0; gi < GRP; ++gi) {
-        const float pr = ps[wave][gi][pi];
-        o[gi].x = __builtin_fmaf(pr, v4.x, o[gi].x);
-        o[gi].y = __builtin_fmaf(pr, v4.y, o[gi].y);
-        o[gi].z = __builtin_fmaf(pr, v4.z, o[gi].z);
-        o[gi].w = __builtin_fmaf(pr, v4.w, o[gi].w);
+      for (int r = 0; r < R; ++r) {
+        const float pr = ps[wave][r][pi];
+        o[r].x = __builtin_fmaf(pr, v4.x, o[r].x);
+        o[r].y = __builtin_fmaf(pr, v4.y, o[r].y);
+        o[r].z = __builtin_fmaf(pr, v4.z, o[r].z);
+        o[r].w = __builtin_fmaf(pr, v4.w, o[r].w);
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();  // this block's reads of ps before the next block's writes
   }
+  __syncthreads();  // every wave is done with qs and ps: the merge buffer reuses them
 #pragma unroll
-  for (int gi = 0; gi < GRP; ++gi) {
+  for (int r = 0; r < R; ++r) {
     if (lane == 0) {
-      wm[wave][gi] = m[gi];
-      wl[wave][gi] = l[gi];
+      wm[wave][r] = m[r];
+      wl[wave][r] = l[r];
     }
-    *reinterpret_cast<float4*>(&wo[wave][gi][4 * lane]) = o[gi];
+    *reinterpret_cast<float4*>(&wo[wave][r][4 * lane]) = o[r];
   }
   __syncthreads();
 #pragma unroll
-  for (int gi = 0; gi < GRP; ++gi) {
+  for (int r = 0; r < R; ++r) {
+    const int tt = r / GRP, gi = r % GRP;
+    if (tt >= nt) continue;
+    const int t = t0 + tt;
     float M = -INFINITY;
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][gi]);
+    for (int w = 0; w < 4; ++w)
+      if (wl[w][r] > 0.f) M = fmaxf(M, wm[w][r]);
     float L = 0.f, O = 0.f;
     for (int w = 0; w < 4; ++w) {
-      const float e = wl[w][gi] > 0.f ? expf(wm[w][gi] - M) : 0.f;
-      L = __builtin_fmaf(wl[w][gi], e, L);
-      O = __builtin_fmaf(wo[w][gi][tid], e, O);
+      const float e = wl[w][r] > 0.f ? expf(wm[w][r] - M) : 0.f;
+      L = __builtin_fmaf(wl[w][r], e, L);
+      O = __builtin_fmaf(wo[w][r][tid], e, O);
     }
     const int h = kvh * GRP + gi;
     if (nch > 1) {

@@ -1215,26 +1215,32 @@ static hipError_t launch(K kfn, dim3 g, dim3 b, hipStream_t s, Args... args) {
   return hipGetLastError();
 }
 
-// Grid (n, nkv, nch); with at least 8 (kv-head, chunk) pairs, a 1-D grid that keeps each pair's
-// tokens on one XCD (bt_attn_kernel).
+// Grid (token groups, nkv, nch); with at least 8 (kv-head, chunk) pairs, a 1-D grid that keeps each
+// pair's token groups on one XCD (bt_attn_kernel).  A few tokens (speculative verify) go two to a
+// workgroup, so that each cache row is read half as often; a long prefill keeps one token per
+// workgroup (more workgroups, fewer registers each).
 static hipError_t launch_bt_attn(int grp, int n, int nkv, int nch, hipStream_t s, const float* qb, const float* gate,
                                  const float* kc, const float* vc, int max_ctx, int nq, int pos0, float* ao, int csz,
                                  float* rec) {
+  const int tpw = n <= 16 ? 2 : 1;
+  const int ng = (n + tpw - 1) / tpw;
   const int pairs = nkv * nch;
   const bool xcd = nch > 1 && pairs >= 8;
-  const dim3 g = xcd ? dim3((unsigned)(8 * ((pairs + 7) / 8) * n)) : dim3((unsigned)n, (unsigned)nkv, (unsigned)nch);
-  const int nx = xcd ? n : 0;
-#define DZ_ATTN(G_) \
-  launch(bt_attn_kernel<G_>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, ao, csz, rec, nx, nkv, nch)
+  const dim3 g = xcd ? dim3((unsigned)(8 * ((pairs + 7) / 8) * ng)) : dim3((unsigned)ng, (unsigned)nkv, (unsigned)nch);
+  const int nx = xcd ? ng : 0;
+#define DZ_ATTN(G_, T_) \
+  launch(bt_attn_kernel<G_, T_>, g, dim3(256), s, qb, gate, kc, vc, max_ctx, nq, pos0, n, ao, csz, rec, nx, nkv, nch)
+#define DZ_ATTN_G(G_) return tpw == 2 ? DZ_ATTN(G_, 2) : DZ_ATTN(G_, 1)
   switch (grp) {
-    case 1: return DZ_ATTN(1);
-    case 2: return DZ_ATTN(2);
-    case 3: return DZ_ATTN(3);
-    case 4: return DZ_ATTN(4);
-    case 6: return DZ_ATTN(6);
-    case 8: return DZ_ATTN(8);
+    case 1: DZ_ATTN_G(1);
+    case 2: DZ_ATTN_G(2);
+    case 3: DZ_ATTN_G(3);
+    case 4: DZ_ATTN_G(4);
+    case 6: DZ_ATTN_G(6);
+    case 8: DZ_ATTN_G(8);
     default: return hipErrorInvalidValue;
   }
+#undef DZ_ATTN_G
 #undef DZ_ATTN
 }
 

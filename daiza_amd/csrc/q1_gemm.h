@@ -53,6 +53,22 @@ __device__ __forceinline__ float pack_sig(float amax) {
   return ldexpf(1.0f, e - 14 < -100 ? -100 : e - 14);
 }
 
+// max(|v.x|, |v.y|, |v.z|, |v.w|) over the 64 lanes of the wave, in every lane: the 16 lanes of each
+// DPP row (xor 1, xor 2, half-row mirror, row mirror), then the four rows' lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_max_abs4(float4 v) {
+  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0xB1, 0xF, 0xF, false)));
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0x4E, 0xF, 0xF, false)));
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0x141, 0xF, 0xF, false)));
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0x140, 0xF, 0xF, false)));
+  const int mi = __builtin_bit_cast(int, m);
+  const float m0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 0));
+  const float m1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 16));
+  const float m2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 32));
+  const float m3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 48));
+  return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+}
+
 // Splits one value (already divided by sig) into its f16 hi and lo parts.
 __device__ __forceinline__ void pack_split(float v, unsigned short& h, unsigned short& l) {
   const _Float16 hi = (_Float16)v;
@@ -226,18 +242,21 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   };
   auto put_x = [&](int b, const u32x4 (&xv)[XV]) {
     if constexpr (RAW) {
+      // token (tid >> 7) + 2j is the same for a whole wave: token rows past n_tok are skipped (their
+      // product columns are never stored)
       const unsigned half = (tid >> 6) & 1u;
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
+        if (tok0 + (int)(tid >> 7) + 2 * j >= n_tok) continue;
         const float4 v = __builtin_bit_cast(float4, xv[j]);
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = wave_max_abs4(v);
         if (lane == 0) tile_max[(tid >> 7) + 2 * j][half] = m;
       }
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
         const int n = (int)(tid >> 7) + 2 * j;
+        if (tok0 + n >= n_tok) continue;
         const float sg = pack_sig(fmaxf(tile_max[n][0], tile_max[n][1]));
         const float rs = 1.0f / sg;  // exact: a power of two
         const float4 v = __builtin_bit_cast(float4, xv[j]);

@@ -475,15 +475,22 @@ __global__ __launch_bounds__(256) void bt_swiglu_kernel(const float* __restrict_
 }
 
 // The same from the partials of a split gate/up product (part[z][t][2F], zstride apart): each sum in
-// split order, as gemm_split_reduce_kernel forms it, then silu(gate) · up.
+// split order, as gemm_split_reduce_kernel forms it (times the token's 1/rms for a normed raw
+// product), then silu(gate) · up.
 __global__ __launch_bounds__(256) void bt_split_swiglu_kernel(const float* __restrict__ part, int splits,
                                                               int64_t zstride, int64_t F, int n,
-                                                              float* __restrict__ s) {
+                                                              float* __restrict__ s, const float* __restrict__ ssq,
+                                                              int ssq_ld, int64_t K, float eps) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int t = blockIdx.y;
   if (i >= F || t >= n) return;
   const size_t off = (size_t)t * 2 * F + i;
-  const float g = ordered_sum(part + off, zstride, splits), u = ordered_sum(part + off + F, zstride, splits);
+  float g = ordered_sum(part + off, zstride, splits), u = ordered_sum(part + off + F, zstride, splits);
+  if (ssq) {  // a normed raw product: 1/rms applied to the sums
+    const float inv = split_inv_rms(ssq, ssq_ld, splits, t, K, eps);
+    g *= inv;
+    u *= inv;
+  }
   s[(size_t)t * F + i] = siluf_(g) * u;
 }
 

@@ -78,6 +78,13 @@ __device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_
   return acc;
 }
 
+// 1/rms of token n from the per-split sums of squares of a normed raw product (splits in order).
+__device__ __forceinline__ float split_inv_rms(const float* __restrict__ ssq, int ssq_ld, int splits, int n, int64_t K,
+                                               float eps) {
+  const float ss = ordered_sum(ssq + n, ssq_ld, splits);
+  return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
 }  // namespace dz
 
 #define DZ_HIP_CHECK(expr)                                                     \

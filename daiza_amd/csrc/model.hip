@@ -1259,10 +1259,12 @@ static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
 // y[n][W.rows] (=|+=) W · (optionally RMS-normalised) x[n][W.cols].
 static int bt_gemm(dz_ctx* x, const Q1Dev& W, const float* xin, int64_t ldx, int n, const float* norm_w, float* y,
                    int64_t ldy, int accumulate, GemmDefer* defer = nullptr) {
-  if (!norm_w && n <= 16) {
-    // no RMSNorm and few tokens (verify): the product packs its tiles itself, which saves the packing
-    // launch; with many tokens every row-block group would repeat the packing of the same tiles
-    DZ_HIP_CHECK(launch_q1_gemm_raw(W, xin, ldx, n, y, ldy, accumulate, x->s, &x->bt.split));
+  if (n <= 16) {
+    // few tokens (verify): the product packs its tiles itself (folding in the RMSNorm, whose 1/rms is
+    // applied to the sums), which saves the packing launch; with many tokens every row-block group
+    // would repeat the packing of the same tiles
+    DZ_HIP_CHECK(launch_q1_gemm_raw(W, xin, ldx, n, y, ldy, accumulate, x->s, &x->bt.split, norm_w,
+                                    x->m->cfg.rms_eps, defer));
     return DZ_OK;
   }
   PackedX p;
@@ -1354,7 +1356,7 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
     if ((rc = bt_gemm(x, l.gate_up, x->bt.h, H, n, l.post_norm, x->bt.ygu, 2 * F, 0, &gd))) return rc;
     if (gd.splits > 1)
       DZ_HIP_CHECK(launch(bt_split_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s, gd.part,
-                          gd.splits, gd.zstride, F, n, x->bt.sw));
+                          gd.splits, gd.zstride, F, n, x->bt.sw, gd.ssq, gd.ssq_ld, gd.K, gd.eps));
     else
       DZ_HIP_CHECK(launch(bt_swiglu_kernel, dim3((unsigned)((F + 255) / 256), nb), dim3(256), s,
                           (const float*)x->bt.ygu, F, n, x->bt.sw));

@@ -43,6 +43,14 @@ struct GemmX {
   // raw form (q1_gemm_kernel<NB, true>): x[n][K] f32 with row stride ldx, packed per tile in LDS
   const float* xf;
   int64_t ldx, K;
+  // raw form with RMSNorm (rmsnorm_into, rmsnorm.rs:17-200): the tiles are packed from x·nw, the
+  // sums of squares of x gathered on the way, and y = inv · W (x·nw) with inv = 1/sqrt(ss/K + eps):
+  // by the kernel itself when it sees every tile, else by the consumer of the split partials, from
+  // the per-split sums ssq[z][ssq_ld] that the workgroups of row-block group 0 write
+  const float* nw;
+  float* ssq;
+  int ssq_ld;
+  float eps;
 };
 
 // The power of two that brings max|x| into [2^13, 2^14) (1 for an all-zero or non-finite row).
@@ -67,6 +75,25 @@ __device__ __forceinline__ float wave_max_abs4(float4 v) {
   const float m2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 32));
   const float m3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, 48));
   return fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+}
+
+// v.x² + v.y² + v.z² + v.w² summed over the 64 lanes of the wave, in every lane, in a fixed order
+// (the DPP row sums as in wave_max_abs4, then rows 0..3).
+__device__ __forceinline__ float wave_sumsq4(float4 v) {
+  float q = v.x * v.x;
+  q = __builtin_fmaf(v.y, v.y, q);
+  q = __builtin_fmaf(v.z, v.z, q);
+  q = __builtin_fmaf(v.w, v.w, q);
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0xB1, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x4E, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x141, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x140, 0xF, 0xF, false));
+  const int qi = __builtin_bit_cast(int, q);
+  const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 0));
+  const float q1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 16));
+  const float q2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 32));
+  const float q3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 48));
+  return (q0 + q1) + (q2 + q3);
 }
 
 // Splits one value (already divided by sig) into its f16 hi and lo parts.
@@ -188,6 +215,9 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float tile_max[TOK][2];   // raw form: per token, max |x| of each half tile
   __shared__ float tile_sig[2][TOK];   // raw form: sig(n, t) of each activation buffer
+  __shared__ float tile_ss[TOK][2];    // raw form with RMSNorm: per token, sum x^2 of each half tile
+  __shared__ float tok_inv[TOK];       // raw form with RMSNorm: 1/rms of each token (unsplit product)
+  float ss_acc = 0.f;                  // thread n < TOK: token n's sum of x^2 over this workgroup's tiles
   const unsigned tid = threadIdx.x, lane = tid & 63u;
   const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6);
   const bool live = rb < nrb;
@@ -240,19 +270,32 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       }
     }
   };
-  auto put_x = [&](int b, const u32x4 (&xv)[XV]) {
+  auto put_x = [&](int b, u32x4 (&xv)[XV], int t_x) {
     if constexpr (RAW) {
       // token (tid >> 7) + 2j is the same for a whole wave: token rows past n_tok are skipped (their
       // product columns are never stored)
       const unsigned half = (tid >> 6) & 1u;
+      const bool normed = x.nw != nullptr;
+      float4 nw4 = make_float4(1.f, 1.f, 1.f, 1.f);
+      if (normed) {
+        const int64_t col = (int64_t)t_x * kTileCols + 4 * (tid & 127u);
+        if (col < x.K) nw4 = *reinterpret_cast<const float4*>(x.nw + col);
+      }
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
         if (tok0 + (int)(tid >> 7) + 2 * j >= n_tok) continue;
-        const float4 v = __builtin_bit_cast(float4, xv[j]);
+        float4 v = __builtin_bit_cast(float4, xv[j]);
+        if (normed) {
+          const float q = wave_sumsq4(v);
+          if (lane == 0) tile_ss[(tid >> 7) + 2 * j][half] = q;
+          v = make_float4(v.x * nw4.x, v.y * nw4.y, v.z * nw4.z, v.w * nw4.w);
+          xv[j] = __builtin_bit_cast(u32x4, v);
+        }
         const float m = wave_max_abs4(v);
         if (lane == 0) tile_max[(tid >> 7) + 2 * j][half] = m;
       }
       __syncthreads();
+      if (normed && (int)tid < TOK && tok0 + (int)tid < n_tok && t_x < t_end) ss_acc += tile_ss[tid][0] + tile_ss[tid][1];
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
         const int n = (int)(tid >> 7) + 2 * j;
@@ -285,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   u32x4 xv[XV];
   load_unit(t_begin, cv, cs);
   load_x(t_begin, xv);
-  put_x(0, xv);
+  put_x(0, xv, t_begin);
   __syncthreads();
   for (int t = t_begin; t < t_end; ++t) {
     const int b = NBUF == 2 ? (t - t_begin) & 1 : 0;
@@ -340,11 +383,11 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       }
     }
     if (NBUF == 2) {
-      put_x(b ^ 1, xv);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
+      put_x(b ^ 1, xv, t + 1);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
     } else {
       __syncthreads();  // every wave is done with this tile's activations
       load_x(t + 1, xv);
-      put_x(0, xv);
+      put_x(0, xv, t + 1);
     }
     __syncthreads();
 #pragma unroll
@@ -353,13 +396,22 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       cs[sb] = csn[sb];
     }
   }
+  // raw form with RMSNorm: each token's 1/rms (every tile seen) or this split's sums of squares
+  if (RAW && x.nw != nullptr) {
+    if (gridDim.z == 1) {
+      if ((int)tid < TOK) tok_inv[tid] = 1.0f / sqrtf(ss_acc / (float)x.K + x.eps);
+      __syncthreads();
+    } else if (blockIdx.x == 0 && (int)tid < TOK && tok0 + (int)tid < n_tok) {
+      x.ssq[(size_t)blockIdx.z * x.ssq_ld + tok0 + tid] = ss_acc;
+    }
+  }
   if (!live) return;
   // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int n = tok0 + 16 * nb + (int)r;
     if (n >= n_tok) continue;
-    const float sg = RAW ? 1.0f : x.sig[n];
+    const float sg = RAW ? (x.nw != nullptr && gridDim.z == 1 ? tok_inv[16 * nb + (int)r] : 1.0f) : x.sig[n];
     float* yr = y + (size_t)n * ldy;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
@@ -376,15 +428,19 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   }
 }
 
-// y[n][row] (=|+=) Σ_z part[z][n][row] for z < splits in order (the partials of a split product).
+// y[n][row] (=|+=) Σ_z part[z][n][row] for z < splits in order (the partials of a split product),
+// times token n's 1/rms when ssq is given (a normed raw product: sums of squares [z][ssq_ld], K).
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part, int splits,
                                                                 int64_t zstride, int64_t rows, int n_tok,
-                                                                float* __restrict__ y, int64_t ldy, int accumulate) {
+                                                                float* __restrict__ y, int64_t ldy, int accumulate,
+                                                                const float* __restrict__ ssq, int ssq_ld, int64_t K,
+                                                                float eps) {
   const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int n = blockIdx.y;
   if (row >= rows || n >= n_tok) return;
   const size_t off = (size_t)n * rows + row;
-  const float v = ordered_sum(part + off, zstride, splits);
+  float v = ordered_sum(part + off, zstride, splits);
+  if (ssq) v *= split_inv_rms(ssq, ssq_ld, splits, n, K, eps);
   float* yr = y + (size_t)n * ldy + row;
   *yr = accumulate ? *yr + v : v;
 }

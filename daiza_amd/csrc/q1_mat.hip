@@ -298,7 +298,7 @@ int gemm_splits(const Q1Dev& W, int n, int* tps) {
 // One product launch: the packed form (p non-null) or the raw form (x f32, row stride ldx).
 static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const float* xr, int64_t ldx, int n, float* y,
                                      int64_t ldy, int accumulate, hipStream_t s, Scratch* split,
-                                     GemmDefer* defer = nullptr) {
+                                     GemmDefer* defer = nullptr, const float* norm_w = nullptr, float eps = 0.f) {
   static bool attr = false;
   if (!attr) {
     const void* ks[4] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
@@ -320,6 +320,8 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
     gx.xf = xr;
     gx.ldx = ldx;
     gx.K = W.cols;
+    gx.nw = norm_w;
+    gx.eps = eps;
   } else {
     gx.xh = p->xh;
     gx.xl = p->xl;
@@ -333,9 +335,14 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
   int64_t ld = ldy, zs = 0;
   if (S > 1) {
     zs = (int64_t)n * W.rows;
-    if (split->reserve((size_t)S * zs * sizeof(float))) return hipErrorOutOfMemory;
+    // the partials, then (normed raw form) the per-split sums of squares [S][n]
+    if (split->reserve(((size_t)S * zs + (norm_w ? (size_t)S * n : 0)) * sizeof(float))) return hipErrorOutOfMemory;
     out = static_cast<float*>(split->ptr);
     ld = W.rows;
+    if (raw && norm_w) {
+      gx.ssq = out + (size_t)S * zs;
+      gx.ssq_ld = n;
+    }
   }
   const unsigned gx_ = (unsigned)((W.nrb + 3) / 4);
   const dim3 g1(gx_, 1, (unsigned)S), g2(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S);
@@ -355,10 +362,11 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
                          W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   }
   hipError_t e = hipGetLastError();
-  if (defer) *defer = GemmDefer{out, S, zs};
+  const float* ssq = S > 1 && raw && norm_w ? gx.ssq : nullptr;
+  if (defer) *defer = GemmDefer{out, S, zs, ssq, n, W.cols, eps};
   if (e != hipSuccess || S == 1 || defer) return e;
   hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((W.rows + 255) / 256), (unsigned)n), dim3(256), 0, s,
-                     (const float*)out, S, zs, W.rows, n, y, ldy, accumulate);
+                     (const float*)out, S, zs, W.rows, n, y, ldy, accumulate, ssq, n, W.cols, eps);
   return hipGetLastError();
 }
 
@@ -368,9 +376,10 @@ hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int
 }
 
 hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,
-                              int accumulate, hipStream_t s, Scratch* split) {
+                              int accumulate, hipStream_t s, Scratch* split, const float* norm_w, float eps,
+                              GemmDefer* defer) {
   if ((W.cols & 3) || (ldx & 3)) return hipErrorInvalidValue;  // 16-byte loads of x rows
-  return launch_q1_gemm_any(W, nullptr, x, ldx, n, y, ldy, accumulate, s, split);
+  return launch_q1_gemm_any(W, nullptr, x, ldx, n, y, ldy, accumulate, s, split, defer, norm_w, eps);
 }
 
 // ------------------------------------------------------------------ matrix API state

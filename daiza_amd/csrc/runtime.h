@@ -79,13 +79,22 @@ struct GemmDefer {
   const float* part = nullptr;
   int splits = 1;
   int64_t zstride = 0;
+  // a normed raw product: per-split sums of squares [splits][ssq_ld] (the caller applies 1/rms)
+  const float* ssq = nullptr;
+  int ssq_ld = 0;
+  int64_t K = 0;
+  float eps = 0.f;
 };
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
                           hipStream_t s, Scratch* split, GemmDefer* defer = nullptr);
 // The same product on f32 x[n][W.cols] (row stride ldx, both multiples of 4), each K tile packed in
-// LDS with its own power-of-two scale per token: no separate packing pass (inputs without RMSNorm).
+// LDS with its own power-of-two scale per token: no separate packing pass.  With norm_w, the product
+// of the RMS-normalised x (weight norm_w, eps): the tiles are packed from x·norm_w and the sums of
+// squares gathered on the way; 1/rms is applied to the result (by the deferred consumer when defer
+// is given and the product is split).
 hipError_t launch_q1_gemm_raw(const Q1Dev& W, const float* x, int64_t ldx, int n, float* y, int64_t ldy,
-                              int accumulate, hipStream_t s, Scratch* split);
+                              int accumulate, hipStream_t s, Scratch* split, const float* norm_w = nullptr,
+                              float eps = 0.f, GemmDefer* defer = nullptr);
 
 }  // namespace dz
 

@@ -441,23 +441,43 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
 }
 
 // Merge of the position chunks of bt_attn_kernel (records with l = 0 held no position), then
-// o·sigmoid(gate).  Grid (n, nq), 256 threads.
+// o·sigmoid(gate).  Grid (n, nq), 256 threads (one output dim each); nch <= 256.  Thread z < nch
+// brings chunk z's (m, l) to LDS, so that every chunk's weight exp(m_z - M) is formed once, and the
+// dims are summed over the chunks in order with their loads issued 16 at a time.
 __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restrict__ rec, int nch,
                                                             const float* __restrict__ gate, int nq,
                                                             float* __restrict__ ao) {
   constexpr int HD = 256;
+  __shared__ float ml[2][256];  // m, then the chunk weight; l
+  __shared__ float red[8];
   const int t = blockIdx.x, h = blockIdx.y;
   const unsigned tid = threadIdx.x;
   const float* rr = rec + ((size_t)t * nq + h) * nch * (2 + HD);
-  float M = -INFINITY;
-  for (int z = 0; z < nch; ++z)
-    if (rr[(size_t)z * (2 + HD) + 1] > 0.f) M = fmaxf(M, rr[(size_t)z * (2 + HD)]);
+  const bool has = (int)tid < nch;
+  const float mz = has ? rr[(size_t)tid * (2 + HD)] : -INFINITY;
+  const float lz = has ? rr[(size_t)tid * (2 + HD) + 1] : 0.f;
+  // M = max of m over the chunks that held a position (in any order: max is exact)
+  float m = lz > 0.f ? mz : -INFINITY;
+  m = wave_max(m);
+  if ((tid & 63u) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  ml[0][tid] = lz > 0.f ? expf(mz - M) : 0.f;
+  ml[1][tid] = lz;
+  __syncthreads();
   float L = 0.f, O = 0.f;
-  for (int z = 0; z < nch; ++z) {
-    const float* c = rr + (size_t)z * (2 + HD);
-    const float e = c[1] > 0.f ? expf(c[0] - M) : 0.f;
-    L = __builtin_fmaf(c[1], e, L);
-    O = __builtin_fmaf(c[2 + tid], e, O);
+  for (int z0 = 0; z0 < nch; z0 += 16) {
+    float o[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o[k] = z0 + k < nch ? rr[(size_t)(z0 + k) * (2 + HD) + 2 + tid] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (z0 + k < nch) {
+        const float e = ml[0][z0 + k];
+        L = __builtin_fmaf(ml[1][z0 + k], e, L);
+        O = __builtin_fmaf(o[k], e, O);
+      }
+    }
   }
   const float gt = gate[((size_t)t * nq + h) * HD + tid];
   ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);

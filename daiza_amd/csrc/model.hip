@@ -1250,7 +1250,7 @@ static hipError_t launch_bt_attn(int grp, int n, int nkv, int nch, hipStream_t s
 // 64 each) where that keeps about the wanted number of chunks.
 static int bt_attn_chunks(int n, int nkv, int ctx_max, int* csz) {
   int nch = (1024 + n * nkv - 1) / (n * nkv);
-  nch = std::max(1, std::min(nch, std::max(1, ctx_max / 64)));
+  nch = std::max(1, std::min({nch, std::max(1, ctx_max / 64), 256}));  // the merge takes up to 256
   *csz = (ctx_max + nch - 1) / nch;
   if (nch > 1 && *csz > 256) *csz = (*csz + 128) / 256 * 256;
   return (ctx_max + *csz - 1) / *csz;

@@ -49,23 +49,42 @@ __global__ __launch_bounds__(256) void bt_embed_kernel(const int* __restrict__ i
 // ring's entry for the earlier tokens (the token at chunk offset t' < 0 sits in slot
 // (head0 + t') & 3, head0 = slot of token 0).  Thread per (token, channel).  keep (verify, else null)
 // receives the conv inputs themselves, keep[t][ch] = x[t][ch], from which the commit rebuilds the ring.
+// The q and k channels (the first 2 nkh·128, whole heads per workgroup: 2 nkh·128 is a multiple of
+// 256) also get their per-head L2 norm (l2norm_inplace, ssm.rs:76-135; q additionally times
+// 1/sqrt(128), ssm.rs:532-533) into qk[t][0 .. 2 nkh·128): a head is two whole waves of the workgroup.
 __global__ __launch_bounds__(256) void bt_conv_kernel(const float* __restrict__ yin, int64_t ldin, int n,
                                                       const float* __restrict__ ring, int head0,
                                                       const float* __restrict__ conv_w, int64_t qkvd,
-                                                      float* __restrict__ cout, float* __restrict__ keep) {
-  const int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x;
+                                                      float* __restrict__ cout, float* __restrict__ keep, int nkh,
+                                                      float* __restrict__ qk) {
+  __shared__ float red[4];
+  const unsigned tid = threadIdx.x;
+  const int64_t ch = (int64_t)blockIdx.x * 256 + tid;
   const int t = blockIdx.y;
-  if (ch >= qkvd || t >= n) return;
+  const bool live = ch < qkvd && t < n;
   float o = 0.f, xt = 0.f;
+  if (live) {
 #pragma unroll
-  for (int tap = 0; tap < 4; ++tap) {
-    const int tt = t - 3 + tap;
-    const float xv = tt >= 0 ? yin[(size_t)tt * ldin + ch] : ring[(size_t)((head0 + tt) & 3) * qkvd + ch];
-    o = __builtin_fmaf(xv, conv_w[(size_t)tap * qkvd + ch], o);
-    if (tap == 3) xt = xv;
+    for (int tap = 0; tap < 4; ++tap) {
+      const int tt = t - 3 + tap;
+      const float xv = tt >= 0 ? yin[(size_t)tt * ldin + ch] : ring[(size_t)((head0 + tt) & 3) * qkvd + ch];
+      o = __builtin_fmaf(xv, conv_w[(size_t)tap * qkvd + ch], o);
+      if (tap == 3) xt = xv;
+    }
   }
-  cout[(size_t)t * qkvd + ch] = siluf_(o);
-  if (keep) keep[(size_t)t * qkvd + ch] = xt;
+  const float v = siluf_(o);
+  if (live) {
+    cout[(size_t)t * qkvd + ch] = v;
+    if (keep) keep[(size_t)t * qkvd + ch] = xt;
+  }
+  const int64_t kdim = (int64_t)nkh * 128;
+  if ((int64_t)blockIdx.x * 256 >= 2 * kdim) return;  // a v-channel workgroup (uniform)
+  const float sq = wave_sum(v * v);
+  if ((tid & 63u) == 0) red[tid >> 6] = sq;
+  __syncthreads();
+  const int hw = (int)(tid >> 7) * 2;  // this head's first wave
+  const float inv = 1.0f / sqrtf((red[hw] + red[hw + 1]) + 1e-6f);
+  if (live) qk[(size_t)t * 2 * kdim + ch] = ch < kdim ? (v * inv) * (1.0f / sqrtf(128.0f)) : v * inv;
 }
 
 // Conv ring after tokens [0, t1) of a chunk: the inputs of tokens [t0, t1) (t0 = max(0, t1 - 4))
@@ -75,24 +94,6 @@ __global__ __launch_bounds__(256) void bt_ring_kernel(const float* __restrict__ 
   const int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (ch >= qkvd) return;
   for (int t = t0; t < t1; ++t) ring[(size_t)((head0 + t) & 3) * qkvd + ch] = yin[(size_t)t * ldin + ch];
-}
-
-// Per-k-head L2 norms of the conv outputs (l2norm_inplace, ssm.rs:76-135; q additionally times
-// 1/sqrt(128), ssm.rs:532-533): qk[t][0 .. kdim) = q, qk[t][kdim .. 2 kdim) = k.  Grid (n, 2 nkh),
-// 128 threads.
-__global__ __launch_bounds__(128) void bt_l2norm_kernel(const float* __restrict__ cout, int64_t qkvd, int nkh,
-                                                        float* __restrict__ qk) {
-  __shared__ float red[2];
-  const int t = blockIdx.x, hh = blockIdx.y;
-  const unsigned tid = threadIdx.x;
-  const int64_t kdim = (int64_t)nkh * 128;
-  const int64_t ch = hh < nkh ? (int64_t)hh * 128 + tid : kdim + (int64_t)(hh - nkh) * 128 + tid;
-  const float v = cout[(size_t)t * qkvd + ch];
-  const float s = wave_sum(v * v);
-  if ((tid & 63u) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
-  qk[(size_t)t * 2 * kdim + ch] = hh < nkh ? (v * inv) * (1.0f / sqrtf(128.0f)) : v * inv;
 }
 
 // Rollback record of a verify chunk for one DeltaNet layer: the decay and the delta of every token

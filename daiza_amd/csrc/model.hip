@@ -1308,9 +1308,10 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
       const int head0 = (x->ring_base[(size_t)si] + p0) & 3;
       const unsigned gch = (unsigned)((qkvd + 255) / 256);
       // verify keeps the chunk's conv inputs (bt.rx) for the commit; a kept forward updates the ring now
+      // (conv, SiLU and the q/k L2 norms in one launch)
       DZ_HIP_CHECK(launch(bt_conv_kernel, dim3(gch, nb), dim3(256), s, (const float*)x->bt.yin, ld_in, n,
                           (const float*)ring, head0, (const float*)l.conv_w, qkvd, x->bt.cout,
-                          verify ? x->bt.rx[(size_t)si] : nullptr));
+                          verify ? x->bt.rx[(size_t)si] : nullptr, (int)c.ssm_k_heads, x->bt.qk));
       DnRecord rec{nullptr, nullptr, nullptr};
       if (verify) {
         rec = x->bt.rec[(size_t)si];
@@ -1318,8 +1319,6 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
         DZ_HIP_CHECK(launch(bt_ring_kernel, dim3(gch), dim3(256), s, (const float*)x->bt.yin, ld_in, std::max(0, n - 4),
                             n, ring, head0, qkvd));
       }
-      DZ_HIP_CHECK(launch(bt_l2norm_kernel, dim3(nb, (unsigned)(2 * c.ssm_k_heads)), dim3(128), s,
-                          (const float*)x->bt.cout, qkvd, (int)c.ssm_k_heads, x->bt.qk));
       float* state = x->ssm_state + (size_t)si * c.ssm_v_heads * hd * hd;
       DZ_HIP_CHECK(launch(bt_scan_kernel, dim3((unsigned)(4 * c.ssm_v_heads)), dim3(256), s, (const float*)x->bt.yin,
                           ld_in, (const float*)x->bt.cout, qkvd, (const float*)x->bt.qk, n, (int)c.ssm_k_heads,

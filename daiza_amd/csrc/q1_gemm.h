@@ -13,8 +13,9 @@
 //
 // Layout.  The weights stay in the GEMV layout (common.h): unit (row-block rb, tile t) holds 64
 // rows × 512 columns, each row's 64 sign bytes as four 16-byte chunks, chunk c of row L holding
-// group (L >> 4) ^ c with its bytes permuted by position ^ L.  Wave w of a workgroup owns row-block
-// rb = 4·blockIdx.x + w and walks the tiles; in a 16-row block sb of that unit, lane (r, q)
+// group (L >> 4) ^ c with its bytes permuted by position ^ L.  A workgroup owns row-blocks
+// 4·blockIdx.x .. +3 (one wave each, or two waves each taking two 16-row blocks: gemm_waves) and
+// walks the tiles; in a 16-row block sb of a unit, lane (r, q)
 // (r = lane & 15, q = lane >> 4) takes the chunk of row 16·sb + r that holds group q, restores the
 // byte order in registers, and feeds sign byte s of that group as the eight f16 values of
 // v_mfma_f32_16x16x32_f16's A operand for step s (columns 128q + 8s + e).  The B operand, token
@@ -30,6 +31,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup (wide form)
 constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup of the wide form, the padding of n
 constexpr int kGemmRowPad = 2 * kTileCols + 16;  // LDS bytes per staged token row (16 B pad: no bank conflicts)
+// Waves per workgroup: the workgroup owns 4 row-blocks; with 8 waves (few tokens) two waves share a
+// row-block, each taking two of its four 16-row blocks, so the per-tile chain of a wave (operand
+// expansion and matrix instructions) is half as long and the packing of the activations is shared
+// by twice as many waves.
+__host__ __device__ constexpr int gemm_waves(int nb) { return nb == 1 ? 8 : 4; }
 // hi and lo tiles of NB token blocks (two buffers of them for NB = 1)
 __host__ __device__ constexpr size_t gemm_shmem(int nb) { return (size_t)(nb == 1 ? 2 : 1) * 2 * 16 * nb * kGemmRowPad; }
 constexpr size_t kGemmShmem = gemm_shmem(kGemmNB);
@@ -101,6 +107,58 @@ __device__ __forceinline__ void pack_split(float v, unsigned short& h, unsigned 
   const _Float16 hi = (_Float16)v;
   h = __builtin_bit_cast(unsigned short, hi);
   l = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)hi));
+}
+
+// The exponent e of the power of two sig = 2^e that pack_sig returns (0 for an all-zero or
+// non-finite row): x / sig = ldexp(x, -e), exact.
+__device__ __forceinline__ int pack_exp(float amax) {
+  if (!(amax > 0.f) || !(amax <= 3.0e38f)) return 0;
+  int e;
+  (void)frexpf(amax, &e);
+  return e - 14 < -100 ? -100 : e - 14;
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Four values divided by 2^e and split into f16 hi and lo parts (round to nearest even, two values
+// per conversion on gfx950), packed in token-row order.
+__device__ __forceinline__ void pack_split4(float4 v, int e, uint2& h, uint2& l) {
+  const f32x2 a = {ldexpf(v.x, -e), ldexpf(v.y, -e)}, c = {ldexpf(v.z, -e), ldexpf(v.w, -e)};
+  const f16x2 ha = __builtin_convertvector(a, f16x2), hc = __builtin_convertvector(c, f16x2);
+  const f16x2 la = __builtin_convertvector(a - __builtin_convertvector(ha, f32x2), f16x2);
+  const f16x2 lc = __builtin_convertvector(c - __builtin_convertvector(hc, f32x2), f16x2);
+  h = make_uint2(__builtin_bit_cast(unsigned, ha), __builtin_bit_cast(unsigned, hc));
+  l = make_uint2(__builtin_bit_cast(unsigned, la), __builtin_bit_cast(unsigned, lc));
+}
+
+// max |v| over the 8 values of every lane of the wave, in every lane (as wave_max_abs4).
+__device__ __forceinline__ float wave_max_abs8(float4 a, float4 b) {
+  const float4 m = make_float4(fmaxf(fabsf(a.x), fabsf(b.x)), fmaxf(fabsf(a.y), fabsf(b.y)), fmaxf(fabsf(a.z), fabsf(b.z)),
+                               fmaxf(fabsf(a.w), fabsf(b.w)));
+  return wave_max_abs4(m);
+}
+
+// Sum of the squares of the 8 values of every lane over the wave, in every lane, in a fixed order.
+__device__ __forceinline__ float wave_sumsq8(float4 a, float4 b) {
+  float q = a.x * a.x;
+  q = __builtin_fmaf(a.y, a.y, q);
+  q = __builtin_fmaf(a.z, a.z, q);
+  q = __builtin_fmaf(a.w, a.w, q);
+  q = __builtin_fmaf(b.x, b.x, q);
+  q = __builtin_fmaf(b.y, b.y, q);
+  q = __builtin_fmaf(b.z, b.z, q);
+  q = __builtin_fmaf(b.w, b.w, q);
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0xB1, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x4E, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x141, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x140, 0xF, 0xF, false));
+  const int qi = __builtin_bit_cast(int, q);
+  const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 0));
+  const float q1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 16));
+  const float q2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 32));
+  const float q3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 48));
+  return (q0 + q1) + (q2 + q3);
 }
 
 // One workgroup (256 threads) per token row n < Np: x[n][0..K) -> xh/xl[n][0..Kp), sig[n]; rows
@@ -197,7 +255,7 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
   s2 = (sc_bits & 0x7FFFu) * 0x00010001u;
 }
 
-// Grid (ceil(nrb / 4), Np / (16·NB), splits), 256 threads, gemm_shmem(NB) bytes of dynamic LDS.
+// Grid (ceil(nrb / 4), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB) bytes of LDS.
 // Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
 // partial to y + z·zstride; an unsplit product (gridDim.z = 1) writes
 // y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xl)[n][k] for n < n_tok, row < rows.
@@ -207,28 +265,34 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
 // tile's products are scaled by it as they are added: y = Σ_t sig(n, t) · W_t (hi + lo)(n, t).
 // That skips the separate packing pass for inputs that need no RMSNorm.
 template <int NB, bool RAW = false>
-__global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
+__global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
                                                          int ntiles, int tps, const GemmX x, int n_tok,
                                                          float* __restrict__ y, int64_t ldy, int64_t zstride,
                                                          int accumulate) {
   constexpr int TOK = 16 * NB;
+  constexpr int NT = 64 * gemm_waves(NB);  // threads
+  constexpr int HALVES = gemm_waves(NB) / 4;  // waves per row-block
+  constexpr int SBW = 4 / HALVES;             // 16-row blocks per wave
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float tile_max[TOK][2];   // raw form: per token, max |x| of each half tile
+  constexpr int WV = gemm_waves(NB);
+  constexpr int TPW = TOK / WV;        // raw form: token rows packed by each wave
   __shared__ float tile_sig[2][TOK];   // raw form: sig(n, t) of each activation buffer
-  __shared__ float tile_ss[TOK][2];    // raw form with RMSNorm: per token, sum x^2 of each half tile
   __shared__ float tok_inv[TOK];       // raw form with RMSNorm: 1/rms of each token (unsplit product)
-  float ss_acc = 0.f;                  // thread n < TOK: token n's sum of x^2 over this workgroup's tiles
+  float ss_acc[TPW];                   // raw form with RMSNorm: sum of x^2 of the wave's token rows over
+#pragma unroll                         // this workgroup's tiles (the same value in every lane)
+  for (int jt = 0; jt < TPW; ++jt) ss_acc[jt] = 0.f;
   const unsigned tid = threadIdx.x, lane = tid & 63u;
-  const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6);
+  const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6) / HALVES;
+  const int sb0 = (int)((tid >> 6) % HALVES) * SBW;  // first 16-row block of this wave
   const bool live = rb < nrb;
   const int tok0 = (int)blockIdx.y * TOK;
   const unsigned r = lane & 15u, q = lane >> 4;
   const int t_begin = (int)blockIdx.z * tps, t_end = min(ntiles, t_begin + tps);
   y += (size_t)blockIdx.z * zstride;
   if (gridDim.z > 1) accumulate = 0;
-  f32x4 acc[4][NB];
+  f32x4 acc[SBW][NB];
 #pragma unroll
-  for (int sb = 0; sb < 4; ++sb)
+  for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -238,32 +302,32 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   // when NB > 1: two would not fit beside a second workgroup).  A tile past the range reloads the
   // last one (never used), so that no loaded value becomes a phi.
   constexpr int NBUF = NB == 1 ? 2 : 1;
-  constexpr int XV = 2 * TOK * 64 / 256;  // 16-byte activation chunks per thread and tile
-  auto load_unit = [&](int t, u32x4 (&cv)[4], unsigned (&cs)[4]) {
+  constexpr int XV = 2 * TOK * 64 / NT;  // 16-byte activation chunks per thread and tile
+  auto load_unit = [&](int t, u32x4 (&cv)[SBW], unsigned (&cs)[SBW]) {
     const int tc = t < t_end ? t : t_end - 1;
     const uint8_t* unit = W + ((size_t)(live ? rb : 0) * ntiles + tc) * kUnitBytes;
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      const unsigned L = 16u * sb + r, c = (unsigned)sb ^ q;
+    for (int sb = 0; sb < SBW; ++sb) {
+      const unsigned L = 16u * (sb0 + sb) + r, c = (unsigned)(sb0 + sb) ^ q;
       cv[sb] = *reinterpret_cast<const u32x4*>(unit + ((size_t)c * 64 + L) * 16);
       const unsigned short* scp = reinterpret_cast<const unsigned short*>(unit + kUnitSignBytes + (size_t)L * 8);
       cs[sb] = scp[c];
     }
   };
-  // Raw form: chunk j of a thread is float4 column c = tid & 127 of token (tid >> 7) + 2j (the TOK
-  // tokens' 128 float4 per tile, XV = TOK / 2 of them per thread); wave w covers half (w & 1) of the
-  // columns of its tokens.
+  // Raw form: token row n = w + WV·jt of the tile is loaded and packed by wave w alone (its own
+  // maxima and sums, no exchange between waves); chunks 2jt and 2jt + 1 of a lane are the float4 at
+  // columns 4·lane and 256 + 4·lane of that row.
   auto load_x = [&](int t, u32x4 (&xv)[XV]) {
     const int tc = t < t_end ? t : t_end - 1;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       if constexpr (RAW) {
-        const int n = tok0 + (int)(tid >> 7) + 2 * j;
-        const int64_t col = (int64_t)tc * kTileCols + 4 * (tid & 127u);
+        const int n = tok0 + (int)(tid >> 6) + WV * (j >> 1);
+        const int64_t col = (int64_t)tc * kTileCols + 4 * lane + 256 * (j & 1);
         xv[j] = n < n_tok && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
                                        : u32x4{0u, 0u, 0u, 0u};
       } else {
-        const int i = (int)tid + 256 * j;
+const int i = (int)tid + NT * j;
         const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
         xv[j] = *reinterpret_cast<const u32x4*>((part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp +
                                                 (size_t)tc * kTileCols + 8 * c);
@@ -272,59 +336,49 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   };
   auto put_x = [&](int b, u32x4 (&xv)[XV], int t_x) {
     if constexpr (RAW) {
-      // token (tid >> 7) + 2j is the same for a whole wave: token rows past n_tok are skipped (their
-      // product columns are never stored)
-      const unsigned half = (tid >> 6) & 1u;
+      // token rows past n_tok are skipped (wave-uniform; their product columns are never stored)
+      const unsigned wave = tid >> 6;
       const bool normed = x.nw != nullptr;
-      float4 nw4 = make_float4(1.f, 1.f, 1.f, 1.f);
+      float4 nw0 = make_float4(1.f, 1.f, 1.f, 1.f), nw1 = nw0;
       if (normed) {
-        const int64_t col = (int64_t)t_x * kTileCols + 4 * (tid & 127u);
-        if (col < x.K) nw4 = *reinterpret_cast<const float4*>(x.nw + col);
+        const int64_t col = (int64_t)t_x * kTileCols + 4 * lane;
+        if (col < x.K) nw0 = *reinterpret_cast<const float4*>(x.nw + col);
+        if (col + 256 < x.K) nw1 = *reinterpret_cast<const float4*>(x.nw + col + 256);
       }
 #pragma unroll
-      for (int j = 0; j < XV; ++j) {
-        if (tok0 + (int)(tid >> 7) + 2 * j >= n_tok) continue;
-        float4 v = __builtin_bit_cast(float4, xv[j]);
-        if (normed) {
-          const float q = wave_sumsq4(v);
-          if (lane == 0) tile_ss[(tid >> 7) + 2 * j][half] = q;
-          v = make_float4(v.x * nw4.x, v.y * nw4.y, v.z * nw4.z, v.w * nw4.w);
-          xv[j] = __builtin_bit_cast(u32x4, v);
-        }
-        const float m = wave_max_abs4(v);
-        if (lane == 0) tile_max[(tid >> 7) + 2 * j][half] = m;
-      }
-      __syncthreads();
-      if (normed && (int)tid < TOK && tok0 + (int)tid < n_tok && t_x < t_end) ss_acc += tile_ss[tid][0] + tile_ss[tid][1];
-#pragma unroll
-      for (int j = 0; j < XV; ++j) {
-        const int n = (int)(tid >> 7) + 2 * j;
+      for (int jt = 0; jt < TPW; ++jt) {
+        const int n = (int)wave + WV * jt;
         if (tok0 + n >= n_tok) continue;
-        const float sg = pack_sig(fmaxf(tile_max[n][0], tile_max[n][1]));
-        const float rs = 1.0f / sg;  // exact: a power of two
-        const float4 v = __builtin_bit_cast(float4, xv[j]);
-        ushort4 h, l;
-        pack_split(v.x * rs, h.x, l.x);
-        pack_split(v.y * rs, h.y, l.y);
-        pack_split(v.z * rs, h.z, l.z);
-        pack_split(v.w * rs, h.w, l.w);
-        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad + 8 * (tid & 127u);
-        *reinterpret_cast<ushort4*>(row) = h;
-        *reinterpret_cast<ushort4*>(row + (size_t)TOK * kGemmRowPad) = l;
-        if ((tid & 127u) == 0) tile_sig[b][n] = sg;
+        float4 v0 = __builtin_bit_cast(float4, xv[2 * jt]), v1 = __builtin_bit_cast(float4, xv[2 * jt + 1]);
+        if (normed) {
+          const float q = wave_sumsq8(v0, v1);
+          if (t_x < t_end) ss_acc[jt] += q;
+          v0 = make_float4(v0.x * nw0.x, v0.y * nw0.y, v0.z * nw0.z, v0.w * nw0.w);
+          v1 = make_float4(v1.x * nw1.x, v1.y * nw1.y, v1.z * nw1.z, v1.w * nw1.w);
+        }
+        const int e = pack_exp(wave_max_abs8(v0, v1));
+        uint2 h0, l0, h1, l1;
+        pack_split4(v0, e, h0, l0);
+        pack_split4(v1, e, h1, l1);
+        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad + 8 * lane;
+        *reinterpret_cast<uint2*>(row) = h0;
+        *reinterpret_cast<uint2*>(row + 512) = h1;
+        *reinterpret_cast<uint2*>(row + (size_t)TOK * kGemmRowPad) = l0;
+        *reinterpret_cast<uint2*>(row + (size_t)TOK * kGemmRowPad + 512) = l1;
+        if (lane == 0) tile_sig[b][n] = ldexpf(1.0f, e);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < XV; ++j) {
-        const int i = (int)tid + 256 * j;
+        const int i = (int)tid + NT * j;
         const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
         *reinterpret_cast<u32x4*>(smem + (size_t)b * (2 * TOK * kGemmRowPad) +
                                   ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
       }
     }
   };
-  u32x4 cv[4];
-  unsigned cs[4];
+  u32x4 cv[SBW];
+  unsigned cs[SBW];
   u32x4 xv[XV];
   load_unit(t_begin, cv, cs);
   load_x(t_begin, xv);
@@ -332,17 +386,18 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
   __syncthreads();
   for (int t = t_begin; t < t_end; ++t) {
     const int b = NBUF == 2 ? (t - t_begin) & 1 : 0;
-    u32x4 cvn[4];
-    unsigned csn[4];
+    const bool more = t + 1 < t_end;  // uniform: the activations of a next tile are loaded and packed
+    u32x4 cvn[SBW];
+    unsigned csn[SBW];
     load_unit(t + 1, cvn, csn);
-    if (NBUF == 2) load_x(t + 1, xv);
+    if (NBUF == 2 && more) load_x(t + 1, xv);
     if (live) {
-      unsigned wn[4][4], s2[4];
+      unsigned wn[SBW][4], s2[SBW];
 #pragma unroll
-      for (int sb = 0; sb < 4; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
-      f32x4 at[4][NB];  // raw form: this tile's products, scaled by sig(n, t) after the tile
+      for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
+      f32x4 at[SBW][NB];  // raw form: this tile's products, scaled by sig(n, t) after the tile
 #pragma unroll
-      for (int sb = 0; sb < 4; ++sb)
+      for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
       // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
@@ -355,7 +410,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       xh_[nb] = *reinterpret_cast<const f16x8*>(bh + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
       xl_[nb] = *reinterpret_cast<const f16x8*>(bl + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
     }                                                                                                 \
-    _Pragma("unroll") for (int sb = 0; sb < 4; ++sb) {                                                \
+    _Pragma("unroll") for (int sb = 0; sb < SBW; ++sb) {                                              \
       const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
       _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                             \
         at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], at[sb][nb], 0, 0, 0);         \
@@ -372,7 +427,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
       for (int nb = 0; nb < NB; ++nb) {
         const float sg = RAW ? tile_sig[b][16 * nb + (int)r] : 1.0f;
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
+        for (int sb = 0; sb < SBW; ++sb) {
           if constexpr (RAW) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[sb][nb][v] = __builtin_fmaf(sg, at[sb][nb][v], acc[sb][nb][v]);
@@ -382,6 +437,7 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
         }
       }
     }
+    if (!more) break;  // the epilogue reads no LDS that another wave still writes
     if (NBUF == 2) {
       put_x(b ^ 1, xv, t + 1);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
     } else {
@@ -391,19 +447,23 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
     }
     __syncthreads();
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
+    for (int sb = 0; sb < SBW; ++sb) {
       cv[sb] = cvn[sb];
       cs[sb] = csn[sb];
     }
   }
   // raw form with RMSNorm: each token's 1/rms (every tile seen) or this split's sums of squares
   if (RAW && x.nw != nullptr) {
-    if (gridDim.z == 1) {
-      if ((int)tid < TOK) tok_inv[tid] = 1.0f / sqrtf(ss_acc / (float)x.K + x.eps);
-      __syncthreads();
-    } else if (blockIdx.x == 0 && (int)tid < TOK && tok0 + (int)tid < n_tok) {
-      x.ssq[(size_t)blockIdx.z * x.ssq_ld + tok0 + tid] = ss_acc;
+#pragma unroll
+    for (int jt = 0; jt < TPW; ++jt) {
+      const int n = (int)(tid >> 6) + WV * jt;
+      if (lane != 0 || tok0 + n >= n_tok) continue;
+      if (gridDim.z == 1)
+        tok_inv[n] = 1.0f / sqrtf(ss_acc[jt] / (float)x.K + x.eps);
+      else if (blockIdx.x == 0)
+        x.ssq[(size_t)blockIdx.z * x.ssq_ld + tok0 + n] = ss_acc[jt];
     }
+    if (gridDim.z == 1) __syncthreads();
   }
   if (!live) return;
   // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
@@ -414,8 +474,8 @@ __global__ __launch_bounds__(256, 2) void q1_gemm_kernel(const uint8_t* __restri
     const float sg = RAW ? (x.nw != nullptr && gridDim.z == 1 ? tok_inv[16 * nb + (int)r] : 1.0f) : x.sig[n];
     float* yr = y + (size_t)n * ldy;
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      const int64_t row0 = rb * kRowBlock + 16 * sb + 4 * (int)q;
+    for (int sb = 0; sb < SBW; ++sb) {
+      const int64_t row0 = rb * kRowBlock + 16 * (sb0 + sb) + 4 * (int)q;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t row = row0 + v;

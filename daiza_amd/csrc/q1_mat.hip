@@ -282,7 +282,8 @@ hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const fl
 }
 
 // Workgroups wanted in flight (two per CU): a product with fewer splits its K tiles over
-// blockIdx.z and sums the partials in a second pass.
+// blockIdx.z and sums the partials in a second pass, with as many splits as keep the grid within
+// one round of resident workgroups (a second round would start only as the first ends).
 constexpr int kGemmMinWgs = 512;
 
 int gemm_splits(const Q1Dev& W, int n, int* tps) {
@@ -290,7 +291,7 @@ int gemm_splits(const Q1Dev& W, int n, int* tps) {
   const int64_t wgs = ((W.nrb + 3) / 4) * ((n + 16 * nb - 1) / (16 * nb));
   const int nt = (int)W.ntiles;
   int S = 1;
-  if (wgs < kGemmMinWgs && nt > 1) S = (int)std::min<int64_t>(nt, (kGemmMinWgs + wgs - 1) / wgs);
+  if (wgs < kGemmMinWgs && nt > 1) S = (int)std::min<int64_t>(nt, std::max<int64_t>(1, kGemmMinWgs / wgs));
   *tps = (nt + S - 1) / S;
   return (nt + *tps - 1) / *tps;
 }
@@ -348,17 +349,17 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
   const dim3 g1(gx_, 1, (unsigned)S), g2(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S);
   if (n <= 16) {
     if (raw)
-      hipLaunchKernelGGL((q1_gemm_kernel<1, true>), g1, dim3(256), gemm_shmem(1), s, W.data, W.rows, W.nrb,
+      hipLaunchKernelGGL((q1_gemm_kernel<1, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows, W.nrb,
                          (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
     else
-      hipLaunchKernelGGL((q1_gemm_kernel<1, false>), g1, dim3(256), gemm_shmem(1), s, W.data, W.rows, W.nrb,
+      hipLaunchKernelGGL((q1_gemm_kernel<1, false>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows, W.nrb,
                          (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   } else {
     if (raw)
-      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, true>), g2, dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows,
+      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, true>), g2, dim3(64 * gemm_waves(kGemmNB)), gemm_shmem(kGemmNB), s, W.data, W.rows,
                          W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
     else
-      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, false>), g2, dim3(256), gemm_shmem(kGemmNB), s, W.data, W.rows,
+      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, false>), g2, dim3(64 * gemm_waves(kGemmNB)), gemm_shmem(kGemmNB), s, W.data, W.rows,
                          W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   }
   hipError_t e = hipGetLastError();

@@ -282,8 +282,7 @@ hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const fl
 }
 
 // Workgroups wanted in flight (two per CU): a product with fewer splits its K tiles over
-// blockIdx.z and sums the partials in a second pass, with as many splits as keep the grid within
-// one round of resident workgroups (a second round would start only as the first ends).
+// blockIdx.z and sums the partials in a second pass.
 constexpr int kGemmMinWgs = 512;
 
 int gemm_splits(const Q1Dev& W, int n, int* tps) {
@@ -291,7 +290,7 @@ int gemm_splits(const Q1Dev& W, int n, int* tps) {
   const int64_t wgs = ((W.nrb + 3) / 4) * ((n + 16 * nb - 1) / (16 * nb));
   const int nt = (int)W.ntiles;
   int S = 1;
-  if (wgs < kGemmMinWgs && nt > 1) S = (int)std::min<int64_t>(nt, std::max<int64_t>(1, kGemmMinWgs / wgs));
+  if (wgs < kGemmMinWgs && nt > 1) S = (int)std::min<int64_t>(nt, (kGemmMinWgs + wgs - 1) / wgs);
   *tps = (nt + S - 1) / S;
   return (nt + *tps - 1) / *tps;
 }

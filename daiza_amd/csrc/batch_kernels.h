@@ -441,6 +441,143 @@ __global__ __launch_bounds__(256) void bt_attn_kernel(const float* __restrict__ 
   }
 }
 
+// Causal GQA attention of few tokens on the matrix cores, f32 operands (v_mfma_f32_16x16x4_f32: the
+// products and sums are f32, in another order than the reference's loop, attention.rs:149-203).
+// The n·GRP (token, q-head) rows of kv-head kvh, row ρ = t·GRP + g, are one matrix: wave w holds
+// rows 16w .. 16w+15 (n·GRP <= 64), so each cache row is read by one workgroup for every token.
+// Workgroup (z, kvh) takes positions [z·csz, (z+1)·csz) in blocks of 16 and writes the record
+// (m, l, o[256]) of each row to rec[t][h][z] for bt_attn_merge_kernel.  Per block:
+//   S^T = K_blk · Q^T: A = K rows (lane = position p0 + (lane & 15), dims 16j + 4(lane >> 4) + c
+//   in step 4j + c), B = the same dims of the wave's Q rows (registers); the result leaves lane
+//   (r, k) the scores of row 16w + r at positions p0 + 4k + i, so the online softmax of a row runs
+//   in the 4 lanes r, r+16, r+32, r+48, and those probabilities are already the A operand of
+//   O += P · V_blk in position order 4k + s (step s): no transpose through LDS.
+//   B of step s, tile (th, c): V[p0 + 4k + s][64th + 4r + c]; O tile (th, c) leaves lane (r, k)
+//   rows 16w + 4k + i at dim 64th + 4r + c.
+// Grid (nch, nkv), 256 threads, no LDS.
+template <int GRP>
+__global__ __launch_bounds__(256) void bt_attn_mfma_kernel(const float* __restrict__ qb, const float* __restrict__ kcache,
+                                                           const float* __restrict__ vcache, int max_ctx, int nq,
+                                                           int pos0, int n, int csz, int nch, float* __restrict__ rec) {
+  constexpr int HD = 256;
+  const int z = (int)blockIdx.x, kvh = (int)blockIdx.y;
+  const unsigned tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  const int ln = (int)(lane & 15u), lk = (int)(lane >> 4);
+  const int rows = n * GRP;
+  const int pbeg = z * csz, pend = min((z + 1) * csz, pos0 + n);  // the chunk's positions seen by anyone
+  // the softmax row of this lane: ρ = 16w + ln, visible positions [pbeg, ctx_r)
+  const int rho = 16 * (int)w + ln;
+  const bool rv = rho < rows;
+  const int ctx_r = rv ? min(pos0 + rho / GRP + 1, pend) : pbeg;
+  float4 q[16];  // Q[ρ][16j + 4lk .. +3]
+  {
+    const float* qr = qb + ((size_t)(rv ? rho / GRP : 0) * nq + kvh * GRP + (rv ? rho % GRP : 0)) * HD + 4 * lk;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) q[j] = rv ? *reinterpret_cast<const float4*>(qr + 16 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  f32x4 o[16];  // tile 4th + c
+#pragma unroll
+  for (int t = 0; t < 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  const float* kb = kcache + (size_t)kvh * max_ctx * HD;
+  const float* vb = vcache + (size_t)kvh * max_ctx * HD;
+  // A block's key and value rows are requested one block ahead (keys while the previous block's
+  // values are multiplied, values while its scores are formed), so that no matrix instruction waits
+  // for a load issued just before it.  Positions past the chunk are clamped to its last one
+  // (written, finite) and masked.
+  float4 kk[16], vv[16];  // kk[j]: K[p][16j + 4lk ..]; vv[4s + th]: V[p0 + 4lk + s][64th + 4ln ..]
+  auto load_k = [&](int pb) {
+    const float* kr = kb + (size_t)min(pb + ln, pend - 1) * HD + 4 * lk;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kk[j] = *reinterpret_cast<const float4*>(kr + 16 * j);
+  };
+  auto load_v = [&](int pb) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float* vr = vb + (size_t)min(pb + 4 * lk + s, pend - 1) * HD + 4 * ln;
+#pragma unroll
+      for (int th = 0; th < 4; ++th) vv[4 * s + th] = *reinterpret_cast<const float4*>(vr + 64 * th);
+    }
+  };
+  if (pbeg < pend) {
+    load_k(pbeg);
+    load_v(pbeg);
+  }
+  for (int p0 = pbeg; p0 < pend; p0 += 16) {
+    const int pn = p0 + 16 < pend ? p0 + 16 : p0;  // the next block (the last one reloads itself)
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j].x, q[j].x, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j + 1].x, q[j + 1].x, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j].y, q[j].y, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j + 1].y, q[j + 1].y, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j].z, q[j].z, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j + 1].z, q[j + 1].z, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j].w, q[j].w, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j + 1].w, q[j + 1].w, s1, 0, 0, 0);
+    }
+    load_k(pn);
+    float sc[4], bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = p0 + 4 * lk + i < ctx_r ? s0[i] + s1[i] : -INFINITY;
+      bm = fmaxf(bm, sc[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float mn = fmaxf(m, bm);
+    // a row with no visible position yet keeps m = -inf: its factors are 0 and 1 by definition
+    const float al = mn == -INFINITY ? 1.0f : expf(m - mn);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = sc[i] == -INFINITY ? 0.f : expf(sc[i] - mn);
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l = l * al + ps;
+    m = mn;
+    // the O rows of this lane are 16w + 4lk + i: their factors live in lanes 4lk + i (skipped when
+    // no row of the wave has a new maximum: every factor is then exactly 1)
+    if (__builtin_amdgcn_ballot_w64(al != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = __shfl(al, 4 * lk + i);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) o[t][i] *= a;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int th = 0; th < 4; ++th) {
+        const float4 v4 = vv[4 * s + th];
+        o[4 * th + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[s], v4.x, o[4 * th + 0], 0, 0, 0);
+        o[4 * th + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[s], v4.y, o[4 * th + 1], 0, 0, 0);
+        o[4 * th + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[s], v4.z, o[4 * th + 2], 0, 0, 0);
+        o[4 * th + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[s], v4.w, o[4 * th + 3], 0, 0, 0);
+      }
+    load_v(pn);
+  }
+  // records: (m, l) of row ρ from lanes lk = 0; o rows 16w + 4lk + i, dims 64th + 4ln .. +3
+  if (lk == 0 && rv) {
+    float* rr = rec + (((size_t)(rho / GRP) * nq + kvh * GRP + rho % GRP) * nch + z) * (2 + HD);
+    rr[0] = m;
+    rr[1] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ro = 16 * (int)w + 4 * lk + i;
+    if (ro >= rows) continue;
+    float* rr = rec + (((size_t)(ro / GRP) * nq + kvh * GRP + ro % GRP) * nch + z) * (2 + HD) + 2 + 4 * ln;
+#pragma unroll
+    for (int th = 0; th < 4; ++th)
+      *reinterpret_cast<float4*>(rr + 64 * th) = make_float4(o[4 * th][i], o[4 * th + 1][i], o[4 * th + 2][i], o[4 * th + 3][i]);
+  }
+}
+
 // Merge of the position chunks of bt_attn_kernel (records with l = 0 held no position), then
 // o·sigmoid(gate).  Grid (n, nq), 256 threads (one output dim each); nch <= 256.  Thread z < nch
 // brings chunk z's (m, l) to LDS, so that every chunk's weight exp(m_z - M) is formed once, and the

@@ -24,6 +24,7 @@ constexpr int kLutBytes = 256 * kTilePos * 4;        // 64 KiB: f32 [256 sign-by
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // matrix-core accumulators
 
 // DeltaNet state: [v-head][row i][column j] (row-major S[i][j]).  A thread holding 16 consecutive
 // columns of one row moves them as four 16-byte words, so the 8 threads of a row cover 512

@@ -1244,6 +1244,31 @@ static hipError_t launch_bt_attn(int grp, int n, int nkv, int nch, hipStream_t s
 #undef DZ_ATTN
 }
 
+// The few-token attention on the matrix cores (every token of a kv-head in one workgroup), grid
+// (nch, nkv), with about one workgroup per CU (one wave per SIMD: the kernel holds its block's
+// keys and values a block ahead in registers).
+static hipError_t launch_bt_attn_mfma(int grp, int nkv, int nch, hipStream_t s, const float* qb, const float* kc,
+                                      const float* vc, int max_ctx, int nq, int pos0, int n, int csz, float* rec) {
+  const dim3 g((unsigned)nch, (unsigned)nkv);
+#define DZ_ATTN_M(G_) return launch(bt_attn_mfma_kernel<G_>, g, dim3(256), s, qb, kc, vc, max_ctx, nq, pos0, n, csz, nch, rec)
+  switch (grp) {
+    case 1: DZ_ATTN_M(1);
+    case 2: DZ_ATTN_M(2);
+    case 3: DZ_ATTN_M(3);
+    case 4: DZ_ATTN_M(4);
+    case 6: DZ_ATTN_M(6);
+    case 8: DZ_ATTN_M(8);
+    default: return hipErrorInvalidValue;
+  }
+#undef DZ_ATTN_M
+}
+
+static int bt_attn_mfma_chunks(int nkv, int ctx_max, int* csz) {
+  int nch = std::max(1, std::min(256, (256 + nkv - 1) / nkv));
+  *csz = ((ctx_max + nch - 1) / nch + 15) / 16 * 16;  // whole blocks of 16 positions
+  return (ctx_max + *csz - 1) / *csz;
+}
+
 // Position chunks of the chunk's attention: enough workgroups to fill the device when the chunk
 // has few tokens (speculative verify at long context), one chunk for a long prefill.
 // A chunk of several positions is a whole number of 256-position rounds (the kernel's 4 waves take
@@ -1335,16 +1360,25 @@ static int bt_forward(dz_ctx* x, const uint32_t* ids, int n, int out_rows, bool 
                           (const float*)x->bt.yin, ld_in, (int)c.n_head, (int)c.n_head_kv, (const float*)l.q_norm,
                           (const float*)l.k_norm, c.rms_eps, (const float*)x->rope, (int)c.rope_dim, p0, x->bt.qb,
                           x->bt.gate, kc, vc, (int)c.max_ctx));
+      // few tokens (verify): all of a kv-head's query rows in one matrix-core workgroup, chunk records
+      // always merged; otherwise token groups per workgroup
+      const int grp = (int)(c.n_head / c.n_head_kv);
+      const bool mf = n * grp <= 64;
       int csz;
-      const int nch = bt_attn_chunks(n, (int)c.n_head_kv, p0 + n, &csz);
+      const int nch = mf ? bt_attn_mfma_chunks((int)c.n_head_kv, p0 + n, &csz)
+                         : bt_attn_chunks(n, (int)c.n_head_kv, p0 + n, &csz);
       float* rec = nullptr;
-      if (nch > 1) {
+      if (nch > 1 || mf) {
         if ((rc = x->bt.arec.reserve((size_t)n * c.n_head * nch * (2 + c.head_dim) * sizeof(float)))) return rc;
         rec = static_cast<float*>(x->bt.arec.ptr);
       }
-      DZ_HIP_CHECK(launch_bt_attn(c.n_head / c.n_head_kv, n, (int)c.n_head_kv, nch, s, x->bt.qb, x->bt.gate, kc, vc,
-                                  (int)c.max_ctx, (int)c.n_head, p0, x->bt.gy, csz, rec));
-      if (nch > 1)
+      if (mf)
+        DZ_HIP_CHECK(launch_bt_attn_mfma(grp, (int)c.n_head_kv, nch, s, x->bt.qb, kc, vc, (int)c.max_ctx, (int)c.n_head,
+                                         p0, n, csz, rec));
+      else
+        DZ_HIP_CHECK(launch_bt_attn(grp, n, (int)c.n_head_kv, nch, s, x->bt.qb, x->bt.gate, kc, vc, (int)c.max_ctx,
+                                    (int)c.n_head, p0, x->bt.gy, csz, rec));
+      if (nch > 1 || mf)
         DZ_HIP_CHECK(launch(bt_attn_merge_kernel, dim3(nb, (unsigned)c.n_head), dim3(256), s, (const float*)rec, nch,
                             (const float*)x->bt.gate, (int)c.n_head, x->bt.gy));
       if ((rc = bt_gemm(x, l.out_proj, x->bt.gy, qd, n, nullptr, x->bt.h, H, 1))) return rc;

@@ -26,7 +26,6 @@
 namespace dz {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup (wide form)
 constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup of the wide form, the padding of n

@@ -218,40 +218,45 @@ __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x
   if (tid == 0) sig[n] = live ? s : 0.f;
 }
 
-// Sign byte s of a restored chunk (4 dwords, bit set = sign bit of the f16 value set, after the
-// fix-up of restore_chunk) as the eight f16 operand values: element e has magnitude |scale|
-// (s2 = |scale| in both halves) and the sign of bit e of byte s.  With b the byte and
-// Y = b | b << 15, Y << (15 - 2p) holds bit 2p at position 15 and bit 2p+1 at position 31, so a
-// pair of elements costs a shift and an and-or.
+// Sign byte s of a restored chunk (4 dwords in position order) as the eight f16 operand values:
+// element e is +scale where bit e of byte s is set, else -scale.  With b the byte and
+// Y = b | b << 15, Y << (15 - 2p) holds bit 2p at position 15 and bit 2p+1 at position 31; s2x is
+// the scale's f16 bits in both halves with both sign bits flipped, so a pair of elements costs a
+// shift and one and-xor: ((Y << (15 - 2p)) & 0x80008000) ^ s2x.
 template <int S>
-__device__ __forceinline__ f16x8 expand_signs(const unsigned (&wn)[4], unsigned s2) {
+__device__ __forceinline__ f16x8 expand_signs(const unsigned (&wn)[4], unsigned s2x) {
   const unsigned b = __builtin_amdgcn_ubfe(wn[S >> 2], 8 * (S & 3), 8);
   const unsigned y = (b << 15) | b;
   unsigned d[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) d[p] = ((y << (15 - 2 * p)) & 0x80008000u) | s2;
+  for (int p = 0; p < 4; ++p) d[p] = ((y << (15 - 2 * p)) & 0x80008000u) ^ s2x;
   u32x4 v = {d[0], d[1], d[2], d[3]};
   return __builtin_bit_cast(f16x8, v);
 }
 
-// Chunk of row L = 16·sb + r holding group q, bytes restored to position order and sign bits
-// turned into "bit set = sign bit of the f16 value set" (the stored bit set means +scale).
-__device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, unsigned r, unsigned (&wn)[4],
-                                              unsigned& s2) {
-  // stored byte i <-> position 16q + (i ^ r): first within dwords (i & 3), then across dwords
-  const unsigned sel = 0x03020100u ^ (0x01010101u * (r & 3u));
+// v_cndmask_b32 with a constant lane mask: mask bit of this lane set ? b : a.
+template <unsigned long long M>
+__device__ __forceinline__ unsigned lane_select(unsigned a, unsigned b) {
+  unsigned d;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(M));
+  return d;
+}
+
+// Chunk of row L = 16·sb + r holding group q, bytes restored to position order: stored byte i holds
+// position i ^ r, so within each dword the bytes move by r & 3 (one v_perm with the lane's
+// selector sel), and the dwords by r >> 2, in two stages of lane selects whose masks are constants
+// (bits 2 and 3 of the lane index are those of r).  s2x: see expand_signs.
+__device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, unsigned sel, unsigned (&wn)[4],
+                                              unsigned& s2x) {
   unsigned u[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) u[k] = __builtin_amdgcn_perm(v[k], v[k], sel);
-  const bool x1 = (r >> 2) & 1u, x2 = (r >> 3) & 1u;
   unsigned t[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) t[k] = x1 ? u[k ^ 1] : u[k];
-  // sign of +scale when the bit is set, of -scale when clear: f16 sign bit = bit ^ !sign(scale)
-  const unsigned flip = (sc_bits & 0x8000u) ? 0u : 0xFFFFFFFFu;
+  for (int k = 0; k < 4; ++k) t[k] = lane_select<0xF0F0F0F0F0F0F0F0ull>(u[k], u[k ^ 1]);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) wn[k] = (x2 ? t[k ^ 2] : t[k]) ^ flip;
-  s2 = (sc_bits & 0x7FFFu) * 0x00010001u;
+  for (int k = 0; k < 4; ++k) wn[k] = lane_select<0xFF00FF00FF00FF00ull>(t[k], t[k ^ 2]);
+  s2x = ((sc_bits & 0xFFFFu) * 0x00010001u) ^ 0x80008000u;
 }
 
 // Grid (ceil(nrb / 4), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB) bytes of LDS.
@@ -286,6 +291,7 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
   const bool live = rb < nrb;
   const int tok0 = (int)blockIdx.y * TOK;
   const unsigned r = lane & 15u, q = lane >> 4;
+  const unsigned psel = 0x03020100u ^ (0x01010101u * (r & 3u));  // restore_chunk's byte selector
   const int t_begin = (int)blockIdx.z * tps, t_end = min(ntiles, t_begin + tps);
   y += (size_t)blockIdx.z * zstride;
   if (gridDim.z > 1) accumulate = 0;
@@ -393,7 +399,7 @@ const int i = (int)tid + NT * j;
     if (live) {
       unsigned wn[SBW][4], s2[SBW];
 #pragma unroll
-      for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], r, wn[sb], s2[sb]);
+      for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], psel, wn[sb], s2[sb]);
       f32x4 at[SBW][NB];  // raw form: this tile's products, scaled by sig(n, t) after the tile
 #pragma unroll
       for (int sb = 0; sb < SBW; ++sb)

@@ -110,16 +110,20 @@ struct DnRecord {
 // columns j = 16·(tid & 7) .. +16 of S[vh][i][j] in registers (64 contiguous bytes per thread); the 8
 // threads of a row sum with DPP.
 // Per token: g = ssm_a·softplus(alpha + dt_bias), decay = exp(g), beta = sigmoid(b); s *= decay;
-// kv = s·k; d = (v_i - kv)·beta; s += d·k; y_i = s·q.  The next token's inputs are loaded while
-// this one computes.  With rec == null the state is written back at the end; otherwise it is left
-// as it was and every token's (decay, d, k) is recorded.
+// kv = s·k; d = (v_i - kv)·beta; s += d·k; y_i = s·q.  The inputs of 16 tokens at a time (q and k
+// of the k-head, v of the workgroup's rows, alpha, beta) are staged in LDS by the whole workgroup,
+// the next 16 requested while these compute: one load latency per 16 tokens instead of one per
+// token.  With rec == null the state is written back at the end; otherwise it is left as it was
+// and every token's (decay, d, k) is recorded.
 __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ yin, int64_t ldin,
                                                       const float* __restrict__ cout, int64_t qkvd,
                                                       const float* __restrict__ qk, int n, int nkh, int nvh,
                                                       int64_t off_a, int64_t off_b, const float* __restrict__ ssm_a,
                                                       const float* __restrict__ dt_bias, float* __restrict__ state,
                                                       float* __restrict__ y, DnRecord rec) {
-  constexpr int HD = 128;
+  constexpr int HD = 128, G = 16;
+  __shared__ __align__(16) float sqk[G][2 * HD];  // token's q then k of this k-head
+  __shared__ float sv[G][32], sab[G][2];
   const unsigned tid = threadIdx.x;
   const int vh = blockIdx.x >> 2, quarter = blockIdx.x & 3, kh = vh % nkh;
   const int i = quarter * 32 + (int)(tid >> 3), js = (int)(tid & 7u);
@@ -128,65 +132,81 @@ __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ 
   float s[16];
   state_row_load(S, s);
   const float A = ssm_a[vh], dtb = dt_bias[vh];
-  auto load = [&](int t, float4 (&k4)[4], float4 (&q4)[4], float& v, float& al, float& be) {
-    const float* qr = qk + (size_t)t * 2 * kdim + (size_t)kh * HD + 16 * js;
+  // staging of tokens [g0, g0 + G): thread (tt = tid >> 4, part = tid & 15) takes 16 of token tt's
+  // 256 q|k values, 2 of its v rows, and (tid < 32) one alpha or beta
+  const int st = (int)(tid >> 4), sp = (int)(tid & 15u);
+  float4 gq[4];
+  float gv0, gv1, gab;
+  auto gload = [&](int g0) {
+    const int t = min(g0 + st, n - 1);
+    const float* src = qk + (size_t)t * 2 * kdim + (sp < 8 ? (size_t)kh * HD + 16 * sp : kdim + (size_t)kh * HD + 16 * (sp - 8));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      q4[c] = *reinterpret_cast<const float4*>(qr + 4 * c);
-      k4[c] = *reinterpret_cast<const float4*>(qr + kdim + 4 * c);
-    }
-    v = cout[(size_t)t * qkvd + 2 * kdim + (int64_t)vh * HD + i];
-    al = yin[(size_t)t * ldin + off_a + vh];
-    be = yin[(size_t)t * ldin + off_b + vh];
+    for (int c = 0; c < 4; ++c) gq[c] = *reinterpret_cast<const float4*>(src + 4 * c);
+    const float* vr = cout + (size_t)t * qkvd + 2 * kdim + (int64_t)vh * HD + quarter * 32 + 2 * sp;
+    gv0 = vr[0];
+    gv1 = vr[1];
+    const int ta = min(g0 + (int)(tid & 15u), n - 1);
+    gab = tid < 32 ? yin[(size_t)ta * ldin + (tid < 16 ? off_a : off_b) + vh] : 0.f;
   };
-  float4 kc[4], qc[4];
-  float vc, alc, bec;
-  load(0, kc, qc, vc, alc, bec);
-  for (int t = 0; t < n; ++t) {
-    float4 kn[4], qn[4];
-    float vn, aln, ben;
-    load(t + 1 < n ? t + 1 : t, kn, qn, vn, aln, ben);
-    const float x = alc + dtb;
-    const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
-    const float decay = expf(A * sp);
-    const float beta = sigmoidf_(bec);
-    const float* kf = reinterpret_cast<const float*>(kc);
-    const float* qf = reinterpret_cast<const float*>(qc);
-    float kvp = 0.f;
+  auto gstore = [&]() {
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      s[jj] *= decay;
-      kvp = __builtin_fmaf(s[jj], kf[jj], kvp);
-    }
-    const float kv = lane8_sum(kvp);
-    const float d = (vc - kv) * beta;
-    float yp = 0.f;
+    for (int c = 0; c < 4; ++c) *reinterpret_cast<float4*>(&sqk[st][16 * sp + 4 * c]) = gq[c];
+    sv[st][2 * sp] = gv0;
+    sv[st][2 * sp + 1] = gv1;
+    if (tid < 32) sab[tid & 15u][tid >> 4] = gab;
+  };
+  gload(0);
+  gstore();
+  __syncthreads();
+  for (int g0 = 0; g0 < n; g0 += G) {
+    const bool more = g0 + G < n;
+    if (more) gload(g0 + G);
+    const int gn = min(G, n - g0);
+    for (int tt = 0; tt < gn; ++tt) {
+      const int t = g0 + tt;
+      const float x = sab[tt][0] + dtb;
+      const float spl = x > 20.0f ? x : logf(1.0f + expf(x));
+      const float decay = expf(A * spl);
+      const float beta = sigmoidf_(sab[tt][1]);
+      float kf[16], qf[16];
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      s[jj] = __builtin_fmaf(d, kf[jj], s[jj]);
-      yp = __builtin_fmaf(s[jj], qf[jj], yp);
-    }
-    const float yy = lane8_sum(yp);
-    if (js == 0) {
-      y[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = yy;
-      if (rec.d) rec.d[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = d;
-    }
-    if (rec.d && tid == 0) rec.decay[(size_t)t * nvh + vh] = decay;
-    if (rec.d && vh < nkh && quarter == 0 && js == 0) {
-      // the key of k-head vh, written once: rows i < 32 of quarter 0 cover 32 of its 128 columns x 4
+      for (int c = 0; c < 4; ++c) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&sqk[tt][16 * js + 4 * c]);
+        const float4 k4 = *reinterpret_cast<const float4*>(&sqk[tt][HD + 16 * js + 4 * c]);
+        qf[4 * c] = q4.x; qf[4 * c + 1] = q4.y; qf[4 * c + 2] = q4.z; qf[4 * c + 3] = q4.w;
+        kf[4 * c] = k4.x; kf[4 * c + 1] = k4.y; kf[4 * c + 2] = k4.z; kf[4 * c + 3] = k4.w;
+      }
+      float kvp = 0.f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        rec.k[(size_t)t * kdim + (int64_t)vh * HD + 4 * (i & 31) + c] =
-            qk[(size_t)t * 2 * kdim + kdim + (int64_t)vh * HD + 4 * (i & 31) + c];
-    }
+      for (int jj = 0; jj < 16; ++jj) {
+        s[jj] *= decay;
+        kvp = __builtin_fmaf(s[jj], kf[jj], kvp);
+      }
+      const float kv = lane8_sum(kvp);
+      const float d = (sv[tt][i & 31] - kv) * beta;
+      float yp = 0.f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      kc[c] = kn[c];
-      qc[c] = qn[c];
+      for (int jj = 0; jj < 16; ++jj) {
+        s[jj] = __builtin_fmaf(d, kf[jj], s[jj]);
+        yp = __builtin_fmaf(s[jj], qf[jj], yp);
+      }
+      const float yy = lane8_sum(yp);
+      if (js == 0) {
+        y[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = yy;
+        if (rec.d) rec.d[(size_t)t * nvh * HD + (int64_t)vh * HD + i] = d;
+      }
+      if (rec.d && tid == 0) rec.decay[(size_t)t * nvh + vh] = decay;
+      if (rec.d && vh < nkh && quarter == 0 && js == 0) {
+        // the key of k-head vh, written once: rows i < 32 of quarter 0 cover 32 of its 128 columns x 4
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rec.k[(size_t)t * kdim + (int64_t)vh * HD + 4 * (i & 31) + c] = sqk[tt][HD + 4 * (i & 31) + c];
+      }
     }
-    vc = vn;
-    alc = aln;
-    bec = ben;
+    if (more) {
+      __syncthreads();  // every thread is done with this group's inputs
+      gstore();
+      __syncthreads();
+    }
   }
   if (!rec.d) state_row_store(S, s);
 }

@@ -17,9 +17,15 @@
 // 4·blockIdx.x .. +3 (one wave each, or two waves each taking two 16-row blocks: gemm_waves) and
 // walks the tiles; in a 16-row block sb of a unit, lane (r, q)
 // (r = lane & 15, q = lane >> 4) takes the chunk of row 16·sb + r that holds group q, restores the
-// byte order in registers, and feeds sign byte s of that group as the eight f16 values of
-// v_mfma_f32_16x16x32_f16's A operand for step s (columns 128q + 8s + e).  The B operand, token
+// byte order in registers, and feeds the 32 sign bits of dword j of that group as the A operands
+// of steps 4j .. 4j+3 of v_mfma_f32_16x16x32_f16 (columns 128q + 32j .. +31).  The B operand, token
 // (lane & 15)'s activations at the same columns, is read from a tile staged in LDS.
+//
+// Column order inside a 32-column block.  Step 4j + s' takes the sign bits 15 - k and 31 - k of
+// dword j, k = 4s' + p for its f16 pairs p = 0..3, so that one shift of the whole dword serves a
+// pair: ((w << k) & 0x80008000).  The staged activations follow the same order: the 16-byte slot
+// s' of a 32-column block holds, as f16 elements 2p and 2p + 1, the columns 15 - 4s' - p and
+// 31 - 4s' - p of the block (pack_slot).  The order is a permutation of the K sum only.
 #pragma once
 #include "common.h"
 
@@ -101,13 +107,6 @@ __device__ __forceinline__ float wave_sumsq4(float4 v) {
   return (q0 + q1) + (q2 + q3);
 }
 
-// Splits one value (already divided by sig) into its f16 hi and lo parts.
-__device__ __forceinline__ void pack_split(float v, unsigned short& h, unsigned short& l) {
-  const _Float16 hi = (_Float16)v;
-  h = __builtin_bit_cast(unsigned short, hi);
-  l = __builtin_bit_cast(unsigned short, (_Float16)(v - (float)hi));
-}
-
 // The exponent e of the power of two sig = 2^e that pack_sig returns (0 for an all-zero or
 // non-finite row): x / sig = ldexp(x, -e), exact.
 __device__ __forceinline__ int pack_exp(float amax) {
@@ -120,15 +119,19 @@ __device__ __forceinline__ int pack_exp(float amax) {
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// Four values divided by 2^e and split into f16 hi and lo parts (round to nearest even, two values
-// per conversion on gfx950), packed in token-row order.
-__device__ __forceinline__ void pack_split4(float4 v, int e, uint2& h, uint2& l) {
-  const f32x2 a = {ldexpf(v.x, -e), ldexpf(v.y, -e)}, c = {ldexpf(v.z, -e), ldexpf(v.w, -e)};
-  const f16x2 ha = __builtin_convertvector(a, f16x2), hc = __builtin_convertvector(c, f16x2);
-  const f16x2 la = __builtin_convertvector(a - __builtin_convertvector(ha, f32x2), f16x2);
-  const f16x2 lc = __builtin_convertvector(c - __builtin_convertvector(hc, f32x2), f16x2);
-  h = make_uint2(__builtin_bit_cast(unsigned, ha), __builtin_bit_cast(unsigned, hc));
-  l = make_uint2(__builtin_bit_cast(unsigned, la), __builtin_bit_cast(unsigned, lc));
+// Eight values of a 32-column block, already divided by the token's power of two — a = columns
+// 4m .. 4m+3 and b = columns 16+4m .. 16+4m+3 (m = 0..3) — split into f16 hi and lo (round to
+// nearest even) and laid out as the block's 16-byte B-operand slot 3 - m: dword p = {a[3-p],
+// b[3-p]} (columns 15 - 4s' - p and 31 - 4s' - p of slot s' = 3 - m).
+__device__ __forceinline__ void pack_slot(float4 a, float4 b, u32x4& h, u32x4& l) {
+  const f32x2 p[4] = {{a.w, b.w}, {a.z, b.z}, {a.y, b.y}, {a.x, b.x}};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 hi = __builtin_convertvector(p[i], f16x2);
+    const f16x2 lo = __builtin_convertvector(p[i] - __builtin_convertvector(hi, f32x2), f16x2);
+    h[i] = __builtin_bit_cast(unsigned, hi);
+    l[i] = __builtin_bit_cast(unsigned, lo);
+  }
 }
 
 // max |v| over the 8 values of every lane of the wave, in every lane (as wave_max_abs4).
@@ -199,37 +202,37 @@ __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x
   const float inv = w ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
   const float s = live ? pack_sig(amax * inv) : 1.0f;
   const float rs = 1.0f / s;  // exact: s is a power of two
-  ushort4* oh = reinterpret_cast<ushort4*>(xh + (size_t)n * Kp);
-  ushort4* ol = reinterpret_cast<ushort4*>(xl + (size_t)n * Kp);
-  for (int64_t k = tid; k < Kp / 4; k += 256) {
-    ushort4 h = make_ushort4(0, 0, 0, 0), l = h;
-    if (k < K4) {
-      const float4 v = row[k];
-      float4 u = v;
-      if (w) u = make_float4((v.x * inv) * w4[k].x, (v.y * inv) * w4[k].y, (v.z * inv) * w4[k].z, (v.w * inv) * w4[k].w);
-      pack_split(u.x * rs, h.x, l.x);
-      pack_split(u.y * rs, h.y, l.y);
-      pack_split(u.z * rs, h.z, l.z);
-      pack_split(u.w * rs, h.w, l.w);
-    }
-    oh[k] = h;
-    ol[k] = l;
+  u32x4* oh = reinterpret_cast<u32x4*>(xh + (size_t)n * Kp);
+  u32x4* ol = reinterpret_cast<u32x4*>(xl + (size_t)n * Kp);
+  // slot k8 = 4J + m of the row: the float4 pair at columns 32J + 4m and 32J + 16 + 4m, written as
+  // slot 3 - m of block J (pack_slot); K is a multiple of 128, so a pair is wholly in or out
+  auto scaled = [&](int64_t k) {
+    const float4 v = row[k];
+    float4 u = v;
+    if (w) u = make_float4((v.x * inv) * w4[k].x, (v.y * inv) * w4[k].y, (v.z * inv) * w4[k].z, (v.w * inv) * w4[k].w);
+    return make_float4(u.x * rs, u.y * rs, u.z * rs, u.w * rs);
+  };
+  for (int64_t k8 = tid; k8 < Kp / 8; k8 += 256) {
+    const int64_t J = k8 >> 2, m = k8 & 3, ka = 8 * J + m;
+    u32x4 h = {0u, 0u, 0u, 0u}, l = h;
+    if (ka < K4) pack_slot(scaled(ka), scaled(ka + 4), h, l);
+    oh[4 * J + 3 - m] = h;
+    ol[4 * J + 3 - m] = l;
   }
   if (tid == 0) sig[n] = live ? s : 0.f;
 }
 
-// Sign byte s of a restored chunk (4 dwords in position order) as the eight f16 operand values:
-// element e is +scale where bit e of byte s is set, else -scale.  With b the byte and
-// Y = b | b << 15, Y << (15 - 2p) holds bit 2p at position 15 and bit 2p+1 at position 31; s2x is
-// the scale's f16 bits in both halves with both sign bits flipped, so a pair of elements costs a
-// shift and one and-xor: ((Y << (15 - 2p)) & 0x80008000) ^ s2x.
+// Step S's eight f16 operand values from dword j = S >> 2 of a restored chunk (32 sign bits in
+// column order): pair p takes bits 15 - k and 31 - k, k = 4·(S & 3) + p, to the sign positions 15
+// and 31 with one shift; an element is +scale where its bit is set, else -scale.  s2x is the
+// scale's f16 bits in both halves with both sign bits flipped, so a pair costs a shift and one
+// and-xor: ((w << k) & 0x80008000) ^ s2x (no shift for k = 0).
 template <int S>
 __device__ __forceinline__ f16x8 expand_signs(const unsigned (&wn)[4], unsigned s2x) {
-  const unsigned b = __builtin_amdgcn_ubfe(wn[S >> 2], 8 * (S & 3), 8);
-  const unsigned y = (b << 15) | b;
+  const unsigned w = wn[S >> 2];
   unsigned d[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) d[p] = ((y << (15 - 2 * p)) & 0x80008000u) ^ s2x;
+  for (int p = 0; p < 4; ++p) d[p] = ((w << (4 * (S & 3) + p)) & 0x80008000u) ^ s2x;
   u32x4 v = {d[0], d[1], d[2], d[3]};
   return __builtin_bit_cast(f16x8, v);
 }
@@ -321,14 +324,16 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
   };
   // Raw form: token row n = w + WV·jt of the tile is loaded and packed by wave w alone (its own
   // maxima and sums, no exchange between waves); chunks 2jt and 2jt + 1 of a lane are the float4 at
-  // columns 4·lane and 256 + 4·lane of that row.
+  // columns 32J + 4m and 32J + 16 + 4m of that row (J = lane >> 2, m = lane & 3): the two halves
+  // of the lane's B-operand slot (pack_slot).
+  const int64_t xcol = 32 * (lane >> 2) + 4 * (lane & 3u);
   auto load_x = [&](int t, u32x4 (&xv)[XV]) {
     const int tc = t < t_end ? t : t_end - 1;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       if constexpr (RAW) {
         const int n = tok0 + (int)(tid >> 6) + WV * (j >> 1);
-        const int64_t col = (int64_t)tc * kTileCols + 4 * lane + 256 * (j & 1);
+        const int64_t col = (int64_t)tc * kTileCols + xcol + 16 * (j & 1);
         xv[j] = n < n_tok && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
                                        : u32x4{0u, 0u, 0u, 0u};
       } else {
@@ -346,9 +351,11 @@ const int i = (int)tid + NT * j;
       const bool normed = x.nw != nullptr;
       float4 nw0 = make_float4(1.f, 1.f, 1.f, 1.f), nw1 = nw0;
       if (normed) {
-        const int64_t col = (int64_t)t_x * kTileCols + 4 * lane;
-        if (col < x.K) nw0 = *reinterpret_cast<const float4*>(x.nw + col);
-        if (col + 256 < x.K) nw1 = *reinterpret_cast<const float4*>(x.nw + col + 256);
+        const int64_t col = (int64_t)t_x * kTileCols + xcol;
+        if (col < x.K) {  // both halves of a 32-column block lie on the same side of K
+          nw0 = *reinterpret_cast<const float4*>(x.nw + col);
+          nw1 = *reinterpret_cast<const float4*>(x.nw + col + 16);
+        }
       }
 #pragma unroll
       for (int jt = 0; jt < TPW; ++jt) {
@@ -362,14 +369,13 @@ const int i = (int)tid + NT * j;
           v1 = make_float4(v1.x * nw1.x, v1.y * nw1.y, v1.z * nw1.z, v1.w * nw1.w);
         }
         const int e = pack_exp(wave_max_abs8(v0, v1));
-        uint2 h0, l0, h1, l1;
-        pack_split4(v0, e, h0, l0);
-        pack_split4(v1, e, h1, l1);
-        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad + 8 * lane;
-        *reinterpret_cast<uint2*>(row) = h0;
-        *reinterpret_cast<uint2*>(row + 512) = h1;
-        *reinterpret_cast<uint2*>(row + (size_t)TOK * kGemmRowPad) = l0;
-        *reinterpret_cast<uint2*>(row + (size_t)TOK * kGemmRowPad + 512) = l1;
+        u32x4 h, l;
+        pack_slot(make_float4(ldexpf(v0.x, -e), ldexpf(v0.y, -e), ldexpf(v0.z, -e), ldexpf(v0.w, -e)),
+                  make_float4(ldexpf(v1.x, -e), ldexpf(v1.y, -e), ldexpf(v1.z, -e), ldexpf(v1.w, -e)), h, l);
+        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad +
+                             64 * (lane >> 2) + 16 * (3u - (lane & 3u));
+        *reinterpret_cast<u32x4*>(row) = h;
+        *reinterpret_cast<u32x4*>(row + (size_t)TOK * kGemmRowPad) = l;
         if (lane == 0) tile_sig[b][n] = ldexpf(1.0f, e);
       }
     } else {

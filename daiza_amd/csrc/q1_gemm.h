@@ -271,11 +271,17 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
 // sig(n, t) per token and tile (max |x| of the tile's 512 columns in [2^13, 2^14), as pack_sig); a
 // tile's products are scaled by it as they are added: y = Σ_t sig(n, t) · W_t (hi + lo)(n, t).
 // That skips the separate packing pass for inputs that need no RMSNorm.
-template <int NB, bool RAW = false>
+//
+// Paired form (HL, raw form with n ≤ 8 tokens): one B operand carries both halves, columns 0..7
+// the hi rows and columns 8..15 the lo rows of the eight tokens, so each (step, block) takes one
+// matrix instruction instead of two; lanes r and r + 8 of the D layout hold the hi and lo sums of
+// token r & 7 (both scaled by that token's sig(n, t)), added once after the last tile.
+template <int NB, bool RAW = false, bool HL = false>
 __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
                                                          int ntiles, int tps, const GemmX x, int n_tok,
                                                          float* __restrict__ y, int64_t ldy, int64_t zstride,
                                                          int accumulate) {
+  static_assert(!HL || (NB == 1 && RAW), "the paired form is a raw form of one token block");
   constexpr int TOK = 16 * NB;
   constexpr int NT = 64 * gemm_waves(NB);  // threads
   constexpr int HALVES = gemm_waves(NB) / 4;  // waves per row-block
@@ -411,11 +417,19 @@ const int i = (int)tid + NT * j;
       for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
-      // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7
-      const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)r * kGemmRowPad + 256u * q;
+      // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7 (paired form:
+      // the hi row of token r for r < 8, else the lo row of token r - 8)
+      const unsigned brow = HL ? (r < 8u ? r : (unsigned)TOK + r - 8u) : r;
+      const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)brow * kGemmRowPad + 256u * q;
       const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
 #define DZ_GEMM_STEP(S)                                                                               \
-  {                                                                                                   \
+  if constexpr (HL) {                                                                                 \
+    const f16x8 xb_ = *reinterpret_cast<const f16x8*>(bh + 16 * (S));                                 \
+    _Pragma("unroll") for (int sb = 0; sb < SBW; ++sb) {                                              \
+      const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
+      at[sb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb_, at[sb][0], 0, 0, 0);                 \
+    }                                                                                                 \
+  } else {                                                                                            \
     f16x8 xh_[NB], xl_[NB];                                                                           \
     _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                               \
       xh_[nb] = *reinterpret_cast<const f16x8*>(bh + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
@@ -436,7 +450,7 @@ const int i = (int)tid + NT * j;
 #undef DZ_GEMM_STEP
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const float sg = RAW ? tile_sig[b][16 * nb + (int)r] : 1.0f;
+        const float sg = RAW ? tile_sig[b][16 * nb + (int)(HL ? r & 7u : r)] : 1.0f;
 #pragma unroll
         for (int sb = 0; sb < SBW; ++sb) {
           if constexpr (RAW) {
@@ -477,11 +491,17 @@ const int i = (int)tid + NT * j;
     if (gridDim.z == 1) __syncthreads();
   }
   if (!live) return;
+  if constexpr (HL) {  // lane r < 8 adds the lo sums of its token from lane r + 8
+#pragma unroll
+    for (int sb = 0; sb < SBW; ++sb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[sb][0][v] += __shfl_xor(acc[sb][0][v], 8, 16);
+  }
   // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int n = tok0 + 16 * nb + (int)r;
-    if (n >= n_tok) continue;
+    if (n >= n_tok || (HL && r >= 8u)) continue;
     const float sg = RAW ? (x.nw != nullptr && gridDim.z == 1 ? tok_inv[16 * nb + (int)r] : 1.0f) : x.sig[n];
     float* yr = y + (size_t)n * ldy;
 #pragma unroll

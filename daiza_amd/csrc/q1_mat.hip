@@ -301,12 +301,13 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
                                      GemmDefer* defer = nullptr, const float* norm_w = nullptr, float eps = 0.f) {
   static bool attr = false;
   if (!attr) {
-    const void* ks[4] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
+    const void* ks[5] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, false>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, true>),
-                         reinterpret_cast<const void*>(q1_gemm_kernel<1, true>)};
-    const size_t sh[4] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(kGemmNB), gemm_shmem(1)};
-    for (int i = 0; i < 4; ++i) {
+                         reinterpret_cast<const void*>(q1_gemm_kernel<1, true>),
+                         reinterpret_cast<const void*>(q1_gemm_kernel<1, true, true>)};
+    const size_t sh[5] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(1)};
+    for (int i = 0; i < 5; ++i) {
       hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh[i]);
       if (e != hipSuccess) return e;
     }
@@ -347,7 +348,10 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
   const unsigned gx_ = (unsigned)((W.nrb + 3) / 4);
   const dim3 g1(gx_, 1, (unsigned)S), g2(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S);
   if (n <= 16) {
-    if (raw)
+    if (raw && n <= 8)  // hi and lo of every token in one operand: one matrix instruction per step
+      hipLaunchKernelGGL((q1_gemm_kernel<1, true, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows,
+                         W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+    else if (raw)
       hipLaunchKernelGGL((q1_gemm_kernel<1, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows, W.nrb,
                          (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
     else

@@ -601,7 +601,8 @@ __global__ __launch_bounds__(256) void bt_attn_mfma_kernel(const float* __restri
 // Merge of the position chunks of bt_attn_kernel (records with l = 0 held no position), then
 // o·sigmoid(gate).  Grid (n, nq), 256 threads (one output dim each); nch <= 256.  Thread z < nch
 // brings chunk z's (m, l) to LDS, so that every chunk's weight exp(m_z - M) is formed once, and the
-// dims are summed over the chunks in order with their loads issued 16 at a time.
+// dims are summed over the chunks in order, the first 64 requested with the statistics and the
+// rest 16 at a time.
 __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restrict__ rec, int nch,
                                                             const float* __restrict__ gate, int nq,
                                                             float* __restrict__ ao) {
@@ -612,6 +613,12 @@ __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restr
   const unsigned tid = threadIdx.x;
   const float* rr = rec + ((size_t)t * nq + h) * nch * (2 + HD);
   const bool has = (int)tid < nch;
+  // this dim of the first NO chunks, requested together with the chunk statistics (they do not
+  // depend on the maximum): one memory round trip for up to NO chunks
+  constexpr int NO = 64;
+  float o0[NO];
+#pragma unroll
+  for (int k = 0; k < NO; ++k) o0[k] = k < nch ? rr[(size_t)k * (2 + HD) + 2 + tid] : 0.f;
   const float mz = has ? rr[(size_t)tid * (2 + HD)] : -INFINITY;
   const float lz = has ? rr[(size_t)tid * (2 + HD) + 1] : 0.f;
   // M = max of m over the chunks that held a position (in any order: max is exact)
@@ -624,7 +631,15 @@ __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restr
   ml[1][tid] = lz;
   __syncthreads();
   float L = 0.f, O = 0.f;
-  for (int z0 = 0; z0 < nch; z0 += 16) {
+#pragma unroll
+  for (int k = 0; k < NO; ++k) {
+    if (k < nch) {
+      const float e = ml[0][k];
+      L = __builtin_fmaf(ml[1][k], e, L);
+      O = __builtin_fmaf(o0[k], e, O);
+    }
+  }
+  for (int z0 = NO; z0 < nch; z0 += 16) {
     float o[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) o[k] = z0 + k < nch ? rr[(size_t)(z0 + k) * (2 + HD) + 2 + tid] : 0.f;

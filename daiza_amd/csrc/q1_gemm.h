@@ -141,6 +141,34 @@ __device__ __forceinline__ float wave_max_abs8(float4 a, float4 b) {
   return wave_max_abs4(m);
 }
 
+// Sum of the squares over the wave of a lane partial q (in every lane, in a fixed order).
+__device__ __forceinline__ float wave_sum_lanes(float q) {
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0xB1, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x4E, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x141, 0xF, 0xF, false));
+  q += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, q), 0x140, 0xF, 0xF, false));
+  const int qi = __builtin_bit_cast(int, q);
+  const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 0));
+  const float q1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 16));
+  const float q2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 32));
+  const float q3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(qi, 48));
+  return (q0 + q1) + (q2 + q3);
+}
+
+// Sum of the squares of the 16 values of every lane over the wave, in every lane, in a fixed order.
+__device__ __forceinline__ float wave_sumsq16(float4 a, float4 b, float4 c, float4 d) {
+  float q = a.x * a.x;
+  const float4 v[4] = {a, b, c, d};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (k > 0) q = __builtin_fmaf(v[k].x, v[k].x, q);
+    q = __builtin_fmaf(v[k].y, v[k].y, q);
+    q = __builtin_fmaf(v[k].z, v[k].z, q);
+    q = __builtin_fmaf(v[k].w, v[k].w, q);
+  }
+  return wave_sum_lanes(q);
+}
+
 // Sum of the squares of the 8 values of every lane over the wave, in every lane, in a fixed order.
 __device__ __forceinline__ float wave_sumsq8(float4 a, float4 b) {
   float q = a.x * a.x;
@@ -337,7 +365,12 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
     const int tc = t < t_end ? t : t_end - 1;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
-      if constexpr (RAW) {
+      if constexpr (HL) {  // the wave's token row in tiles t and t + 1 (zeros past the range)
+        const int n = tok0 + (int)(tid >> 6), tg = t + (j >> 1);
+        const int64_t col = (int64_t)tg * kTileCols + xcol + 16 * (j & 1);
+        xv[j] = n < n_tok && tg < t_end && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
+                                                     : u32x4{0u, 0u, 0u, 0u};
+      } else if constexpr (RAW) {
         const int n = tok0 + (int)(tid >> 6) + WV * (j >> 1);
         const int64_t col = (int64_t)tc * kTileCols + xcol + 16 * (j & 1);
         xv[j] = n < n_tok && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
@@ -351,7 +384,46 @@ const int i = (int)tid + NT * j;
     }
   };
   auto put_x = [&](int b, u32x4 (&xv)[XV], int t_x) {
-    if constexpr (RAW) {
+    if constexpr (HL) {
+      // the wave's token row n in tiles t_x and t_x + 1 (tile slot u: hi row 8u + n, lo row
+      // TOK + 8u + n), with one power of two for both (one pair of reductions per two tiles)
+      const int n = (int)(tid >> 6);
+      if (tok0 + n >= n_tok) return;  // wave-uniform; these product columns are never stored
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = __builtin_bit_cast(float4, xv[j]);
+      if (x.nw != nullptr) {
+        ss_acc[0] += wave_sumsq16(v[0], v[1], v[2], v[3]);  // a tile past the range holds zeros
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t col = (int64_t)(t_x + u) * kTileCols + xcol;
+          float4 w0 = make_float4(1.f, 1.f, 1.f, 1.f), w1 = w0;
+          if (t_x + u < t_end && col < x.K) {
+            w0 = *reinterpret_cast<const float4*>(x.nw + col);
+            w1 = *reinterpret_cast<const float4*>(x.nw + col + 16);
+          }
+          v[2 * u] = make_float4(v[2 * u].x * w0.x, v[2 * u].y * w0.y, v[2 * u].z * w0.z, v[2 * u].w * w0.w);
+          v[2 * u + 1] = make_float4(v[2 * u + 1].x * w1.x, v[2 * u + 1].y * w1.y, v[2 * u + 1].z * w1.z, v[2 * u + 1].w * w1.w);
+        }
+      }
+      const float4 m0 = make_float4(fmaxf(fabsf(v[0].x), fabsf(v[2].x)), fmaxf(fabsf(v[0].y), fabsf(v[2].y)),
+                                    fmaxf(fabsf(v[0].z), fabsf(v[2].z)), fmaxf(fabsf(v[0].w), fabsf(v[2].w)));
+      const float4 m1 = make_float4(fmaxf(fabsf(v[1].x), fabsf(v[3].x)), fmaxf(fabsf(v[1].y), fabsf(v[3].y)),
+                                    fmaxf(fabsf(v[1].z), fabsf(v[3].z)), fmaxf(fabsf(v[1].w), fabsf(v[3].w)));
+      const int e = pack_exp(wave_max_abs8(m0, m1));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float4 a = v[2 * u], c = v[2 * u + 1];
+        u32x4 h, l;
+        pack_slot(make_float4(ldexpf(a.x, -e), ldexpf(a.y, -e), ldexpf(a.z, -e), ldexpf(a.w, -e)),
+                  make_float4(ldexpf(c.x, -e), ldexpf(c.y, -e), ldexpf(c.z, -e), ldexpf(c.w, -e)), h, l);
+        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)(8 * u + n) * kGemmRowPad +
+                             64 * (lane >> 2) + 16 * (3u - (lane & 3u));
+        *reinterpret_cast<u32x4*>(row) = h;
+        *reinterpret_cast<u32x4*>(row + (size_t)TOK * kGemmRowPad) = l;
+      }
+      if (lane == 0) tile_sig[b][n] = ldexpf(1.0f, e);
+    } else if constexpr (RAW) {
       // token rows past n_tok are skipped (wave-uniform; their product columns are never stored)
       const unsigned wave = tid >> 6;
       const bool normed = x.nw != nullptr;
@@ -397,31 +469,37 @@ const int i = (int)tid + NT * j;
   u32x4 cv[SBW];
   unsigned cs[SBW];
   u32x4 xv[XV];
+  // Tiles are staged PT at a time (the paired form: two tiles in one LDS buffer, in the rows the
+  // eight tokens leave free), one group per barrier; the weights stay one tile ahead.
+  constexpr int PT = HL ? 2 : 1;
   load_unit(t_begin, cv, cs);
   load_x(t_begin, xv);
   put_x(0, xv, t_begin);
   __syncthreads();
-  for (int t = t_begin; t < t_end; ++t) {
-    const int b = NBUF == 2 ? (t - t_begin) & 1 : 0;
-    const bool more = t + 1 < t_end;  // uniform: the activations of a next tile are loaded and packed
-    u32x4 cvn[SBW];
-    unsigned csn[SBW];
-    load_unit(t + 1, cvn, csn);
-    if (NBUF == 2 && more) load_x(t + 1, xv);
-    if (live) {
-      unsigned wn[SBW][4], s2[SBW];
+  for (int g0 = t_begin; g0 < t_end; g0 += PT) {
+    const int g1 = min(t_end, g0 + PT);
+    const int b = NBUF == 2 ? ((g0 - t_begin) / PT) & 1 : 0;
+    const bool more = g1 < t_end;  // uniform: the activations of a next group are loaded and packed
+    if (NBUF == 2 && more) load_x(g1, xv);
+    f32x4 at[SBW][NB];  // raw form: this group's products, scaled by sig(n, group) after it
 #pragma unroll
-      for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], psel, wn[sb], s2[sb]);
-      f32x4 at[SBW][NB];  // raw form: this tile's products, scaled by sig(n, t) after the tile
+    for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
-      for (int sb = 0; sb < SBW; ++sb)
+      for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
+    for (int t = g0; t < g1; ++t) {
+      u32x4 cvn[SBW];
+      unsigned csn[SBW];
+      load_unit(t + 1, cvn, csn);
+      if (live) {
+        unsigned wn[SBW][4], s2[SBW];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
-      // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7 (paired form:
-      // the hi row of token r for r < 8, else the lo row of token r - 8)
-      const unsigned brow = HL ? (r < 8u ? r : (unsigned)TOK + r - 8u) : r;
-      const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)brow * kGemmRowPad + 256u * q;
-      const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
+        for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], psel, wn[sb], s2[sb]);
+        // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7 (paired form:
+        // the hi row of token r for r < 8, else the lo row of token r - 8, of tile slot t - g0)
+        const unsigned u8 = HL ? 8u * (unsigned)(t - g0) : 0u;
+        const unsigned brow = HL ? (r < 8u ? u8 + r : (unsigned)TOK + u8 + r - 8u) : r;
+        const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)brow * kGemmRowPad + 256u * q;
+        const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
 #define DZ_GEMM_STEP(S)                                                                               \
   if constexpr (HL) {                                                                                 \
     const f16x8 xb_ = *reinterpret_cast<const f16x8*>(bh + 16 * (S));                                 \
@@ -443,11 +521,19 @@ const int i = (int)tid + NT * j;
       }                                                                                               \
     }                                                                                                 \
   }
-      DZ_GEMM_STEP(0) DZ_GEMM_STEP(1) DZ_GEMM_STEP(2) DZ_GEMM_STEP(3)
-      DZ_GEMM_STEP(4) DZ_GEMM_STEP(5) DZ_GEMM_STEP(6) DZ_GEMM_STEP(7)
-      DZ_GEMM_STEP(8) DZ_GEMM_STEP(9) DZ_GEMM_STEP(10) DZ_GEMM_STEP(11)
-      DZ_GEMM_STEP(12) DZ_GEMM_STEP(13) DZ_GEMM_STEP(14) DZ_GEMM_STEP(15)
+        DZ_GEMM_STEP(0) DZ_GEMM_STEP(1) DZ_GEMM_STEP(2) DZ_GEMM_STEP(3)
+        DZ_GEMM_STEP(4) DZ_GEMM_STEP(5) DZ_GEMM_STEP(6) DZ_GEMM_STEP(7)
+        DZ_GEMM_STEP(8) DZ_GEMM_STEP(9) DZ_GEMM_STEP(10) DZ_GEMM_STEP(11)
+        DZ_GEMM_STEP(12) DZ_GEMM_STEP(13) DZ_GEMM_STEP(14) DZ_GEMM_STEP(15)
 #undef DZ_GEMM_STEP
+      }
+#pragma unroll
+      for (int sb = 0; sb < SBW; ++sb) {
+        cv[sb] = cvn[sb];
+        cs[sb] = csn[sb];
+      }
+    }
+    if (live) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const float sg = RAW ? tile_sig[b][16 * nb + (int)(HL ? r & 7u : r)] : 1.0f;
@@ -464,18 +550,13 @@ const int i = (int)tid + NT * j;
     }
     if (!more) break;  // the epilogue reads no LDS that another wave still writes
     if (NBUF == 2) {
-      put_x(b ^ 1, xv, t + 1);  // the other buffer: its last reads (tile t-1) finished before the previous barrier
+      put_x(b ^ 1, xv, g1);  // the other buffer: its last reads (group before this) finished before the previous barrier
     } else {
-      __syncthreads();  // every wave is done with this tile's activations
-      load_x(t + 1, xv);
-      put_x(0, xv, t + 1);
+      __syncthreads();  // every wave is done with this group's activations
+      load_x(g1, xv);
+      put_x(0, xv, g1);
     }
     __syncthreads();
-#pragma unroll
-    for (int sb = 0; sb < SBW; ++sb) {
-      cv[sb] = cvn[sb];
-      cs[sb] = csn[sb];
-    }
   }
   // raw form with RMSNorm: each token's 1/rms (every tile seen) or this split's sums of squares
   if (RAW && x.nw != nullptr) {

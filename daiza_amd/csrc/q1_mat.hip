@@ -301,13 +301,12 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
                                      GemmDefer* defer = nullptr, const float* norm_w = nullptr, float eps = 0.f) {
   static bool attr = false;
   if (!attr) {
-    const void* ks[5] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
+    const void* ks[4] = {reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, false>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, false>),
-                         reinterpret_cast<const void*>(q1_gemm_kernel<kGemmNB, true>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, true>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, true, true>)};
-    const size_t sh[5] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(1)};
-    for (int i = 0; i < 5; ++i) {
+    const size_t sh[4] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(1), gemm_shmem(1)};
+    for (int i = 0; i < 4; ++i) {
       hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh[i]);
       if (e != hipSuccess) return e;
     }
@@ -315,6 +314,7 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
   }
   const bool raw = p == nullptr;
   if (!raw && (W.ntiles * kTileCols != p->Kp || n > p->Np)) return hipErrorInvalidValue;
+  if (raw && n > 16) return hipErrorInvalidValue;  // the raw form packs one 16-token block per workgroup
   GemmX gx{};
   if (raw) {
     gx.Kp = W.ntiles * kTileCols;
@@ -358,12 +358,8 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
       hipLaunchKernelGGL((q1_gemm_kernel<1, false>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows, W.nrb,
                          (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   } else {
-    if (raw)
-      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, true>), g2, dim3(64 * gemm_waves(kGemmNB)), gemm_shmem(kGemmNB), s, W.data, W.rows,
-                         W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
-    else
-      hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, false>), g2, dim3(64 * gemm_waves(kGemmNB)), gemm_shmem(kGemmNB), s, W.data, W.rows,
-                         W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
+    hipLaunchKernelGGL((q1_gemm_kernel<kGemmNB, false>), g2, dim3(64 * gemm_waves(kGemmNB)), gemm_shmem(kGemmNB), s, W.data, W.rows,
+                       W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
   }
   hipError_t e = hipGetLastError();
   const float* ssq = S > 1 && raw && norm_w ? gx.ssq : nullptr;

@@ -87,7 +87,8 @@ struct GemmDefer {
 };
 hipError_t launch_q1_gemm(const Q1Dev& W, const PackedX& p, int n, float* y, int64_t ldy, int accumulate,
                           hipStream_t s, Scratch* split, GemmDefer* defer = nullptr);
-// The same product on f32 x[n][W.cols] (row stride ldx, both multiples of 4), each K tile packed in
+// The same product for n <= 16 tokens on f32 x[n][W.cols] (row stride ldx, both multiples of 4; a
+// larger n is refused with hipErrorInvalidValue: callers pack it first), each K tile packed in
 // LDS with its own power-of-two scale per token: no separate packing pass.  With norm_w, the product
 // of the RMS-normalised x (weight norm_w, eps): the tiles are packed from x·norm_w and the sums of
 // squares gathered on the way; 1/rms is applied to the result (by the deferred consumer when defer

@@ -61,20 +61,21 @@ struct Q1Dev {
 
 // p[0] + p[s] + p[2s] + ... + p[(n-1)s] (n >= 1), added in index order, with the loads issued 16 at a
 // time: a loop of dependent adds with a run-time count otherwise waits one memory round trip per term.
+// Every load of a round is issued (a term past n reloads term n-1, whose value is not added), so
+// that no load sits behind a branch: predicated loads compile to branches whose merges wait for
+// the loads already issued, and the round trips add up again.
 __device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_t stride, int n) {
   float v[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) v[k] = k < n ? p[(size_t)k * stride] : 0.f;
+  for (int k = 0; k < 16; ++k) v[k] = p[(size_t)min(k, n - 1) * stride];
   float acc = v[0];
 #pragma unroll
-  for (int k = 1; k < 16; ++k)
-    if (k < n) acc += v[k];
+  for (int k = 1; k < 16; ++k) acc = k < n ? acc + v[k] : acc;
   for (int b = 16; b < n; b += 16) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = b + k < n ? p[(size_t)(b + k) * stride] : 0.f;
+    for (int k = 0; k < 16; ++k) v[k] = p[(size_t)min(b + k, n - 1) * stride];
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-      if (b + k < n) acc += v[k];
+    for (int k = 0; k < 16; ++k) acc = b + k < n ? acc + v[k] : acc;
   }
   return acc;
 }

@@ -64,13 +64,20 @@ __global__ __launch_bounds__(256) void bt_conv_kernel(const float* __restrict__ 
   const bool live = ch < qkvd && t < n;
   float o = 0.f, xt = 0.f;
   if (live) {
+    // every tap's input and weight requested before the sums (the address is selected, not the
+    // load: a load under a branch waits for the loads before it)
+    float xs[4], ws[4];
 #pragma unroll
     for (int tap = 0; tap < 4; ++tap) {
       const int tt = t - 3 + tap;
-      const float xv = tt >= 0 ? yin[(size_t)tt * ldin + ch] : ring[(size_t)((head0 + tt) & 3) * qkvd + ch];
-      o = __builtin_fmaf(xv, conv_w[(size_t)tap * qkvd + ch], o);
-      if (tap == 3) xt = xv;
+      const float* src = tt >= 0 ? yin + (size_t)tt * ldin + ch : ring + (size_t)((head0 + tt) & 3) * qkvd + ch;
+      xs[tap] = *src;
+      ws[tap] = conv_w[(size_t)tap * qkvd + ch];
     }
+    __builtin_amdgcn_sched_barrier(0);  // all eight loads issued before the first sum waits for one
+#pragma unroll
+    for (int tap = 0; tap < 4; ++tap) o = __builtin_fmaf(xs[tap], ws[tap], o);
+    xt = xs[3];
   }
   const float v = siluf_(o);
   if (live) {
@@ -134,33 +141,46 @@ __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ 
   const float A = ssm_a[vh], dtb = dt_bias[vh];
   // staging of tokens [g0, g0 + G): thread (tt = tid >> 4, part = tid & 15) takes 16 of token tt's
   // 256 q|k values, 2 of its v rows, and (tid < 32) one alpha or beta
+  // (the staged values are returned by value and kept in named registers: held in an array
+  // captured by a lambda, they went to scratch memory, one wait per load)
   const int st = (int)(tid >> 4), sp = (int)(tid & 15u);
-  float4 gq[4];
-  float gv0, gv1, gab;
-  auto gload = [&](int g0) {
+  struct Stage {
+    float4 q0, q1, q2, q3;
+    float v0, v1, ab;
+  };
+  auto gload = [&](int g0) -> Stage {
     const int t = min(g0 + st, n - 1);
     const float* src = qk + (size_t)t * 2 * kdim + (sp < 8 ? (size_t)kh * HD + 16 * sp : kdim + (size_t)kh * HD + 16 * (sp - 8));
-#pragma unroll
-    for (int c = 0; c < 4; ++c) gq[c] = *reinterpret_cast<const float4*>(src + 4 * c);
     const float* vr = cout + (size_t)t * qkvd + 2 * kdim + (int64_t)vh * HD + quarter * 32 + 2 * sp;
-    gv0 = vr[0];
-    gv1 = vr[1];
+    // every thread loads alpha or beta (a valid address) and tid < 32 keep it: a load under a
+    // branch waits for the loads before it
     const int ta = min(g0 + (int)(tid & 15u), n - 1);
-    gab = tid < 32 ? yin[(size_t)ta * ldin + (tid < 16 ? off_a : off_b) + vh] : 0.f;
+    Stage r;
+    r.q0 = *reinterpret_cast<const float4*>(src);
+    r.q1 = *reinterpret_cast<const float4*>(src + 4);
+    r.q2 = *reinterpret_cast<const float4*>(src + 8);
+    r.q3 = *reinterpret_cast<const float4*>(src + 12);
+    r.v0 = vr[0];
+    r.v1 = vr[1];
+    r.ab = yin[(size_t)ta * ldin + ((tid & 16u) ? off_b : off_a) + vh];
+    return r;
   };
-  auto gstore = [&]() {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) *reinterpret_cast<float4*>(&sqk[st][16 * sp + 4 * c]) = gq[c];
-    sv[st][2 * sp] = gv0;
-    sv[st][2 * sp + 1] = gv1;
-    if (tid < 32) sab[tid & 15u][tid >> 4] = gab;
+  auto gstore = [&](const Stage& r) {
+    float4* dq = reinterpret_cast<float4*>(&sqk[st][16 * sp]);
+    dq[0] = r.q0;
+    dq[1] = r.q1;
+    dq[2] = r.q2;
+    dq[3] = r.q3;
+    sv[st][2 * sp] = r.v0;
+    sv[st][2 * sp + 1] = r.v1;
+    if (tid < 32) sab[tid & 15u][tid >> 4] = r.ab;
   };
-  gload(0);
-  gstore();
+  Stage nx = gload(0);
+  gstore(nx);
   __syncthreads();
   for (int g0 = 0; g0 < n; g0 += G) {
     const bool more = g0 + G < n;
-    if (more) gload(g0 + G);
+    if (more) nx = gload(g0 + G);
     const int gn = min(G, n - g0);
     for (int tt = 0; tt < gn; ++tt) {
       const int t = g0 + tt;
@@ -204,7 +224,7 @@ __global__ __launch_bounds__(256) void bt_scan_kernel(const float* __restrict__ 
     }
     if (more) {
       __syncthreads();  // every thread is done with this group's inputs
-      gstore();
+      gstore(nx);
       __syncthreads();
     }
   }
@@ -245,12 +265,13 @@ __global__ __launch_bounds__(128) void bt_gate_y_kernel(const float* __restrict_
   const unsigned tid = threadIdx.x;
   const int64_t col = (int64_t)vh * 128 + tid;
   const float v = y[(size_t)t * nvh * 128 + col];
+  const float z = yin[(size_t)t * ldin + off_z + col];  // requested with y: one memory round trip
+  const float w = nw[tid];
   const float s = wave_sum(v * v);
   if ((tid & 63u) == 0) red[tid >> 6] = s;
   __syncthreads();
   const float inv = 1.0f / sqrtf((red[0] + red[1]) * (1.0f / 128.0f) + eps);
-  const float z = yin[(size_t)t * ldin + off_z + col];
-  g[(size_t)t * nvh * 128 + col] = ((v * inv) * nw[tid]) * siluf_(z);
+  g[(size_t)t * nvh * 128 + col] = ((v * inv) * w) * siluf_(z);
 }
 
 // Attention inputs of token t at position pos0 + t (attention.rs:87-123): per q-head RMSNorm
@@ -273,30 +294,34 @@ __global__ __launch_bounds__(256) void bt_attn_prep_kernel(const float* __restri
   const bool isq = hh < nq;
   const int kvh = hh - nq;
   const float raw = isq ? row[(size_t)hh * 2 * HD + tid] : row[(size_t)nq * 2 * HD + (size_t)kvh * HD + tid];
+  // the gate (q-head) or v (kv-head) value of this dim, the norm weight and the RoPE factors,
+  // requested with raw: one memory round trip
+  const float other = isq ? row[(size_t)hh * 2 * HD + HD + tid] : row[(size_t)nq * 2 * HD + (size_t)nkv * HD + (size_t)kvh * HD + tid];
+  const float nwt = isq ? q_norm[tid] : k_norm[tid];
+  const int half = rope_dim / 2;
+  const int pos = pos0 + t;
+  const int dd = (int)tid < half ? (int)tid : (int)tid - half;
+  const bool rot = (int)tid < rope_dim;
+  const float* cs = rope + (size_t)pos * rope_dim;
+  const float c = rot ? cs[dd] : 0.f, sn = rot ? cs[half + dd] : 0.f;
   const float s = wave_sum(raw * raw);
   if ((tid & 63u) == 0) red[tid >> 6] = s;
   __syncthreads();
   const float ssum = (red[0] + red[1]) + (red[2] + red[3]);
   const float in = 1.0f / sqrtf(ssum / (float)HD + eps);
-  xs[tid] = (raw * in) * (isq ? q_norm[tid] : k_norm[tid]);
+  xs[tid] = (raw * in) * nwt;
   __syncthreads();
-  const int half = rope_dim / 2;
-  const int pos = pos0 + t;
   float v = xs[tid];
-  if ((int)tid < rope_dim) {
-    const float* cs = rope + (size_t)pos * rope_dim;
-    const int dd = (int)tid < half ? (int)tid : (int)tid - half;
-    const float c = cs[dd], sn = cs[half + dd];
+  if (rot) {
     const float x1 = xs[dd], x2 = xs[dd + half];
     v = (int)tid < half ? __builtin_fmaf(x1, c, x2 * sn) : __builtin_fmaf(x2, c, x1 * sn);
   }
   if (isq) {
     qb[((size_t)t * nq + hh) * HD + tid] = v * (1.0f / sqrtf((float)HD));
-    gate[((size_t)t * nq + hh) * HD + tid] = row[(size_t)hh * 2 * HD + HD + tid];
+    gate[((size_t)t * nq + hh) * HD + tid] = other;
   } else {
     kcache[((size_t)kvh * max_ctx + pos) * HD + tid] = v;
-    vcache[((size_t)kvh * max_ctx + pos) * HD + tid] =
-        row[(size_t)nq * 2 * HD + (size_t)nkv * HD + (size_t)kvh * HD + tid];
+    vcache[((size_t)kvh * max_ctx + pos) * HD + tid] = other;
   }
 }
 

@@ -641,6 +641,7 @@ __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restr
   // this dim of the first NO chunks, requested together with the chunk statistics (they do not
   // depend on the maximum): one memory round trip for up to NO chunks
   constexpr int NO = 64;
+  const float gt = gate[((size_t)t * nq + h) * HD + tid];  // the output gate, with the rest
   float o0[NO];
 #pragma unroll
   for (int k = 0; k < NO; ++k) o0[k] = k < nch ? rr[(size_t)k * (2 + HD) + 2 + tid] : 0.f;
@@ -677,7 +678,6 @@ __global__ __launch_bounds__(256) void bt_attn_merge_kernel(const float* __restr
       }
     }
   }
-  const float gt = gate[((size_t)t * nq + h) * HD + tid];
   ao[((size_t)t * nq + h) * HD + tid] = (O * (1.0f / L)) * sigmoidf_(gt);
 }
 

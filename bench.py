@@ -237,6 +237,8 @@ def bench_gemv(dz, H, rows=17408, cols=5120, nmat=32, reps=8):
     H.hipEventRecord(ev.ev[1], s)
     H.hipEventSynchronize(ev.ev[1])
     g.free()
+    if L.dz_q1_0_matvec_dev_status(s) != 0:  # a timed call whose wait gave up
+        raise SystemExit("gemv: " + L.dz_last_error().decode())
     avg_us = 1e3 * ev.elapsed_ms(0, 1) / n
     algo = rows * (cols // 128) * 18 + cols * 4 + rows * 4  # W + x + y (config 1)
     ev.destroy()

@@ -96,6 +96,7 @@ def lib():
     L.dz_q1_0_matvec_multi.argtypes = [ctypes.POINTER(_vp), ctypes.c_int, _f32p, ctypes.POINTER(_f32p)]
     L.dz_q1_0_matvec_batch.argtypes = [_vp, _f32p, ctypes.c_int, _f32p, ctypes.c_int]
     L.dz_q1_0_matvec_dev.argtypes = [_vp, _vp, _vp, ctypes.c_int, _vp]
+    L.dz_q1_0_matvec_dev_status.argtypes = [_vp]
     L.dz_q1_0_dequant_rows.argtypes = [_vp, ctypes.c_size_t, ctypes.c_size_t, _f32p]
     L.dz_q1_0_gemv_partials.argtypes = [_vp, _vp, _vp, _vp]
     L.dz_q1_0_partials_ld.argtypes = [_vp]
@@ -172,7 +173,7 @@ _MODEL_PROTOS = {
 EXPORTED_SYMBOLS = [
     "dz_config_bonsai27b", "dz_last_error", "dz_device_init",
     "dz_q1_0_upload", "dz_q1_0_free", "dz_q1_0_shape", "dz_q1_0_matvec", "dz_q1_0_matvec_multi", "dz_q1_0_matvec_batch",
-    "dz_q1_0_matvec_dev", "dz_q1_0_dequant_rows", "dz_q1_0_gemv_partials", "dz_q1_0_partials_ld", "dz_q1_0_ntiles",
+    "dz_q1_0_matvec_dev", "dz_q1_0_matvec_dev_status", "dz_q1_0_dequant_rows", "dz_q1_0_gemv_partials", "dz_q1_0_partials_ld", "dz_q1_0_ntiles",
     "dz_q1_0_matvec_dev_noalloc", "dz_q1_0_noalloc_max_partials",
 ] + list(k for k in _MODEL_PROTOS if k != "dz_config_bonsai27b")
 

@@ -105,12 +105,18 @@ static bool read_value(GgufReader& r, int t, GgufValue& v) {
 }
 
 // Bytes of n elements of a ggml type, as byte_size (tensor/dtype.rs) for the types of this path.
-static uint64_t type_bytes(uint32_t type, uint64_t n) {
+// Bytes of n elements of a loadable type (0 for other types).  *overflow is set when the size does
+// not fit 64 bits.
+static uint64_t type_bytes(uint32_t type, uint64_t n, bool* overflow) {
+  uint64_t r = 0;
   switch (type) {
-    case 0: return 4 * n;                            // F32
-    case 1: return 2 * n;                            // F16
-    case 30: return 2 * n;                           // BF16
-    case 41: return n % kGroup ? 0 : n / kGroup * kBlockBytes;  // Q1_0: 18 bytes per 128 weights
+    case 0: *overflow |= __builtin_mul_overflow(n, (uint64_t)4, &r); return r;   // F32
+    case 1:                                                                       // F16
+    case 30: *overflow |= __builtin_mul_overflow(n, (uint64_t)2, &r); return r;  // BF16
+    case 41:  // Q1_0: 18 bytes per 128 weights
+      if (n % kGroup) return 0;
+      *overflow |= __builtin_mul_overflow(n / kGroup, (uint64_t)kBlockBytes, &r);
+      return r;
     default: return 0;
   }
 }
@@ -183,20 +189,24 @@ int dz_gguf_open(const char* path, dz_gguf** out) {
     const uint32_t nd = r.get<uint32_t>();
     if (r.fail || nd > 4) return fail(set_error(DZ_ERR_MODEL, "tensor %s: %u dims (at most 4)", t.name.c_str(), nd));
     uint64_t ne = 1;
+    bool ovf = false;
     for (uint32_t d = 0; d < nd; ++d) {
       t.dims.push_back(r.get<uint64_t>());
-      ne *= t.dims.back();
+      ovf |= __builtin_mul_overflow(ne, t.dims.back(), &ne);
     }
     t.type = r.get<uint32_t>();
     t.offset = r.get<uint64_t>();
-    t.n_bytes = type_bytes(t.type, ne);
+    t.n_bytes = type_bytes(t.type, ne, &ovf);
     if (r.fail) return fail(set_error(DZ_ERR_MODEL, "truncated GGUF tensor table"));
+    if (ovf) return fail(set_error(DZ_ERR_MODEL, "tensor %s: size overflows 64 bits", t.name.c_str()));
   }
   // the data section starts at the next multiple of the alignment
   g->data_offset = ((uint64_t)r.pos + g->alignment - 1) / g->alignment * g->alignment;
   for (size_t i = 0; i < g->tensors.size(); ++i) {
     const GgufTensor& t = g->tensors[i];
-    if (t.n_bytes && (g->data_offset + t.offset + t.n_bytes > g->size || g->data_offset + t.offset < g->data_offset))
+    // compared without sums that could wrap: offset and size each within what follows the data start
+    const uint64_t room = g->size > g->data_offset ? g->size - g->data_offset : 0;
+    if (t.n_bytes && (t.offset > room || t.n_bytes > room - t.offset))
       return fail(set_error(DZ_ERR_MODEL, "tensor %s data out of range", t.name.c_str()));
     g->index[t.name] = i;
   }

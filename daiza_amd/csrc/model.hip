@@ -807,7 +807,7 @@ static int ctx_move_pos(dz_ctx* x, int pos) {
 }
 
 // Refuses work on a context whose last token-kernel launch gave up part-way.
-static int ctx_usable(const dz_ctx* x) {
+int ctx_usable(const dz_ctx* x) {
   if (x->poisoned)
     return set_error(DZ_ERR_DEVICE, "context state is inconsistent after a failed launch: call dz_ctx_reset");
   return DZ_OK;
@@ -1822,7 +1822,8 @@ int dz_kv_truncate(dz_ctx* x, int len) {
 int dz_ctx_set_pos(dz_ctx* x, int pos) {
   if (!x) return set_error(DZ_ERR_MODEL, "null context");
   x->bt.pending = 0;
-  if (pos < 0 || pos >= x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "pos %d out of [0, max_ctx)", pos);
+  // max_ctx itself is a full context: forwards are refused there, but the state is valid
+  if (pos < 0 || pos > x->m->cfg.max_ctx) return set_error(DZ_ERR_TENSOR, "pos %d out of [0, max_ctx]", pos);
   return ctx_move_pos(x, pos);
 }
 

@@ -258,7 +258,9 @@ struct ReduceSeg {
 // order of partial_reduce_kernel), polling each word until it carries this call's tag: readiness
 // travels with the data, so no fence, counter or barrier is involved.  The summing workgroup waits
 // only for workgroups of lower index; the host launches this kernel only when the whole grid is
-// resident at once, so all of them run.  A poll that never completes (bounded) leaves NaN in the row.
+// resident at once, so all of them run.  A poll that never completes (bounded by spin_limit rounds;
+// 0 gives up before the first check, for tests of the failure path) leaves NaN in the row and sets
+// *err, which the host turns into DZ_ERR_DEVICE.
 struct FusedGemvArgs {
   GemvGrid g;                  // tpw == 1, rbw == NWAVES
   const float* x;
@@ -268,6 +270,7 @@ struct FusedGemvArgs {
   unsigned tag;                // this call's tag (never 0: the buffer starts zeroed)
   int accumulate;
   int spin_limit;
+  int* err;                    // set to 1 by a summing thread whose wait gave up
   ReduceSeg seg[8];            // output of each stacked matrix
 };
 
@@ -319,14 +322,14 @@ __global__ __launch_bounds__(NWAVES * 64) void gemv_fused_kernel(const FusedGemv
                              : ((unsigned long long)a.tag << 32) | (unsigned long long)__float_as_uint(acc);
     }
     for (int spin = 0;; ++spin) {
-      bool all = true;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) all &= (unsigned)(w[k] >> 32) == a.tag;
-      if (all) break;
       if (spin >= a.spin_limit) {
         good = false;
         break;
       }
+      bool all = true;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) all &= (unsigned)(w[k] >> 32) == a.tag;
+      if (all) break;
 #pragma unroll
       for (int k = 0; k < 16; ++k)
         if ((unsigned)(w[k] >> 32) != a.tag)
@@ -344,6 +347,7 @@ __global__ __launch_bounds__(NWAVES * 64) void gemv_fused_kernel(const FusedGemv
   const int64_t r = v - a.seg[s].vrow_begin;
   if (r >= a.seg[s].rows) return;
   float* y = a.seg[s].y + r;
+  if (!good) __hip_atomic_store((__attribute__((address_space(1))) int*)a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   *y = !good ? __builtin_nanf("") : (a.accumulate ? *y + sum : sum);
 }
 

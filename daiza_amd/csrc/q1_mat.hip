@@ -420,10 +420,36 @@ static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* co
 }
 
 // The tagged partials of the one-launch product (gemv_fused_kernel).  The buffer starts zeroed and
-// tags grow by one per call; it is cleared again before a tag would wrap.
+// tags grow by one per call; it is cleared again before a tag would wrap.  One buffer serves every
+// stream: each launch waits for the previous one (g_fused_done) when it goes to another stream, so
+// calls run one after another on the device in the order the host made them.
 static Scratch g_tpart;
 static unsigned g_tag = 0;
 static int g_fused_cap = -1;  // workgroups of gemv_fused_kernel resident at once on the device
+static hipEvent_t g_fused_done = nullptr;
+static hipStream_t g_fused_last = nullptr;
+static int* g_fused_err = nullptr;  // device word: 1 once a launch's wait gave up (until read)
+
+// Wait bound of the summing threads: DAIZA_GEMV_SPIN=<n> lowers it (0 gives up at once), so that
+// tests of the failure path stay on the host's side.
+static int fused_spin_limit() {
+  if (const char* e = getenv("DAIZA_GEMV_SPIN")) {
+    const long v = strtol(e, nullptr, 10);
+    if (v >= 0 && v < (1 << 20)) return (int)v;
+  }
+  return 1 << 20;
+}
+
+// DZ_ERR_DEVICE if a launch since the last check gave up on its wait (the word is cleared).
+// The caller has synchronised the stream of those launches.
+static int fused_check() {
+  if (!g_fused_err) return DZ_OK;
+  int v = 0;
+  DZ_HIP_CHECK(hipMemcpy(&v, g_fused_err, 4, hipMemcpyDeviceToHost));
+  if (!v) return DZ_OK;
+  DZ_HIP_CHECK(hipMemset(g_fused_err, 0, 4));
+  return set_error(DZ_ERR_DEVICE, "matvec: a wait for split-K partials gave up (rows left NaN)");
+}
 
 // y = W x in one launch when the whole grid is resident at once (its summing workgroups wait for
 // workgroups of lower index); otherwise the split-K kernel and the tile-sum kernel.
@@ -438,6 +464,9 @@ static int matvec_fused(dz_mat* const* mats, int n, const float* x_dev, float* c
     DZ_HIP_CHECK(hipGetDevice(&dev));
     DZ_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
     DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kGemvWaves * 64, shmem));
+    DZ_HIP_CHECK(hipEventCreateWithFlags(&g_fused_done, hipEventDisableTiming));
+    DZ_HIP_CHECK(hipMalloc(&g_fused_err, 4));
+    DZ_HIP_CHECK(hipMemset(g_fused_err, 0, 4));
     g_fused_cap = occ * prop.multiProcessorCount;
   }
   const Q1Dev* ds[8];
@@ -463,14 +492,18 @@ static int matvec_fused(dz_mat* const* mats, int n, const float* x_dev, float* c
   a.ld = p.ld;
   a.tag = ++g_tag;
   a.accumulate = accumulate;
-  a.spin_limit = 1 << 20;
+  a.spin_limit = fused_spin_limit();
+  a.err = g_fused_err;
   for (int i = 0; i < n; ++i) {
     a.seg[i].y = y_dev[i];
     a.seg[i].vrow_begin = p.g.seg[i].rb_begin * kRowBlock;
     a.seg[i].rows = mats[i]->d.rows;
   }
+  if (g_fused_last && g_fused_last != s) DZ_HIP_CHECK(hipStreamWaitEvent(s, g_fused_done, 0));
   hipLaunchKernelGGL(gemv_fused_kernel<kGemvWaves>, dim3(p.nwg), dim3(kGemvWaves * 64), shmem, s, a);
   DZ_HIP_CHECK(hipGetLastError());
+  DZ_HIP_CHECK(hipEventRecord(g_fused_done, s));
+  g_fused_last = s;
   return DZ_OK;
 }
 
@@ -547,6 +580,15 @@ int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumula
   return matvec_fused(ms, 1, x_dev, ys, accumulate, stream ? (hipStream_t)stream : lib_stream());
 }
 
+int dz_q1_0_matvec_dev_status(void* stream) {
+  int rc = ensure_device();
+  if (rc) return rc;
+  DZ_HIP_CHECK(hipStreamSynchronize(stream ? (hipStream_t)stream : lib_stream()));
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_fused_last) DZ_HIP_CHECK(hipEventSynchronize(g_fused_done));
+  return fused_check();
+}
+
 int dz_q1_0_matvec_dev_noalloc(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream) {
   if (!m || !x_dev || !y_dev) return set_error(DZ_ERR_TENSOR, "matvec_dev_noalloc: null pointer");
   int dev = -1;
@@ -611,7 +653,8 @@ static int matvec_host(dz_mat* const* mats, int n, const float* x, float* const*
   for (int i = 0; i < n; ++i)
     DZ_HIP_CHECK(hipMemcpyAsync(ys[i], ydev[i], (size_t)mats[i]->d.rows * 4, hipMemcpyDeviceToHost, s));
   DZ_HIP_CHECK(hipStreamSynchronize(s));
-  return DZ_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return fused_check();
 }
 
 int dz_q1_0_matvec(dz_mat* m, const float* x, float* y, int accumulate) {

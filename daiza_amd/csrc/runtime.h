@@ -51,6 +51,9 @@ int prepare_gemv_kernels();
 
 // The model config of a context (model.hip).
 const dz_config* ctx_config(const dz_ctx* x);
+// DZ_ERR_DEVICE for a context whose last token-kernel launch gave up part-way (every forward and
+// save is refused until a reset or a restore), else DZ_OK.
+int ctx_usable(const dz_ctx* x);
 
 // Sum of the tile-group partials into each segment's output: y = [y +] sum_tg part[tg][row].
 hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const ReduceSeg* segs, int nseg,

@@ -17,8 +17,11 @@
 
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <string>
 #include <vector>
+
+#include <sys/stat.h>
 
 namespace dz {
 
@@ -92,9 +95,11 @@ uint64_t dz_session_cfg_hash(const dz_config* c, uint64_t context_length) {
   return siphash(1, 3, 0, 0, m, sizeof m);
 }
 
-int dz_ctx_save(dz_ctx* x, const char* path, uint64_t context_length, const uint32_t* history, uint64_t n_history,
-                int32_t think_enabled, const char* system_prompt) {
+static int ctx_save(dz_ctx* x, const char* path, uint64_t context_length, const uint32_t* history, uint64_t n_history,
+                    int32_t think_enabled, const char* system_prompt) {
   if (!x || !path || (!history && n_history)) return set_error(DZ_ERR_MODEL, "null argument");
+  // a context left inconsistent by a failed launch is not a session state
+  if (int rc0 = ctx_usable(x)) return rc0;
   const dz_config* c = ctx_config(x);
   const int pos = dz_ctx_pos(x);
   File fh;
@@ -155,9 +160,9 @@ int dz_ctx_save(dz_ctx* x, const char* path, uint64_t context_length, const uint
   return DZ_OK;
 }
 
-int dz_ctx_load(dz_ctx* x, const char* path, uint64_t context_length, uint32_t* history, uint64_t history_cap,
-                uint64_t* n_history, int32_t* think_enabled, char* system_prompt, uint64_t prompt_cap,
-                uint64_t* prompt_len) {
+static int ctx_load(dz_ctx* x, const char* path, uint64_t context_length, uint32_t* history, uint64_t history_cap,
+                    uint64_t* n_history, int32_t* think_enabled, char* system_prompt, uint64_t prompt_cap,
+                    uint64_t* prompt_len) {
   if (!x || !path) return set_error(DZ_ERR_MODEL, "null argument");
   const dz_config* c = ctx_config(x);
   File fh;
@@ -182,8 +187,15 @@ int dz_ctx_load(dz_ctx* x, const char* path, uint64_t context_length, uint32_t* 
   if (nb != (uint32_t)c->n_layers) return set_error(DZ_ERR_MODEL, "block_count mismatch: file=%u expected=%d", nb, c->n_layers);
   if (pos > (uint64_t)c->max_ctx) return set_error(DZ_ERR_TENSOR, "session position %llu exceeds max_ctx %d",
                                                    (unsigned long long)pos, c->max_ctx);
+  // the history is bounded before anything is allocated for it: at most 2^32 tokens, and no more
+  // than the bytes left after the header
+  struct stat sb;
+  if (fstat(fileno(f), &sb) != 0) return set_error(DZ_ERR_MODEL, "stat %s", path);
+  const uint64_t left = (uint64_t)sb.st_size > kDzssHeader ? (uint64_t)sb.st_size - kDzssHeader : 0;
+  if (nh > (1ull << 32) || nh > left / 4)
+    return set_error(DZ_ERR_MODEL, "%s: history of %llu tokens exceeds the file", path, (unsigned long long)nh);
   std::vector<uint32_t> hist((size_t)nh);
-  if (nh > (1ull << 32) || !rd(f, hist.data(), (size_t)nh * 4)) return set_error(DZ_ERR_MODEL, "%s: short history", path);
+  if (!rd(f, hist.data(), (size_t)nh * 4)) return set_error(DZ_ERR_MODEL, "%s: short history", path);
   // read every block before touching the context, so that a bad file leaves it as it was
   const int64_t hd = c->ssm_state, qkvd = (2 * (int64_t)c->ssm_k_heads + c->ssm_v_heads) * hd;
   const size_t st_n = (size_t)c->ssm_v_heads * hd * hd, cv_n = (size_t)c->ssm_conv_kernel * qkvd;
@@ -263,6 +275,31 @@ int dz_ctx_load(dz_ctx* x, const char* path, uint64_t context_length, uint32_t* 
     system_prompt[n] = 0;
   }
   return DZ_OK;
+}
+
+// The C entry points: no C++ exception (an allocation that fails, for one) leaves the library.
+int dz_ctx_save(dz_ctx* x, const char* path, uint64_t context_length, const uint32_t* history, uint64_t n_history,
+                int32_t think_enabled, const char* system_prompt) {
+  try {
+    return ctx_save(x, path, context_length, history, n_history, think_enabled, system_prompt);
+  } catch (const std::exception& ex) {
+    return set_error(DZ_ERR_MODEL, "session save: %s", ex.what());
+  } catch (...) {
+    return set_error(DZ_ERR_MODEL, "session save: unexpected exception");
+  }
+}
+
+int dz_ctx_load(dz_ctx* x, const char* path, uint64_t context_length, uint32_t* history, uint64_t history_cap,
+                uint64_t* n_history, int32_t* think_enabled, char* system_prompt, uint64_t prompt_cap,
+                uint64_t* prompt_len) {
+  try {
+    return ctx_load(x, path, context_length, history, history_cap, n_history, think_enabled, system_prompt,
+                    prompt_cap, prompt_len);
+  } catch (const std::exception& ex) {
+    return set_error(DZ_ERR_MODEL, "session load: %s", ex.what());
+  } catch (...) {
+    return set_error(DZ_ERR_MODEL, "session load: unexpected exception");
+  }
 }
 
 }  // extern "C"

@@ -95,8 +95,18 @@ int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* cons
 int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumulate);
 
 /* Same as dz_q1_0_matvec on device pointers, enqueued on `stream` (a hipStream_t, NULL = default),
- * without a host synchronisation.  The token loop uses the fused kernels instead. */
+ * without a host synchronisation.  The token loop uses the fused kernels instead.
+ * Calls on different streams run one after another on the device, in the order they were made
+ * (the one-launch product shares one buffer of split-K partials).  A launch whose bounded wait for
+ * those partials gives up leaves NaN in the rows it could not form and is reported as
+ * DZ_ERR_DEVICE by dz_q1_0_matvec_dev_status (or by the next synchronous dz_q1_0_matvec*). */
 int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);
+
+/* Synchronises `stream` (NULL = the library's) and every dz_q1_0_matvec_dev launch made before,
+ * and returns DZ_ERR_DEVICE if any of them gave up on a wait since the last check, else DZ_OK.
+ * No counterpart in the reference, whose matvec is synchronous: the status of the asynchronous
+ * form above. */
+int dz_q1_0_matvec_dev_status(void* stream);
 
 /* dz_q1_0_matvec_dev that allocates nothing, for callers that cannot call hipMalloc (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation); no counterpart in the

@@ -3,6 +3,7 @@ committed tests/golden/tiny.gguf against hand-derived expected values, round tri
 by tests/gguf_writer.py, Config::from_metadata (model/config.rs:76-160), and malformed files.
 Reference: GgufFile::open (gguf/parser.rs:40-119), metadata.rs, tensor_info.rs:41-201."""
 import os
+import struct
 
 import numpy as np
 import pytest
@@ -120,3 +121,40 @@ def test_malformed_files_are_refused(dz, tmp_path):
         assert e.value.code == dz.DZ_ERR_MODEL, name
     with pytest.raises(dz.DaizaError):
         dz.GgufFile(str(tmp_path / "missing.gguf"))
+
+
+def _one_tensor_file(dims, ty, offset=0):
+    """A GGUF v3 file whose single tensor info declares `dims` of type `ty` at `offset`, followed
+    by 64 data bytes: the declared size is whatever the dims say."""
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    out = bytearray(b"GGUF") + struct.pack("<IQQ", 3, 1, 1)
+    out += s("general.architecture") + struct.pack("<I", STR) + s("qwen35")
+    out += s("t") + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+    out += struct.pack("<IQ", ty, offset)
+    out += bytes((-len(out)) % 32) + bytes(64)
+    return bytes(out)
+
+
+def test_sizes_that_overflow_are_refused(dz, tmp_path):
+    """Declared tensor sizes are computed without wrapping: an F32 tensor of 2^62 - 2 elements
+    (4 x that is 2^64 - 8, which wraps below the file size), an element count whose dims product
+    passes 2^64, and an offset near 2^64 are refused, where the reference fails on its slice bounds;
+    a tensor that fits is read."""
+    cases = {
+        "f32_bytes_wrap": _one_tensor_file([2 ** 62 - 2], 0),
+        "dims_product_wraps": _one_tensor_file([2 ** 33, 2 ** 33], 1),
+        "offset_wraps": _one_tensor_file([4], 0, offset=2 ** 64 - 8),
+        "past_the_end": _one_tensor_file([17], 0),
+    }
+    for name, blob in cases.items():
+        p = tmp_path / (name + ".gguf")
+        p.write_bytes(blob)
+        with pytest.raises(dz.DaizaError) as e:
+            dz.GgufFile(str(p))
+        assert e.value.code == dz.DZ_ERR_MODEL, name
+    p = tmp_path / "fits.gguf"
+    p.write_bytes(_one_tensor_file([16], 0))
+    (name, ty, dims, off, nb), = dz.GgufFile(str(p)).tensors()
+    assert (name, ty, nb) == ("t", 0, 64)

@@ -123,3 +123,83 @@ def test_matvec_subnormal_scales_exact_conversion(dz, oracle):
     y = m.matvec(x)
     ref = oracle.matvec(aos2, rows, cols, x)
     assert normwise_rel(y, ref) < 1e-5
+
+
+def _hip():
+    import ctypes
+    h = ctypes.CDLL("libamdhip64.so")
+    h.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    h.hipFree.argtypes = [ctypes.c_void_p]
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    h.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    h.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    return h
+
+
+def test_gemv_give_up_is_reported(dz, oracle, monkeypatch):
+    """The one-launch product's bounded wait for its split-K partials, forced to give up from the
+    host (DAIZA_GEMV_SPIN=0: every kernel still exits normally), is reported as DZ_ERR_DEVICE by the
+    synchronous matvec and by dz_q1_0_matvec_dev_status for the asynchronous form -- never NaN with
+    DZ_OK -- and the next calls are correct again."""
+    import ctypes
+    rows, cols = 1030, 5120
+    aos, m = _mat(dz, oracle, rows, cols)
+    x = oracle.synth_normal(SEED, K_X, 0, cols)
+    ref = oracle.matvec(aos, rows, cols, x)
+    L = dz.lib()
+    monkeypatch.setenv("DAIZA_GEMV_SPIN", "0")
+    with pytest.raises(dz.DaizaError) as e:
+        m.matvec(x)
+    assert e.value.code == dz.DZ_ERR_DEVICE
+    h = _hip()
+    dx, dy = ctypes.c_void_p(), ctypes.c_void_p()
+    assert h.hipMalloc(ctypes.byref(dx), cols * 4) == 0 and h.hipMalloc(ctypes.byref(dy), rows * 4) == 0
+    assert h.hipMemcpy(dx, x.ctypes.data, cols * 4, 1) == 0
+    assert L.dz_q1_0_matvec_dev(m._h, dx, dy, 0, None) == 0
+    assert L.dz_q1_0_matvec_dev_status(None) == dz.DZ_ERR_DEVICE
+    assert L.dz_q1_0_matvec_dev_status(None) == 0  # reported once
+    monkeypatch.delenv("DAIZA_GEMV_SPIN")
+    assert normwise_rel(m.matvec(x), ref) < 1e-5
+    assert L.dz_q1_0_matvec_dev(m._h, dx, dy, 0, None) == 0
+    assert L.dz_q1_0_matvec_dev_status(None) == 0
+    y = np.empty(rows, np.float32)
+    assert h.hipMemcpy(y.ctypes.data, dy, rows * 4, 2) == 0
+    assert normwise_rel(y, ref) < 1e-5
+    h.hipFree(dx)
+    h.hipFree(dy)
+
+
+def test_gemv_calls_on_two_streams(dz, oracle):
+    """Asynchronous products enqueued alternately on two streams (they share one buffer of tagged
+    partials) run in call order and each matches the oracle."""
+    import ctypes
+    rows, cols = 2048, 5120
+    L = dz.lib()
+    h = _hip()
+    mats = [_mat(dz, oracle, rows, cols, layer=i) for i in range(2)]
+    x = oracle.synth_normal(SEED, K_X, 1, cols)
+    refs = [oracle.matvec(a, rows, cols, x) for a, _ in mats]
+    dx = ctypes.c_void_p()
+    assert h.hipMalloc(ctypes.byref(dx), cols * 4) == 0
+    assert h.hipMemcpy(dx, x.ctypes.data, cols * 4, 1) == 0
+    ys, ss = [], []
+    for i in range(8):
+        p = ctypes.c_void_p()
+        assert h.hipMalloc(ctypes.byref(p), rows * 4) == 0
+        ys.append(p)
+    for _ in range(2):
+        s = ctypes.c_void_p()
+        assert h.hipStreamCreate(ctypes.byref(s)) == 0
+        ss.append(s)
+    for i in range(8):
+        assert L.dz_q1_0_matvec_dev(mats[i % 2][1]._h, dx, ys[i], 0, ss[i % 2]) == 0
+    for s in ss:
+        assert L.dz_q1_0_matvec_dev_status(s) == 0
+    for i in range(8):
+        y = np.empty(rows, np.float32)
+        assert h.hipMemcpy(y.ctypes.data, ys[i], rows * 4, 2) == 0
+        assert normwise_rel(y, refs[i % 2]) < 1e-5, i
+        h.hipFree(ys[i])
+    for s in ss:
+        h.hipStreamDestroy(s)
+    h.hipFree(dx)

@@ -264,3 +264,50 @@ def test_refused_files_leave_the_context_unchanged(dz, small, tmp_path):
     with pytest.raises(dz.DaizaError):
         ctx.load(p, history_cap=2)
     assert ctx.pos == 4
+
+
+def test_history_length_is_bounded_before_allocation(dz, small, tmp_path):
+    """A header whose n_history is 2^62 (or anything beyond the bytes that follow it) is refused
+    with DZ_ERR_MODEL before any allocation, and the context is left as it was."""
+    cfg, m = small
+    ctx = dz.Context(m)
+    ctx.forward_batch(np.array([5, 6, 7], np.uint32))
+    p = str(tmp_path / "ok.dzss")
+    ctx.save(p, history=[5, 6, 7])
+    good = open(p, "rb").read()
+    for name, nh in (("huge", 2 ** 62), ("past_2_32", 2 ** 32 + 1), ("past_the_file", len(good) // 4)):
+        q = tmp_path / (name + ".dzss")
+        q.write_bytes(good[:24] + struct.pack("<Q", nh) + good[32:])
+        with pytest.raises(dz.DaizaError) as e:
+            ctx.load(str(q))
+        assert e.value.code == dz.DZ_ERR_MODEL, name
+        assert ctx.pos == 3, name
+    am0, lg0 = ctx.forward_single_token(9)
+    c2 = dz.Context(m)
+    c2.load(p)
+    am1, lg1 = c2.forward_single_token(9)
+    assert np.array_equal(lg0, lg1)
+
+
+def test_full_context_round_trip(dz, small, tmp_path):
+    """A context filled to max_ctx saves and restores (position max_ctx is a valid, full state;
+    forwards there are refused), and a refused forward leaves the restored state intact."""
+    cfg, m = small
+    ctx = dz.Context(m)
+    rng = np.random.default_rng(5)
+    ctx.forward_batch(rng.integers(0, cfg.vocab, cfg.max_ctx).astype(np.uint32))
+    assert ctx.pos == cfg.max_ctx
+    p = str(tmp_path / "full.dzss")
+    ctx.save(p, history=list(range(cfg.max_ctx)))
+    c2 = dz.Context(m)
+    c2.forward_batch(np.array([1, 2], np.uint32))
+    hist = c2.load(p)[0]
+    assert c2.pos == cfg.max_ctx and list(hist) == list(range(cfg.max_ctx))
+    for a, b in zip(_state_blocks(ctx, cfg), _state_blocks(c2, cfg)):
+        for x, y in zip(a[1:], b[1:]):
+            assert np.array_equal(np.asarray(x), np.asarray(y))
+    with pytest.raises(dz.DaizaError) as e:
+        c2.forward_single_token(3)
+    assert e.value.code == dz.DZ_ERR_TENSOR
+    c2.save(str(tmp_path / "again.dzss"), history=list(range(cfg.max_ctx)))
+    assert open(p, "rb").read() == open(str(tmp_path / "again.dzss"), "rb").read()

@@ -176,7 +176,7 @@ def test_decode_greedy_eos_stop(dz, oracle, launch_path):
     assert len(ctx.decode_greedy_eos(eos, 4, eos)) == 0 and ctx.pos == p1
 
 
-def test_failed_wait_poisons_context(dz, oracle, monkeypatch):
+def test_failed_wait_poisons_context(dz, oracle, monkeypatch, tmp_path):
     """A launch whose bounded waits give up (forced from the host with a tiny spin limit, so every
     kernel still exits normally) fails with DZ_ERR_DEVICE and leaves the context refusing forwards
     until dz_ctx_reset; after the reset it matches the oracle again."""
@@ -191,10 +191,13 @@ def test_failed_wait_poisons_context(dz, oracle, monkeypatch):
     assert e.value.code == dz.DZ_ERR_DEVICE
     monkeypatch.delenv("DAIZA_PTK_SPIN")
     for call in (lambda: ctx.forward_single_token(3), lambda: ctx.decode_greedy(3, 2),
-                 lambda: ctx.forward_batch(np.array([1, 2], np.uint32)), lambda: ctx.verify_forward([1, 2])):
+                 lambda: ctx.forward_batch(np.array([1, 2], np.uint32)), lambda: ctx.verify_forward([1, 2]),
+                 lambda: ctx.save(str(tmp_path / "poisoned.dzss"))):
         with pytest.raises(dz.DaizaError) as e:
             call()
         assert e.value.code == dz.DZ_ERR_DEVICE
+    import os
+    assert not os.path.exists(str(tmp_path / "poisoned.dzss")) or os.path.getsize(str(tmp_path / "poisoned.dzss")) == 0
     ctx.reset()
     om = oracle.Model(cfg, SEED + 2)
     for t in (1, 2, 3):

@@ -174,8 +174,10 @@ struct PtkPlan {
 
 constexpr int kPtkMaxLayers = 128;
 // Trace stamps per (token, phase, workgroup): 0 = phase done; in a GEMV phase 1 = first compute
-// wave at the staging barrier, 2 = table built (lookups start), 3 = sync wave done staging.
-constexpr int kPtkTraceSlots = 4;
+// wave at the staging barrier, 2 = table built (lookups start), 3 = sync wave done staging; in a
+// DeltaNet phase 2 = inputs polled, 4 = conv inputs in LDS, 5 = conv and SiLU done, 3 = prologue
+// done, 1 = delta-rule waves at the barrier, 6 = delta rule computed, 7 = its stores issued.
+constexpr int kPtkTraceSlots = 8;
 
 struct PtkRun {
   PtkPlan plan;                // by value: kernel arguments are read with scalar loads

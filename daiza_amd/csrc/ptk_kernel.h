@@ -17,6 +17,16 @@ namespace dz {
 
 constexpr int kCW = kPtkWaves - 1;  // compute waves per workgroup
 
+// Hardware reciprocal, reciprocal square root, exp and log (v_rcp_f32, v_rsq_f32 about 1 ulp;
+// v_exp_f32 / v_log_f32 on the scaled argument) for the code that one wave runs on the token's
+// critical path, where every instruction of a serial chain adds to the token's time.  The
+// reference's own AVX2 path approximates the same functions (exp_ps, a degree-5 polynomial;
+// sigmoid_ps / silu_ps, rcp_ps with one Newton step: simd_exp.rs:44-123).
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsq(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float fast_sigmoid(float x) { return fast_rcp(1.0f + __expf(-x)); }
+__device__ __forceinline__ float fast_silu(float x) { return x * fast_rcp(1.0f + __expf(-x)); }
+
 // LDS map (dynamic LDS only, so that the lookup table sits at LDS address 0 as unit_dot needs).
 constexpr int kLdsXs = kLutBytes;                                // staged LUT inputs: up to 16 tiles (lm_head)
 constexpr int kLdsRed = kLdsXs + kMaxTilesH * kTileCols * 4;     // 64 floats: reductions
@@ -240,13 +250,16 @@ struct SrcGatedYLL {
     const bool ok = poll<17>(addr, valid, TagC{tag}, x, e);
     // lanes 16h..16h+15 hold the 16 partial sums of head h0 + h
     const float hs = row16_sum(valid(16) ? ll_val(x[16]) : 0.f);
-    const int hb = __builtin_bit_cast(int, hs);
+    {
+      // every lane forms the inverse norm of its row's head once; columns lane + 64m of the tile
+      // belong to head m / 2, whose value lane 16 * (m / 2) holds
+      const float hinv = fast_rsq(hs * (1.0f / 128.0f) + 1e-6f);
+      const int hb = __builtin_bit_cast(int, hinv);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      // columns lane + 64m of the tile belong to head m / 2 of the tile
-      const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(hb, 16 * (m >> 1)));
-      const float inv = 1.0f / sqrtf(s * (1.0f / 128.0f) + 1e-6f);
-      xs[lane + 64 * m] = base + 64 * m < K ? ((ll_val(x[m]) * inv) * nwv[m]) * ll_val(x[8 + m]) : 0.f;
+      for (int m = 0; m < 8; ++m) {
+        const float inv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(hb, 16 * (m >> 1)));
+        xs[lane + 64 * m] = base + 64 * m < K ? ((ll_val(x[m]) * inv) * nwv[m]) * ll_val(x[8 + m]) : 0.f;
+      }
     }
     sq = 0.f;
     return ok;
@@ -290,10 +303,29 @@ __device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->t
 struct NoPost {
   __device__ __forceinline__ void operator()() const {}
 };
+// The sync wave's gate.  A CU returns its vector-memory operations in issue order, stores included,
+// so a compute wave's partial stores issued while the sync wave has a poll round in flight leave
+// the CU only after that round returns (a memory round trip).  The next phase's inputs cannot be
+// ready before this workgroup's own outputs are out, so the sync wave holds its next polls until
+// every compute wave has issued its stores: compute waves count themselves in at LDS int [60] (GEMV
+// phases) or [61] (the DeltaNet outputs), and the sync wave waits for the count of the phases passed.
+// Bounded LDS spin of the sync wave until the count at LDS int index `idx` reaches `target`.
+__device__ __forceinline__ void lds_gate_wait(unsigned char* smem, int idx, int target) {
+  int* c = lds_ptr<int>(smem, kLdsRed) + idx;
+  for (int spin = 0; spin < (1 << 22); ++spin) {
+    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void lds_gate_arrive(unsigned char* smem, int idx, unsigned tid) {
+  if ((tid & 63u) == 0)
+    __hip_atomic_fetch_add(lds_ptr<int>(smem, kLdsRed) + idx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 template <bool SYNC, int UN, int UNX, int U, class Src, class Post = NoPost>
 __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, const Src& src, WRegs<U>& r, const Assign& a,
                                            bool lead, u64* out, int64_t ld, unsigned tag, unsigned tid,
-                                           const PtkErr& e, const NextW& nx, const TraceAt& tr,
+                                           const PtkErr& e, const NextW& nx, const TraceAt& tr, int& gs,
                                            const Post& post = Post{}) {
   float* lut = lds_ptr<float>(smem, 0);
   float* xs = lds_ptr<float>(smem, kLdsXs);
@@ -314,6 +346,10 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
   if (!wg_ok(smem, ok)) return false;  // inputs staged; every compute wave is done with the previous table
   build_lut<kPtkThreads>(lut, xs, tid);
   lds_barrier();
+  ++gs;
+  if constexpr (SYNC) {
+    lds_gate_wait(smem, 60, kCW * gs);
+  }
   if constexpr (!SYNC) {
     tr(tid, 64, 2);
     const unsigned cw = (tid >> 6) - 1, lane = tid & 63u;
@@ -331,6 +367,7 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
       const int rb = a.rb0 + (int)cw + kCW * m;
       if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, y[m], tag);
     }
+    lds_gate_arrive(smem, 60, tid);
     tr.last_wave(smem, tid);
     post();
 #pragma unroll
@@ -498,12 +535,12 @@ __device__ __forceinline__ bool r_swiglu(unsigned char* smem, bool prior, const 
     }
     if (tid < 64) {
       const float ss = wave_sum(sq_lane ? ll_val(x[MF * NTH]) : 0.f);
-      if (tid == 0) red[33] = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+      if (tid == 0) red[33] = fast_rsq(ss / (float)P.H + P.eps);
     }
   }
   if (!wg_ok(smem, ok)) return false;
   const float inv = red[33];
-  for (int f = (int)tid; f < nf; f += kPtkThreads) ll_st(sw + f0 + f, siluf_(gu[f] * inv) * (gu[nf + f] * inv), tag);
+  for (int f = (int)tid; f < nf; f += kPtkThreads) ll_st(sw + f0 + f, fast_silu(gu[f] * inv) * (gu[nf + f] * inv), tag);
   lds_barrier();
   return true;
 }
@@ -533,7 +570,7 @@ __device__ __forceinline__ bool r_qkv(const PtkPlan& P, const PtkLayer& Ly, int 
   };
   const bool ok = poll<N>(addr, valid, TagC{tag_in}, x, e);
   const float ss = wave_sum(lane < T ? ll_val(x[MR * NTH]) : 0.f);
-  const float inv = 1.0f / sqrtf(ss / (float)P.H + P.eps);
+  const float inv = fast_rsq(ss / (float)P.H + P.eps);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     const int row = (int)tid + kPtkThreads * m;
@@ -606,7 +643,7 @@ __device__ __forceinline__ bool phase_merge(const PtkPlan& P, int w, unsigned ti
     op = __builtin_fmaf(valid(3 * q) ? ll_val(x[3 * q + 2]) : 0.f, ex, op);
   }
   const float L = row16_sum(lp), O = row16_sum(op);
-  if (act && sub == 0 && ok) ll_st(ao + j, (O * (1.0f / L)) * sigmoidf_(ll_val(x[12])), tag);
+  if (act && sub == 0 && ok) ll_st(ao + j, (O * fast_rcp(L)) * fast_sigmoid(ll_val(x[12])), tag);
   return ok;
 }
 
@@ -764,11 +801,11 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
       o = __builtin_fmaf(rl[1 * kDnCh + ch], cwl[1 * kDnCh + ch], o);
       o = __builtin_fmaf(rl[2 * kDnCh + ch], cwl[2 * kDnCh + ch], o);
       o = __builtin_fmaf(xn[sl], cwl[3 * kDnCh + ch], o);
-      c[sl] = siluf_(o);
+      c[sl] = fast_silu(o);
     }
     if (ok) {
       // silu(z) first (the out-projection waits for it), then the conv ring
-      if (!vlane) ll_st(zs + (size_t)vh * HD + quarter * 32 + (lane - 32), siluf_(xn[4]), tag);
+      if (!vlane) ll_st(zs + (size_t)vh * HD + quarter * 32 + (lane - 32), fast_silu(xn[4]), tag);
       if (vh < P.nkh && quarter == 0) {
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) co_st(Ly.conv + (size_t)hb * qkvd + row[sl], xn[sl]);
@@ -777,14 +814,14 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
     }
     if (lane == 0) {
       const float xa = xn[5] + gl[1];
-      const float sp = xa > 20.0f ? xa : logf(1.0f + expf(xa));
-      sc[0] = expf(gl[0] * sp);
+      const float sp = xa > 20.0f ? xa : __logf(1.0f + __expf(xa));
+      sc[0] = __expf(gl[0] * sp);
     } else if (lane == 1) {
-      sc[1] = sigmoidf_(xn[5]);
+      sc[1] = fast_sigmoid(xn[5]);
     }
     // L2 norms of q and k (ssm.rs:76-135), q *= 1/sqrt(128) (ssm.rs:532-533)
-    const float inq = 1.0f / sqrtf(wave_sum(c[0] * c[0] + c[1] * c[1]) + 1e-6f);
-    const float ink = 1.0f / sqrtf(wave_sum(c[2] * c[2] + c[3] * c[3]) + 1e-6f);
+    const float inq = fast_rsq(wave_sum(c[0] * c[0] + c[1] * c[1]) + 1e-6f);
+    const float ink = fast_rsq(wave_sum(c[2] * c[2] + c[3] * c[3]) + 1e-6f);
     const float qsc = 1.0f / sqrtf((float)HD);
     qs[lane] = (c[0] * inq) * qsc;
     qs[lane + 64] = (c[1] * inq) * qsc;
@@ -828,6 +865,7 @@ __device__ __forceinline__ bool phase_dn(unsigned char* smem, bool prior, const 
     if (js == 0) ll_st(y + (size_t)vh * HD + i, yy, tag);
     const float ys = wave_sum(js == 0 ? yy * yy : 0.f);
     if (lane == 0) ll_st(yss + (size_t)vh * 16 + quarter * 4 + w4, ys, tag);
+    lds_gate_arrive(smem, 61, tid);
     // the state rows are stored by dn_state_store after the out-projection's stores
   }
   return true;
@@ -902,7 +940,7 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
 #pragma unroll
       for (int m = 0; m < 4; ++m) v[m] = ll_val(x[gi * 4 + m]);
       const float ss = wave_sum((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
-      const float in = 1.0f / sqrtf(ss / (float)HD + P.eps);
+      const float in = fast_rsq(ss / (float)HD + P.eps);
 #pragma unroll
       for (int m = 0; m < 4; ++m) v[m] = (v[m] * in) * (gi < GRP ? qn[m] : kw[m]);
       const float o = __shfl_xor(v[0], 32, 64);
@@ -1176,6 +1214,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   // `ok` carries the sync wave's outcome from its poll phases to the next workgroup barrier
   bool ok = true;
   int dn_seq = 0;  // DeltaNet phases passed (the compute waves' conv-input arrivals count 3 per phase)
+  int gseq = 0;    // GEMV phases passed (both roles count them)
   bool stopped = false;
   int n_done = r.n_tok;
   for (int i = 0; i < r.n_tok; ++i) {
@@ -1273,7 +1312,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
             dn_state_load(P, Ly, w, tid, sreg);
           };
           if (!gemv_phase<SYNC, U_IN, U_OUT>(smem, ok, src, wn, a, asg_lead(smem, Ly.attn), R + O.pin, ld_in, t0, tid,
-                                             e, nx, TraceAt{&r, &P, i, Ly.ph0, w}, post))
+                                             e, nx, TraceAt{&r, &P, i, Ly.ph0, w}, gseq, post))
             return;
         }
         if (!Ly.attn) {
@@ -1287,8 +1326,11 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           // C: out-proj
           SrcGatedYLL src{R + O.y, R + O.zs, R + O.yss, t0 + 2, Ly.ssm_norm, P.inner};
           auto post = [&]() { dn_state_store(P, Ly, w, tid, sreg); };
+          if constexpr (SYNC) {
+            if (w < 4 * P.nvh) lds_gate_wait(smem, 61, 4 * dn_seq);
+          }
           if (!gemv_phase<SYNC, U_OUT, 0>(smem, true, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 3, tid, e,
-                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 3, w}, post))
+                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 3, w}, gseq, post))
             return;
         } else {
           // B': attention chunks (then the out-proj weights, after the cache reads they would delay)
@@ -1306,7 +1348,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           // C': out-proj
           SrcPlainLL src{R + O.ao, t0 + 3, P.nq * 256};
           if (!gemv_phase<SYNC, U_OUT, 0>(smem, ok, src, wn, a_out, false, R + O.po, ld_in_h, t0 + 4, tid, e,
-                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 4, w}))
+                                          NextW{}, TraceAt{&r, &P, i, Ly.ph0 + 4, w}, gseq))
             return;
         }
         // the gate/up weights (issued once after the layer kinds' branches join, so that no phi of two
@@ -1318,14 +1360,14 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
           const NextW nx_dn{Ly.w_dn, P.nT_f, a_dn.t, a_dn.rb0, a_dn.rb1};
           if (!gemv_phase<SYNC, U_GU, U_DN>(smem, true, src, wn, a_gu, asg_lead(smem, 4), R + O.pgu,
                                             (int64_t)P.nrb_gu * kRowBlock, t0 + k + 1, tid, e, nx_dn,
-                                            TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}))
+                                            TraceAt{&r, &P, i, Ly.ph0 + k + 1, w}, gseq))
             return;
         }
         // E: down (its input is R2's SwiGLU)
         {
           SrcPlainLL src{R + O.sw, t0 + k + 2, P.F};
           if (!gemv_phase<SYNC, U_DN, 0>(smem, true, src, wn, a_dn, false, R + O.pd, ld_in_h, t0 + k + 3, tid, e,
-                                         NextW{}, TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}))
+                                         NextW{}, TraceAt{&r, &P, i, Ly.ph0 + k + 3, w}, gseq))
             return;
         }
         if constexpr (!SYNC) ptk_mark(r, P, i, Ly.ph0 + k + 4, w, tid, 64, 1);
@@ -1365,6 +1407,7 @@ __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
   const unsigned tid = threadIdx.x;
   const int w = (int)blockIdx.x, G = P.G;
   if (tid < 4) lds_ptr<int>(smem, kLdsFlag)[tid] = 0;
+  if (tid < 2) lds_ptr<int>(smem, kLdsRed)[60 + tid] = 0;
   // this workgroup's GEMV assignments per matrix kind (0/1: in-proj of a DeltaNet/attention layer,
   // 2/3: out-proj, 4: gate/up, 5: down) and the conv ring bases, fixed for the launch
   if (tid < 6) {

@@ -878,7 +878,7 @@ static int ptk_prepare(dz_ctx* x) {
       const int nw = tile_first_wg(t + 1, T, Gp) - tile_first_wg(t, T, Gp);
       mx = std::max(mx, (nrb + nw - 1) / nw);
     }
-    return (mx + kCW - 1) / kCW;
+    return (mx + kLW - 1) / kLW;  // layer GEMVs: every wave runs lookups
   };
   auto per = [](int n, int k) { return (n + k - 1) / k; };  // items per part of an even split
   const int nc = per(c.hidden, NR);                        // reducer residual columns per workgroup

@@ -16,6 +16,15 @@
 namespace dz {
 
 constexpr int kCW = kPtkWaves - 1;  // compute waves per workgroup
+constexpr int kLW = kPtkWaves;      // lookup waves of a layer GEMV phase (the sync wave included)
+
+// Index of this thread's wave among the NW lookup waves of a phase: all waves (NW == kLW), or the
+// compute waves 1..7 (NW == kCW, the lm_head, where the sync wave stages the next tile meanwhile).
+template <int NW>
+__device__ __forceinline__ unsigned lookup_wave(unsigned tid) {
+  static_assert(NW == kLW || NW == kCW, "lookup waves: all waves or the compute waves");
+  return NW == kLW ? (tid >> 6) : (tid >> 6) - 1;
+}
 
 // Hardware reciprocal, reciprocal square root, exp and log (v_rcp_f32, v_rsq_f32 about 1 ulp;
 // v_exp_f32 / v_log_f32 on the scaled argument) for the code that one wave runs on the token's
@@ -120,21 +129,21 @@ struct WRegs {
   UnitRegs u[U];
 };
 
-// Compute wave cw (0..kCW-1) loads its row-blocks rb0 + cw + kCW*m of tile t into slots m < UN
+// Lookup wave cw (0..NW-1) loads its row-blocks rb0 + cw + NW*m of tile t into slots m < UN
 // (slots >= UN are left alone: the phase that uses these registers reads only its UN slots).  Every
 // slot m < UN is loaded: one without a row-block reads 16 bytes of the matrix's first cache line, at
 // an offset of its own, in every lane, and its registers are never used.  A slot that were either
 // loaded or left as it was would become a phi, and the register allocator resolves phis (as it does
 // identical, merged loads) with copies next to the loads -- each copy waits for its load and turns
 // the prefetch into a stall.
-template <int UN, int U>
+template <int UN, int U, int NW = kLW>
 __device__ __forceinline__ void gemv_prefetch(const uint8_t* W, int ntiles, int t, int rb0, int rb1, unsigned tid,
                                               WRegs<U>& r) {
   static_assert(UN <= U, "prefetch slots exceed the register set");
-  const unsigned lane = tid & 63u, cw = (tid >> 6) - 1;
+  const unsigned lane = tid & 63u, cw = lookup_wave<NW>(tid);
 #pragma unroll
   for (int m = 0; m < UN; ++m) {
-    const int rb = rb0 + (int)cw + kCW * m;
+    const int rb = rb0 + (int)cw + NW * m;
     const bool v = rb < rb1;
     const uint8_t* unit = W + ((size_t)(v ? rb : 0) * ntiles + t) * kUnitBytes;
     const u32x4* sp = reinterpret_cast<const u32x4*>(v ? unit + (size_t)lane * 16 : W + (size_t)m * 80);
@@ -150,8 +159,8 @@ __device__ __forceinline__ void gemv_prefetch(const uint8_t* W, int ntiles, int 
 template <int U>
 __device__ __forceinline__ void gemv_prefetch_slot(const uint8_t* W, int ntiles, int t, int rb0, int rb1, unsigned tid,
                                                    WRegs<U>& r, int m) {
-  const unsigned lane = tid & 63u, cw = (tid >> 6) - 1;
-  const int rb = rb0 + (int)cw + kCW * m;
+  const unsigned lane = tid & 63u, cw = lookup_wave<kLW>(tid);
+  const int rb = rb0 + (int)cw + kLW * m;
   const bool v = rb < rb1;
   const uint8_t* unit = W + ((size_t)(v ? rb : 0) * ntiles + t) * kUnitBytes;
   const u32x4* sp = reinterpret_cast<const u32x4*>(v ? unit + (size_t)lane * 16 : W + (size_t)m * 80);
@@ -347,12 +356,10 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
   build_lut<kPtkThreads>(lut, xs, tid);
   lds_barrier();
   ++gs;
-  if constexpr (SYNC) {
-    lds_gate_wait(smem, 60, kCW * gs);
-  }
-  if constexpr (!SYNC) {
-    tr(tid, 64, 2);
-    const unsigned cw = (tid >> 6) - 1, lane = tid & 63u;
+  if constexpr (!SYNC) tr(tid, 64, 2);
+  {
+    // all waves, the sync wave included, run their row-blocks
+    const unsigned cw = lookup_wave<kLW>(tid), lane = tid & 63u;
     unsigned c[16];
     make_pos_consts(lane, c);
     // Every lookup before the first store: gfx9 counts loads and stores on one vmcnt, and with a
@@ -361,18 +368,22 @@ __device__ __forceinline__ bool gemv_phase(unsigned char* smem, bool prior, cons
     // behind a prefetch reach the consumers only after it.
     float y[UN];
 #pragma unroll
-    for (int m = 0; m < UN; ++m) y[m] = a.rb0 + (int)cw + kCW * m < a.rb1 ? unit_dot(r.u[m], c) : 0.f;
+    for (int m = 0; m < UN; ++m) y[m] = a.rb0 + (int)cw + kLW * m < a.rb1 ? unit_dot(r.u[m], c) : 0.f;
 #pragma unroll
     for (int m = 0; m < UN; ++m) {
-      const int rb = a.rb0 + (int)cw + kCW * m;
+      const int rb = a.rb0 + (int)cw + kLW * m;
       if (rb < a.rb1) ll_st(out + (size_t)a.t * ld + (size_t)rb * kRowBlock + lane, y[m], tag);
     }
+  }
+  if constexpr (SYNC) {
+    lds_gate_wait(smem, 60, kCW * gs);
+  } else {
     lds_gate_arrive(smem, 60, tid);
     tr.last_wave(smem, tid);
     post();
-#pragma unroll
-    for (int m = 0; m < UNX; ++m) gemv_prefetch_slot<U>(nx.W, nx.ntiles, nx.t, nx.rb0, nx.rb1, tid, r, m);
   }
+#pragma unroll
+  for (int m = 0; m < UNX; ++m) gemv_prefetch_slot<U>(nx.W, nx.ntiles, nx.t, nx.rb0, nx.rb1, tid, r, m);
   return true;
 }
 
@@ -900,7 +911,7 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
   int chunk, gc;
   attn_chunks(P, pos, &chunk, &gc);
   if (kvh >= P.nkv || g >= gc) {
-    if constexpr (!SYNC) pf();
+    pf();
     return wg_ok(smem, SYNC ? prior : true);
   }
   const unsigned lane = tid & 63u, wave = tid >> 6;
@@ -1068,7 +1079,7 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
   }
   tr(tid, 64, 2);
   // the out-projection weights, after the record stores (queued behind them, not ahead)
-  if constexpr (!SYNC) pf();
+  pf();
   return true;
 }
 
@@ -1094,7 +1105,7 @@ __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const 
   float* red = lds_ptr<float>(smem, kLdsRed);
   float ssq = 0.f;  // sync wave: this lane's share of sum(h^2), the output norm's statistics
   bool ok = SYNC ? prior : true;
-  if constexpr (!SYNC) gemv_prefetch<U_LM>(P.w_lm, NTH, 0, rb0, rb1, tid, cur);
+  if constexpr (!SYNC) gemv_prefetch<U_LM, U, kCW>(P.w_lm, NTH, 0, rb0, rb1, tid, cur);
 #pragma unroll
   for (int t = 0; t < NTH; ++t) {  // NTH is the tile count itself (checked on the host)
     if (SYNC && ok) {
@@ -1115,7 +1126,7 @@ __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const 
         if (rb < rb1) acc[m] += unit_dot(cur.u[m], c);
       }
       // the next tile (after the last one, slots without row-blocks: one cache line)
-      gemv_prefetch<U_LM>(P.w_lm, NTH, t + 1 < NTH ? t + 1 : t, rb0, t + 1 < NTH ? rb1 : rb0, tid, cur);
+      gemv_prefetch<U_LM, U, kCW>(P.w_lm, NTH, t + 1 < NTH ? t + 1 : t, rb0, t + 1 < NTH ? rb1 : rb0, tid, cur);
     }
   }
   if constexpr (SYNC) {
@@ -1289,7 +1300,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         // The in-projection weights.  Every prefetch is issued in the block that uses it: a loaded
         // value carried around a loop becomes a phi, resolved with register copies that wait for the
         // loads.
-        if constexpr (!SYNC) {
+        {
           ptk_mark(r, P, i, Ly.ph0 + 1, w, tid, 64, 1);
           const Assign a = asg_at(smem, Ly.attn);
           gemv_prefetch<U_IN>(Ly.w_in, P.nT_h, a.t, a.rb0, a.rb1, tid, wn);
@@ -1353,7 +1364,7 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
         }
         // the gate/up weights (issued once after the layer kinds' branches join, so that no phi of two
         // loads forms); the sync wave's next polls are this GEMV's own inputs (h_mid, from R1)
-        if constexpr (!SYNC) gemv_prefetch<U_GU>(Ly.w_gu, P.nT_h, a_gu.t, a_gu.rb0, a_gu.rb1, tid, wn);
+        gemv_prefetch<U_GU>(Ly.w_gu, P.nT_h, a_gu.t, a_gu.rb0, a_gu.rb1, tid, wn);
         // D: gate/up of h_mid * post_norm; tile leaders publish sum(h_mid^2) per tile
         {
           SrcNormedLL src{R + O.hmid, t0 + k, Ly.post_norm, P.H, R + O.sst_mid};

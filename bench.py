@@ -122,17 +122,41 @@ def bench_copy(H, nbytes, reps=32):
     return {"bytes": nbytes, "us": us, "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
+# Sources of each measured kernel: a PMC summary is used only for the source revision it was
+# taken on (its `kernel_source_sha16:` line must equal the hash of these files in this tree).
+KERNEL_SOURCES = {
+    "decode_config4_pmc.txt": ["ptk_kernel.h", "ptk.h", "q1_gemv.h", "model_kernels.h", "common.h", "model.hip"],
+    "gemv_config1_pmc.txt": ["q1_gemv.h", "common.h", "q1_mat.hip"],
+}
+
+
+def kernel_source_sha16(name):
+    """sha256 prefix over the sources of the kernel a summary measures (file names and bytes)."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES[name]:
+        h.update(f.encode())
+        with open(os.path.join(ROOT, "daiza_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(name, key="traffic_bytes_per_launch"):
     """HBM bytes from a committed rocprofv3 --pmc summary under profiles/ (FETCH_SIZE and
     WRITE_SIZE, each scaled by the same counter on a copy of known size): the value of the line
-    `key:`, or None when the summary or the line is absent."""
+    `key:`, or None when the summary or the line is absent, or when the summary was taken on other
+    kernel sources than this tree's."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
+    vals = {}
     for line in open(path):
-        if line.startswith(key + ":"):
-            return int(float(line.split(":", 1)[1]))
-    return None
+        if ":" in line and not line.startswith(" "):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    if vals.get("kernel_source_sha16") != kernel_source_sha16(name) or key not in vals:
+        return None
+    return int(float(vals[key]))
 
 
 def decode_bytes(cfg, wbytes, pos0, n):

@@ -857,14 +857,12 @@ static int ptk_prepare(dz_ctx* x) {
   DZ_HIP_CHECK(hipGetDevice(&dev));
   hipDeviceProp_t prop;
   DZ_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
-  int coop = 0;
-  DZ_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
   const int G = prop.multiProcessorCount;
   int64_t ld_in, ld_h, ld_gu;
   int th, to, tf;
   ctx_dims(m, &ld_in, &ld_h, &ld_gu, &th, &to, &tf);
   const int grp = c.n_head / c.n_head_kv;
-  if (!coop || c.head_dim != 256 || c.rope_dim != 64 || c.ssm_state != 128 || G < 8 || G > kPtkThreads ||
+  if (c.head_dim != 256 || c.rope_dim != 64 || c.ssm_state != 128 || G < 8 || G > kPtkThreads ||
       c.n_layers > kPtkMaxLayers || th > kMaxTilesH || c.hidden < G)
     return DZ_OK;
   // workgroup roles: GEMV workgroups [0, Gp), reducers [Gp, G) (one in eight)
@@ -903,6 +901,8 @@ static int ptk_prepare(dz_ctx* x) {
   int occ = 0;
   DZ_HIP_CHECK(hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
   DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, kPtkThreads, kPtkLds));
+  // one workgroup per CU, all G of them resident at once: the hand-overs need every workgroup
+  // running (a short grid is caught by the bounded waits: DZ_ERR_DEVICE, never a hang)
   if (occ < 1) return DZ_OK;
   const int gmax = std::min(64, Gp / std::max(1, c.n_head_kv));
   if (4 * c.ssm_v_heads > Gp || c.n_head_kv * gmax > Gp || gmax < 1) return DZ_OK;
@@ -1035,7 +1035,7 @@ static int ptk_prepare(dz_ctx* x) {
   return DZ_OK;
 }
 
-// Runs n tokens at positions pos_host.. in one cooperative launch: tokens [0, n_feed) take the fed
+// Runs n tokens at positions pos_host.. in one launch: tokens [0, n_feed) take the fed
 // ids (already in x->feed), the rest the greedy pick.  toklog[pos + i] receives token i and
 // toklog[pos + n] the greedy pick after the last one; logits of the last token land in x->logits,
 // and with per_pos every token's logits in ptk.logits_all[i] (n <= ptk.chunk).
@@ -1082,7 +1082,17 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0,
     r.trace = trace;
   }
   void* args[] = {&r};
-  DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  // A plain launch of G workgroups, one per CU (the occupancy query at plan time found room for one
+  // per CU, and more than 80 KiB of LDS keeps a second one off each CU): every workgroup is
+  // resident once the device is otherwise idle, which the hand-overs need; should one not start,
+  // the others' bounded waits end the launch with an error.  DAIZA_PTK_COOP=1 asks for a
+  // cooperative launch instead, whose residency guarantee comes from the runtime (profilers on
+  // this stack fault at process exit after a cooperative launch).
+  const char* coop = getenv("DAIZA_PTK_COOP");
+  if (coop && coop[0] == '1')
+    DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  else
+    DZ_HIP_CHECK(hipLaunchKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
   int err[4];
   DZ_HIP_CHECK(hipMemcpyAsync(err, x->ptk.err, 16, hipMemcpyDeviceToHost, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));

@@ -1,4 +1,4 @@
-// ptk.h — the persistent token kernel: one cooperative launch runs whole tokens of the decode loop
+// ptk.h — the persistent token kernel: one launch runs whole tokens of the decode loop
 // (forward_single_token, Daiza-engine/src/model/forward.rs:204-375, and the greedy selection of
 // engine.rs:850-871) with every phase of every layer inside it.
 //

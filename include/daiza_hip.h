@@ -342,7 +342,7 @@ void* dz_ctx_stream(dz_ctx* c);
 
 /*
  * 1 if this context's forwards (dz_forward_token / dz_forward_batch / dz_decode_greedy) run in the
- * persistent token kernel (one cooperative launch per call, the default for the shapes it covers),
+ * persistent token kernel (one launch per call, the default for the shapes it covers),
  * 0 if they replay the per-kernel token graph.  Setting DAIZA_PTK=0 in the environment before
  * dz_ctx_create selects the graph.  Diagnostic only; it has no counterpart in the reference.
  */

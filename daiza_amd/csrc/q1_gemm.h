@@ -5,11 +5,14 @@
 //
 // Numerics.  A weight is ±scale with scale an f16 value, so it is exact as an f16 matrix-core
 // operand (f16 subnormal scales included).  Each token's activations are divided by a power of two
-// sig (exact) that puts their largest magnitude in [2^13, 2^14), and split into two f16 values
-// hi = f16(x/sig), lo = f16(x/sig - hi); hi + lo carries 22 significant bits.  The products of the
-// f16 operands are exact in the f32 accumulator, so y = sig·(W·hi + W·lo) differs from an f32
-// dot product only by the f32 accumulation order (the reference's GEMM reorders its sums too,
-// gemm.rs:153-225).
+// sig (exact) that puts their largest magnitude in [2^13, 2^14), and split into three f16 values
+// hi = f16(v), mid = f16(v - hi), lo = f16(v - hi - mid) (v = x/sig; each difference is exact in
+// f32): 33 significant bits, so hi + mid + lo = v exactly for every f32 activation whose residuals
+// stay in f16's normal range (those below max|x| · 2^-24 lose bits only beneath f32's own precision
+// relative to the row's largest term).  The products of the f16 operands are exact in the f32
+// accumulator, so y = sig·(W·hi + W·mid + W·lo) carries the activations at f32 width and differs
+// from an f32 dot product only by the f32 accumulation order (the reference's GEMM reorders its
+// sums too, gemm.rs:153-225).
 //
 // Layout.  The weights stay in the GEMV layout (common.h): unit (row-block rb, tile t) holds 64
 // rows × 512 columns, each row's 64 sign bytes as four 16-byte chunks, chunk c of row L holding
@@ -36,19 +39,26 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 constexpr int kGemmNB = 2;                     // 16-token column blocks per workgroup (wide form)
 constexpr int kGemmTok = 16 * kGemmNB;         // tokens per workgroup of the wide form, the padding of n
 constexpr int kGemmRowPad = 2 * kTileCols + 16;  // LDS bytes per staged token row (16 B pad: no bank conflicts)
-// Waves per workgroup: the workgroup owns 4 row-blocks; with 8 waves (few tokens) two waves share a
-// row-block, each taking two of its four 16-row blocks, so the per-tile chain of a wave (operand
-// expansion and matrix instructions) is half as long and the packing of the activations is shared
-// by twice as many waves.
-__host__ __device__ constexpr int gemm_waves(int nb) { return nb == 1 ? 8 : 4; }
-// hi and lo tiles of NB token blocks (two buffers of them for NB = 1)
-__host__ __device__ constexpr size_t gemm_shmem(int nb) { return (size_t)(nb == 1 ? 2 : 1) * 2 * 16 * nb * kGemmRowPad; }
-constexpr size_t kGemmShmem = gemm_shmem(kGemmNB);
+constexpr int kGemmParts = 3;                  // hi, mid and lo f16 parts of every activation
+// Waves per workgroup: the workgroup owns 4 row-blocks, and two waves share a row-block, each taking
+// two of its four 16-row blocks, so the per-tile chain of a wave (operand expansion and matrix
+// instructions) is half as long and the packing of the activations is shared by twice as many waves.
+__host__ __device__ constexpr int gemm_waves(int) { return 8; }
+// LDS of a workgroup: the hi, mid and lo tiles of NB token blocks (two buffers of them for NB = 1);
+// the paired form (hl) stages one tile of eight tokens per buffer as 32 rows: hi 0..7, mid 8..15,
+// lo 16..23 (rows 24..31 are read as the unused columns 8..15 of the lo operand).
+__host__ __device__ constexpr size_t gemm_buf(int nb, bool hl) {
+  return hl ? (size_t)2 * 16 * kGemmRowPad : (size_t)kGemmParts * 16 * nb * kGemmRowPad;
+}
+__host__ __device__ constexpr size_t gemm_shmem(int nb, bool hl = false) {
+  return (size_t)(nb == 1 ? 2 : 1) * gemm_buf(nb, hl);
+}
 
 // Activations packed for the matrix cores.
 struct GemmX {
-  const uint16_t* xh;  // [Np][Kp] f16 bits of x/sig
-  const uint16_t* xl;  // [Np][Kp] f16 bits of x/sig - hi
+  const uint16_t* xh;  // [Np][Kp] f16 bits of v = x/sig
+  const uint16_t* xm;  // [Np][Kp] f16 bits of v - hi
+  const uint16_t* xl;  // [Np][Kp] f16 bits of v - hi - mid
   const float* sig;    // [Np] power-of-two scale of each token
   int64_t Kp;          // columns padded to the tile (ntiles * 512)
   // raw form (q1_gemm_kernel<NB, true>): x[n][K] f32 with row stride ldx, packed per tile in LDS
@@ -120,16 +130,20 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // Eight values of a 32-column block, already divided by the token's power of two — a = columns
-// 4m .. 4m+3 and b = columns 16+4m .. 16+4m+3 (m = 0..3) — split into f16 hi and lo (round to
-// nearest even) and laid out as the block's 16-byte B-operand slot 3 - m: dword p = {a[3-p],
-// b[3-p]} (columns 15 - 4s' - p and 31 - 4s' - p of slot s' = 3 - m).
-__device__ __forceinline__ void pack_slot(float4 a, float4 b, u32x4& h, u32x4& l) {
+// 4m .. 4m+3 and b = columns 16+4m .. 16+4m+3 (m = 0..3) — split into f16 hi, mid and lo (round to
+// nearest even; the residuals v - hi and v - hi - mid are exact in f32) and laid out as the block's
+// 16-byte B-operand slot 3 - m: dword p = {a[3-p], b[3-p]} (columns 15 - 4s' - p and 31 - 4s' - p
+// of slot s' = 3 - m).
+__device__ __forceinline__ void pack_slot(float4 a, float4 b, u32x4& h, u32x4& md, u32x4& l) {
   const f32x2 p[4] = {{a.w, b.w}, {a.z, b.z}, {a.y, b.y}, {a.x, b.x}};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const f16x2 hi = __builtin_convertvector(p[i], f16x2);
-    const f16x2 lo = __builtin_convertvector(p[i] - __builtin_convertvector(hi, f32x2), f16x2);
+    const f32x2 r1 = p[i] - __builtin_convertvector(hi, f32x2);
+    const f16x2 mi = __builtin_convertvector(r1, f16x2);
+    const f16x2 lo = __builtin_convertvector(r1 - __builtin_convertvector(mi, f32x2), f16x2);
     h[i] = __builtin_bit_cast(unsigned, hi);
+    md[i] = __builtin_bit_cast(unsigned, mi);
     l[i] = __builtin_bit_cast(unsigned, lo);
   }
 }
@@ -191,14 +205,15 @@ __device__ __forceinline__ float wave_sumsq8(float4 a, float4 b) {
   return (q0 + q1) + (q2 + q3);
 }
 
-// One workgroup (256 threads) per token row n < Np: x[n][0..K) -> xh/xl[n][0..Kp), sig[n]; rows
+// One workgroup (256 threads) per token row n < Np: x[n][0..K) -> xh/xm/xl[n][0..Kp), sig[n]; rows
 // n >= n_tok and columns k >= K are zero.  When w is given the row is first RMS-normalised with
 // weight w (rmsnorm_into, Daiza-engine/src/math/rmsnorm.rs:17-200: x·(1/sqrt(ss/K + eps))·w).
 // One pass gathers Σx² and max|x·w| (the norm's scale is positive, so the normalised row's
 // maximum is the scale times that), the second writes.  K is a multiple of 4 (of 128 for Q1_0).
 __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x, int64_t ldx, int64_t K, int n_tok,
                                                      const float* __restrict__ w, float eps, uint16_t* __restrict__ xh,
-                                                     uint16_t* __restrict__ xl, float* __restrict__ sig, int64_t Kp) {
+                                                     uint16_t* __restrict__ xm, uint16_t* __restrict__ xl,
+                                                     float* __restrict__ sig, int64_t Kp) {
   __shared__ float red[8];
   const int n = blockIdx.x;
   const unsigned tid = threadIdx.x;
@@ -231,6 +246,7 @@ __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x
   const float s = live ? pack_sig(amax * inv) : 1.0f;
   const float rs = 1.0f / s;  // exact: s is a power of two
   u32x4* oh = reinterpret_cast<u32x4*>(xh + (size_t)n * Kp);
+  u32x4* om = reinterpret_cast<u32x4*>(xm + (size_t)n * Kp);
   u32x4* ol = reinterpret_cast<u32x4*>(xl + (size_t)n * Kp);
   // slot k8 = 4J + m of the row: the float4 pair at columns 32J + 4m and 32J + 16 + 4m, written as
   // slot 3 - m of block J (pack_slot); K is a multiple of 128, so a pair is wholly in or out
@@ -242,9 +258,10 @@ __global__ __launch_bounds__(256) void x_pack_kernel(const float* __restrict__ x
   };
   for (int64_t k8 = tid; k8 < Kp / 8; k8 += 256) {
     const int64_t J = k8 >> 2, m = k8 & 3, ka = 8 * J + m;
-    u32x4 h = {0u, 0u, 0u, 0u}, l = h;
-    if (ka < K4) pack_slot(scaled(ka), scaled(ka + 4), h, l);
+    u32x4 h = {0u, 0u, 0u, 0u}, md = h, l = h;
+    if (ka < K4) pack_slot(scaled(ka), scaled(ka + 4), h, md, l);
     oh[4 * J + 3 - m] = h;
+    om[4 * J + 3 - m] = md;
     ol[4 * J + 3 - m] = l;
   }
   if (tid == 0) sig[n] = live ? s : 0.f;
@@ -290,20 +307,22 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
   s2x = ((sc_bits & 0xFFFFu) * 0x00010001u) ^ 0x80008000u;
 }
 
-// Grid (ceil(nrb / 4), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB) bytes of LDS.
-// Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
+// Grid (ceil(nrb / 4), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB, HL) bytes of
+// LDS.  Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
 // partial to y + z·zstride; an unsplit product (gridDim.z = 1) writes
-// y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xl)[n][k] for n < n_tok, row < rows.
+// y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xm + xl)[n][k] for n < n_tok,
+// row < rows.
 //
 // Raw form (RAW): the workgroup reads x[n][K] as f32 and packs each tile itself, with a power of two
 // sig(n, t) per token and tile (max |x| of the tile's 512 columns in [2^13, 2^14), as pack_sig); a
-// tile's products are scaled by it as they are added: y = Σ_t sig(n, t) · W_t (hi + lo)(n, t).
+// tile's products are scaled by it as they are added: y = Σ_t sig(n, t) · W_t (hi + mid + lo)(n, t).
 // That skips the separate packing pass for inputs that need no RMSNorm.
 //
-// Paired form (HL, raw form with n ≤ 8 tokens): one B operand carries both halves, columns 0..7
-// the hi rows and columns 8..15 the lo rows of the eight tokens, so each (step, block) takes one
-// matrix instruction instead of two; lanes r and r + 8 of the D layout hold the hi and lo sums of
-// token r & 7 (both scaled by that token's sig(n, t)), added once after the last tile.
+// Paired form (HL, raw form with n ≤ 8 tokens): one B operand carries two parts, columns 0..7 the
+// hi rows and columns 8..15 the mid rows of the eight tokens, and a second the lo rows in columns
+// 0..7, so each (step, block) takes two matrix instructions instead of three; lanes r and r + 8 of
+// the first D layout hold the hi and mid sums of token r & 7, lane r of the second its lo sum (all
+// scaled by that token's sig(n, t)), added once after the last tile.
 template <int NB, bool RAW = false, bool HL = false>
 __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
                                                          int ntiles, int tps, const GemmX x, int n_tok,
@@ -317,6 +336,7 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int WV = gemm_waves(NB);
   constexpr int TPW = TOK / WV;        // raw form: token rows packed by each wave
+  constexpr size_t BUF = gemm_buf(NB, HL);  // bytes of one activation buffer
   __shared__ float tile_sig[2][TOK];   // raw form: sig(n, t) of each activation buffer
   __shared__ float tok_inv[TOK];       // raw form with RMSNorm: 1/rms of each token (unsplit product)
   float ss_acc[TPW];                   // raw form with RMSNorm: sum of x^2 of the wave's token rows over
@@ -333,18 +353,23 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
   y += (size_t)blockIdx.z * zstride;
   if (gridDim.z > 1) accumulate = 0;
   f32x4 acc[SBW][NB];
+  f32x4 acc2[HL ? SBW : 1];  // paired form: the lo sums
 #pragma unroll
   for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[sb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sb = 0; sb < (HL ? SBW : 1); ++sb) acc2[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Tile t's operands are requested one tile ahead: the wave's unit (four 16-byte chunks and their
-  // scale slots) into registers, the activations (hi and lo rows of the TOK tokens) into registers
-  // that are written to the other of two LDS buffers after the current tile's products (one buffer
-  // when NB > 1: two would not fit beside a second workgroup).  A tile past the range reloads the
-  // last one (never used), so that no loaded value becomes a phi.
+  // scale slots) into registers, the activations (hi, mid and lo rows of the TOK tokens) into
+  // registers that are written to the other of two LDS buffers after the current tile's products
+  // (one buffer when NB > 1).  A tile past the range reloads the last one (never used), so that no
+  // loaded value becomes a phi.
   constexpr int NBUF = NB == 1 ? 2 : 1;
-  constexpr int XV = 2 * TOK * 64 / NT;  // 16-byte activation chunks per thread and tile
+  // 16-byte activation chunks per thread and tile: the paired form's wave row (two per lane), the
+  // raw form's TPW rows (two per lane each), or the packed form's three parts
+  constexpr int XV = HL ? 2 : RAW ? 2 * TPW : kGemmParts * TOK * 64 / NT;
   auto load_unit = [&](int t, u32x4 (&cv)[SBW], unsigned (&cs)[SBW]) {
     const int tc = t < t_end ? t : t_end - 1;
     const uint8_t* unit = W + ((size_t)(live ? rb : 0) * ntiles + tc) * kUnitBytes;
@@ -365,63 +390,49 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
     const int tc = t < t_end ? t : t_end - 1;
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
-      if constexpr (HL) {  // the wave's token row in tiles t and t + 1 (zeros past the range)
-        const int n = tok0 + (int)(tid >> 6), tg = t + (j >> 1);
-        const int64_t col = (int64_t)tg * kTileCols + xcol + 16 * (j & 1);
-        xv[j] = n < n_tok && tg < t_end && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
-                                                     : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (HL) {  // the wave's token row in tile t (zeros past the range)
+        const int n = tok0 + (int)(tid >> 6);
+        const int64_t col = (int64_t)t * kTileCols + xcol + 16 * (j & 1);
+        xv[j] = n < n_tok && t < t_end && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
+                                                    : u32x4{0u, 0u, 0u, 0u};
       } else if constexpr (RAW) {
         const int n = tok0 + (int)(tid >> 6) + WV * (j >> 1);
         const int64_t col = (int64_t)tc * kTileCols + xcol + 16 * (j & 1);
         xv[j] = n < n_tok && col < x.K ? *reinterpret_cast<const u32x4*>(x.xf + (size_t)n * x.ldx + col)
                                        : u32x4{0u, 0u, 0u, 0u};
       } else {
-const int i = (int)tid + NT * j;
+        const int i = (int)tid + NT * j;
         const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
-        xv[j] = *reinterpret_cast<const u32x4*>((part ? x.xl : x.xh) + (size_t)(tok0 + n) * x.Kp +
-                                                (size_t)tc * kTileCols + 8 * c);
+        const uint16_t* src = part == 0 ? x.xh : part == 1 ? x.xm : x.xl;
+        xv[j] = *reinterpret_cast<const u32x4*>(src + (size_t)(tok0 + n) * x.Kp + (size_t)tc * kTileCols + 8 * c);
       }
     }
   };
   auto put_x = [&](int b, u32x4 (&xv)[XV], int t_x) {
     if constexpr (HL) {
-      // the wave's token row n in tiles t_x and t_x + 1 (tile slot u: hi row 8u + n, lo row
-      // TOK + 8u + n), with one power of two for both (one pair of reductions per two tiles)
+      // the wave's token row n of tile t_x: hi in row n, mid in row 8 + n, lo in row 16 + n
       const int n = (int)(tid >> 6);
       if (tok0 + n >= n_tok) return;  // wave-uniform; these product columns are never stored
-      float4 v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = __builtin_bit_cast(float4, xv[j]);
+      float4 v0 = __builtin_bit_cast(float4, xv[0]), v1 = __builtin_bit_cast(float4, xv[1]);
       if (x.nw != nullptr) {
-        ss_acc[0] += wave_sumsq16(v[0], v[1], v[2], v[3]);  // a tile past the range holds zeros
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int64_t col = (int64_t)(t_x + u) * kTileCols + xcol;
-          float4 w0 = make_float4(1.f, 1.f, 1.f, 1.f), w1 = w0;
-          if (t_x + u < t_end && col < x.K) {
-            w0 = *reinterpret_cast<const float4*>(x.nw + col);
-            w1 = *reinterpret_cast<const float4*>(x.nw + col + 16);
-          }
-          v[2 * u] = make_float4(v[2 * u].x * w0.x, v[2 * u].y * w0.y, v[2 * u].z * w0.z, v[2 * u].w * w0.w);
-          v[2 * u + 1] = make_float4(v[2 * u + 1].x * w1.x, v[2 * u + 1].y * w1.y, v[2 * u + 1].z * w1.z, v[2 * u + 1].w * w1.w);
+        ss_acc[0] += wave_sumsq8(v0, v1);  // a tile past the range holds zeros
+        const int64_t col = (int64_t)t_x * kTileCols + xcol;
+        float4 w0 = make_float4(1.f, 1.f, 1.f, 1.f), w1 = w0;
+        if (t_x < t_end && col < x.K) {
+          w0 = *reinterpret_cast<const float4*>(x.nw + col);
+          w1 = *reinterpret_cast<const float4*>(x.nw + col + 16);
         }
+        v0 = make_float4(v0.x * w0.x, v0.y * w0.y, v0.z * w0.z, v0.w * w0.w);
+        v1 = make_float4(v1.x * w1.x, v1.y * w1.y, v1.z * w1.z, v1.w * w1.w);
       }
-      const float4 m0 = make_float4(fmaxf(fabsf(v[0].x), fabsf(v[2].x)), fmaxf(fabsf(v[0].y), fabsf(v[2].y)),
-                                    fmaxf(fabsf(v[0].z), fabsf(v[2].z)), fmaxf(fabsf(v[0].w), fabsf(v[2].w)));
-      const float4 m1 = make_float4(fmaxf(fabsf(v[1].x), fabsf(v[3].x)), fmaxf(fabsf(v[1].y), fabsf(v[3].y)),
-                                    fmaxf(fabsf(v[1].z), fabsf(v[3].z)), fmaxf(fabsf(v[1].w), fabsf(v[3].w)));
-      const int e = pack_exp(wave_max_abs8(m0, m1));
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float4 a = v[2 * u], c = v[2 * u + 1];
-        u32x4 h, l;
-        pack_slot(make_float4(ldexpf(a.x, -e), ldexpf(a.y, -e), ldexpf(a.z, -e), ldexpf(a.w, -e)),
-                  make_float4(ldexpf(c.x, -e), ldexpf(c.y, -e), ldexpf(c.z, -e), ldexpf(c.w, -e)), h, l);
-        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)(8 * u + n) * kGemmRowPad +
-                             64 * (lane >> 2) + 16 * (3u - (lane & 3u));
-        *reinterpret_cast<u32x4*>(row) = h;
-        *reinterpret_cast<u32x4*>(row + (size_t)TOK * kGemmRowPad) = l;
-      }
+      const int e = pack_exp(wave_max_abs8(v0, v1));
+      u32x4 h, md, l;
+      pack_slot(make_float4(ldexpf(v0.x, -e), ldexpf(v0.y, -e), ldexpf(v0.z, -e), ldexpf(v0.w, -e)),
+                make_float4(ldexpf(v1.x, -e), ldexpf(v1.y, -e), ldexpf(v1.z, -e), ldexpf(v1.w, -e)), h, md, l);
+      unsigned char* row = smem + (size_t)b * BUF + (size_t)n * kGemmRowPad + 64 * (lane >> 2) + 16 * (3u - (lane & 3u));
+      *reinterpret_cast<u32x4*>(row) = h;
+      *reinterpret_cast<u32x4*>(row + (size_t)8 * kGemmRowPad) = md;
+      *reinterpret_cast<u32x4*>(row + (size_t)16 * kGemmRowPad) = l;
       if (lane == 0) tile_sig[b][n] = ldexpf(1.0f, e);
     } else if constexpr (RAW) {
       // token rows past n_tok are skipped (wave-uniform; their product columns are never stored)
@@ -447,13 +458,13 @@ const int i = (int)tid + NT * j;
           v1 = make_float4(v1.x * nw1.x, v1.y * nw1.y, v1.z * nw1.z, v1.w * nw1.w);
         }
         const int e = pack_exp(wave_max_abs8(v0, v1));
-        u32x4 h, l;
+        u32x4 h, md, l;
         pack_slot(make_float4(ldexpf(v0.x, -e), ldexpf(v0.y, -e), ldexpf(v0.z, -e), ldexpf(v0.w, -e)),
-                  make_float4(ldexpf(v1.x, -e), ldexpf(v1.y, -e), ldexpf(v1.z, -e), ldexpf(v1.w, -e)), h, l);
-        unsigned char* row = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)n * kGemmRowPad +
-                             64 * (lane >> 2) + 16 * (3u - (lane & 3u));
+                  make_float4(ldexpf(v1.x, -e), ldexpf(v1.y, -e), ldexpf(v1.z, -e), ldexpf(v1.w, -e)), h, md, l);
+        unsigned char* row = smem + (size_t)b * BUF + (size_t)n * kGemmRowPad + 64 * (lane >> 2) + 16 * (3u - (lane & 3u));
         *reinterpret_cast<u32x4*>(row) = h;
-        *reinterpret_cast<u32x4*>(row + (size_t)TOK * kGemmRowPad) = l;
+        *reinterpret_cast<u32x4*>(row + (size_t)TOK * kGemmRowPad) = md;
+        *reinterpret_cast<u32x4*>(row + (size_t)2 * TOK * kGemmRowPad) = l;
         if (lane == 0) tile_sig[b][n] = ldexpf(1.0f, e);
       }
     } else {
@@ -461,17 +472,15 @@ const int i = (int)tid + NT * j;
       for (int j = 0; j < XV; ++j) {
         const int i = (int)tid + NT * j;
         const int part = i / (TOK * 64), rem = i % (TOK * 64), n = rem >> 6, c = rem & 63;
-        *reinterpret_cast<u32x4*>(smem + (size_t)b * (2 * TOK * kGemmRowPad) +
-                                  ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
+        *reinterpret_cast<u32x4*>(smem + (size_t)b * BUF + ((size_t)part * TOK + n) * kGemmRowPad + 16 * c) = xv[j];
       }
     }
   };
   u32x4 cv[SBW];
   unsigned cs[SBW];
   u32x4 xv[XV];
-  // Tiles are staged PT at a time (the paired form: two tiles in one LDS buffer, in the rows the
-  // eight tokens leave free), one group per barrier; the weights stay one tile ahead.
-  constexpr int PT = HL ? 2 : 1;
+  // Tiles are staged one per buffer and barrier; the weights stay one tile ahead.
+  constexpr int PT = 1;
   load_unit(t_begin, cv, cs);
   load_x(t_begin, xv);
   put_x(0, xv, t_begin);
@@ -482,10 +491,13 @@ const int i = (int)tid + NT * j;
     const bool more = g1 < t_end;  // uniform: the activations of a next group are loaded and packed
     if (NBUF == 2 && more) load_x(g1, xv);
     f32x4 at[SBW][NB];  // raw form: this group's products, scaled by sig(n, group) after it
+    f32x4 at2[HL ? SBW : 1];
 #pragma unroll
     for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) at[sb][nb] = RAW ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[sb][nb];
+#pragma unroll
+    for (int sb = 0; sb < (HL ? SBW : 1); ++sb) at2[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int t = g0; t < g1; ++t) {
       u32x4 cvn[SBW];
       unsigned csn[SBW];
@@ -494,29 +506,33 @@ const int i = (int)tid + NT * j;
         unsigned wn[SBW][4], s2[SBW];
 #pragma unroll
         for (int sb = 0; sb < SBW; ++sb) restore_chunk(cv[sb], cs[sb], psel, wn[sb], s2[sb]);
-        // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7 (paired form:
-        // the hi row of token r for r < 8, else the lo row of token r - 8, of tile slot t - g0)
-        const unsigned u8 = HL ? 8u * (unsigned)(t - g0) : 0u;
-        const unsigned brow = HL ? (r < 8u ? u8 + r : (unsigned)TOK + u8 + r - 8u) : r;
-        const unsigned char* bh = smem + (size_t)b * (2 * TOK * kGemmRowPad) + (size_t)brow * kGemmRowPad + 256u * q;
-        const unsigned char* bl = bh + (size_t)TOK * kGemmRowPad;
+        // B operand of step s for token block nb: token 16·nb + r, columns 128q + 8s .. +7, of the hi,
+        // mid and lo rows (paired form: row r holds hi of token r for r < 8, else mid of token r - 8;
+        // row 16 + r holds lo of token r for r < 8)
+        const unsigned char* bh = smem + (size_t)b * BUF + (size_t)r * kGemmRowPad + 256u * q;
+        const unsigned char* bm = bh + (size_t)(HL ? 16 : TOK) * kGemmRowPad;
+        const unsigned char* bl = bh + (size_t)2 * TOK * kGemmRowPad;
 #define DZ_GEMM_STEP(S)                                                                               \
   if constexpr (HL) {                                                                                 \
     const f16x8 xb_ = *reinterpret_cast<const f16x8*>(bh + 16 * (S));                                 \
+    const f16x8 xc_ = *reinterpret_cast<const f16x8*>(bm + 16 * (S));                                 \
     _Pragma("unroll") for (int sb = 0; sb < SBW; ++sb) {                                              \
       const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
       at[sb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb_, at[sb][0], 0, 0, 0);                 \
+      at2[sb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xc_, at2[sb], 0, 0, 0);                     \
     }                                                                                                 \
   } else {                                                                                            \
-    f16x8 xh_[NB], xl_[NB];                                                                           \
+    f16x8 xh_[NB], xm_[NB], xl_[NB];                                                                  \
     _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                               \
       xh_[nb] = *reinterpret_cast<const f16x8*>(bh + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
+      xm_[nb] = *reinterpret_cast<const f16x8*>(bm + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
       xl_[nb] = *reinterpret_cast<const f16x8*>(bl + (size_t)nb * 16 * kGemmRowPad + 16 * (S));       \
     }                                                                                                 \
     _Pragma("unroll") for (int sb = 0; sb < SBW; ++sb) {                                              \
       const f16x8 a = expand_signs<S>(wn[sb], s2[sb]);                                                \
       _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                             \
         at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh_[nb], at[sb][nb], 0, 0, 0);         \
+        at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xm_[nb], at[sb][nb], 0, 0, 0);         \
         at[sb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl_[nb], at[sb][nb], 0, 0, 0);         \
       }                                                                                               \
     }                                                                                                 \
@@ -542,6 +558,10 @@ const int i = (int)tid + NT * j;
           if constexpr (RAW) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[sb][nb][v] = __builtin_fmaf(sg, at[sb][nb][v], acc[sb][nb][v]);
+            if constexpr (HL) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc2[sb][v] = __builtin_fmaf(sg, at2[sb][v], acc2[sb][v]);
+            }
           } else {
             acc[sb][nb] = at[sb][nb];
           }
@@ -572,11 +592,11 @@ const int i = (int)tid + NT * j;
     if (gridDim.z == 1) __syncthreads();
   }
   if (!live) return;
-  if constexpr (HL) {  // lane r < 8 adds the lo sums of its token from lane r + 8
+  if constexpr (HL) {  // lane r < 8 adds the mid sums of its token from lane r + 8, then its lo sums
 #pragma unroll
     for (int sb = 0; sb < SBW; ++sb)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[sb][0][v] += __shfl_xor(acc[sb][0][v], 8, 16);
+      for (int v = 0; v < 4; ++v) acc[sb][0][v] = (acc[sb][0][v] + __shfl_xor(acc[sb][0][v], 8, 16)) + acc2[sb][v];
   }
   // D layout: lane holds rows 4q .. 4q+3 of block sb for token 16·nb + r
 #pragma unroll

@@ -262,13 +262,14 @@ int upload_q1_host(const uint8_t* aos, int64_t rows, int64_t cols, Q1Dev* out, s
 int packed_x_reserve(Scratch& buf, int n, int64_t K, PackedX* out) {
   const int Np = (n + kGemmTok - 1) / kGemmTok * kGemmTok;
   const int64_t Kp = (K + kTileCols - 1) / kTileCols * kTileCols;
-  const size_t half_bytes = (size_t)Np * Kp * 2;
-  const int rc = buf.reserve(2 * half_bytes + (size_t)Np * 4);
+  const size_t part_bytes = (size_t)Np * Kp * 2;
+  const int rc = buf.reserve(kGemmParts * part_bytes + (size_t)Np * 4);
   if (rc) return rc;
   char* b = static_cast<char*>(buf.ptr);
   out->xh = reinterpret_cast<uint16_t*>(b);
-  out->xl = reinterpret_cast<uint16_t*>(b + half_bytes);
-  out->sig = reinterpret_cast<float*>(b + 2 * half_bytes);
+  out->xm = reinterpret_cast<uint16_t*>(b + part_bytes);
+  out->xl = reinterpret_cast<uint16_t*>(b + 2 * part_bytes);
+  out->sig = reinterpret_cast<float*>(b + kGemmParts * part_bytes);
   out->Kp = Kp;
   out->Np = Np;
   return DZ_OK;
@@ -276,8 +277,8 @@ int packed_x_reserve(Scratch& buf, int n, int64_t K, PackedX* out) {
 
 hipError_t launch_x_pack(const float* x, int64_t ldx, int64_t K, int n, const float* w, float eps, const PackedX& p,
                          hipStream_t s) {
-  hipLaunchKernelGGL(x_pack_kernel, dim3((unsigned)p.Np), dim3(256), 0, s, x, ldx, K, n, w, eps, p.xh, p.xl, p.sig,
-                     p.Kp);
+  hipLaunchKernelGGL(x_pack_kernel, dim3((unsigned)p.Np), dim3(256), 0, s, x, ldx, K, n, w, eps, p.xh, p.xm, p.xl,
+                     p.sig, p.Kp);
   return hipGetLastError();
 }
 
@@ -305,7 +306,7 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, false>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, true>),
                          reinterpret_cast<const void*>(q1_gemm_kernel<1, true, true>)};
-    const size_t sh[4] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(1), gemm_shmem(1)};
+    const size_t sh[4] = {gemm_shmem(kGemmNB), gemm_shmem(1), gemm_shmem(1), gemm_shmem(1, true)};
     for (int i = 0; i < 4; ++i) {
       hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh[i]);
       if (e != hipSuccess) return e;
@@ -325,6 +326,7 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
     gx.eps = eps;
   } else {
     gx.xh = p->xh;
+    gx.xm = p->xm;
     gx.xl = p->xl;
     gx.sig = p->sig;
     gx.Kp = p->Kp;
@@ -348,8 +350,8 @@ static hipError_t launch_q1_gemm_any(const Q1Dev& W, const PackedX* p, const flo
   const unsigned gx_ = (unsigned)((W.nrb + 3) / 4);
   const dim3 g1(gx_, 1, (unsigned)S), g2(gx_, (unsigned)((n + kGemmTok - 1) / kGemmTok), (unsigned)S);
   if (n <= 16) {
-    if (raw && n <= 8)  // hi and lo of every token in one operand: one matrix instruction per step
-      hipLaunchKernelGGL((q1_gemm_kernel<1, true, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows,
+    if (raw && n <= 8)  // hi and mid of every token in one operand, lo in a second: two matrix instructions per step
+      hipLaunchKernelGGL((q1_gemm_kernel<1, true, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1, true), s, W.data, W.rows,
                          W.nrb, (int)W.ntiles, tps, gx, n, out, ld, zs, accumulate);
     else if (raw)
       hipLaunchKernelGGL((q1_gemm_kernel<1, true>), g1, dim3(64 * gemm_waves(1)), gemm_shmem(1), s, W.data, W.rows, W.nrb,

@@ -63,6 +63,7 @@ hipError_t launch_partial_reduce(const float* part, int64_t ld, int n_tg, const 
 // one launch per matrix.
 struct PackedX {
   uint16_t* xh = nullptr;
+  uint16_t* xm = nullptr;
   uint16_t* xl = nullptr;
   float* sig = nullptr;
   int64_t Kp = 0;  // padded columns

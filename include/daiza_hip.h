@@ -88,9 +88,9 @@ int dz_q1_0_matvec(dz_mat* m, const float* x, float* y, int accumulate);
 int dz_q1_0_matvec_multi(dz_mat* const* mats, int n, const float* x, float* const* ys);
 
 /* n columns at once: y[i] = W x[i] (accumulate = 0) or y[i] += W x[i] for i < n; host x[n][cols],
- * y[n][rows].  Runs on the matrix cores with the activations split into two f16 parts (about 22
- * significant bits) and exact ±scale weights, so it agrees with an f32 dot product to within f32
- * accumulation order.  Replaces matvec_batch_into_slice / matvec_add_batch_into_slice
+ * y[n][rows].  Runs on the matrix cores with the activations split into three f16 parts (33
+ * significant bits: f32 width) and exact ±scale weights, so it agrees with an f32 dot product to
+ * within f32 accumulation order.  Replaces matvec_batch_into_slice / matvec_add_batch_into_slice
  * (weights.rs:475-682, 976-980). */
 int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumulate);
 

@@ -2,9 +2,10 @@
 prefill and speculative verify run on the matrix cores.
 
 Bar: every column within 1e-3 normwise relative error of the reference quad kernel
-(quant.rs:614-740) applied to that column, and in practice ~1e-6: the weights are exact f16
-operands and the activations carry ~22 significant bits, so only the f32 accumulation order
-differs.  Closed forms pin the sign convention and the scale handling independently of the oracle.
+(quant.rs:614-740) applied to that column, and in practice ~1e-7: the weights are exact f16
+operands and the activations are carried at f32 width (three f16 parts, 33 significant bits), so
+only the f32 accumulation order differs; a full-mantissa input through unit scales comes back bit
+for bit.  Closed forms pin the sign convention and the scale handling independently of the oracle.
 Cases with n <= 16 run the raw form (each K tile packed in LDS with its own scale per token), the
 others the packed form (one scale per token, packed by a separate pass).
 """
@@ -110,6 +111,35 @@ def test_basis_columns_and_scales(dz, oracle):
         bit = (blk[:, g, 2 + b] >> j) & 1
         want = np.where(bit == 1, sc[:, g], -sc[:, g])
         assert np.array_equal(y[i], want), k
+
+
+@pytest.mark.parametrize("n", [1, 5, 8, 9, 16, 17, 40])
+def test_activations_carried_at_f32_width(dz, n):
+    """x = v_i e_k with v_i an f32 whose 24-bit significand has its low bits set, through a
+    matrix of unit scales: every output is exactly +-v_i, which a product carrying fewer than 24
+    significant bits of the activation (a two-part f16 split keeps 22) would round.  All three
+    forms: paired (n <= 8), raw (9..16), packed (> 16)."""
+    rows, cols = 128, 1024
+    rng = np.random.default_rng(n)
+    blk = np.empty((rows, cols // 128, 18), np.uint8)
+    blk[:, :, 2:] = rng.integers(0, 256, (rows, cols // 128, 16), dtype=np.uint8)
+    blk[:, :, 0], blk[:, :, 1] = 0x00, 0x3C  # f16 1.0
+    m = dz.Q1_0Matrix(blk.reshape(-1), rows, cols)
+    ks = rng.integers(0, cols, n)
+    # significands 1.m with the lowest mantissa bits set; magnitudes over a wide range
+    mant = rng.integers(0, 1 << 23, n, dtype=np.int64) | 0x3
+    expo = rng.integers(-20, 21, n)
+    v = np.ldexp((1.0 + mant / float(1 << 23)), expo).astype(np.float32)
+    assert np.all(v.astype(np.float64) == (1.0 + mant / float(1 << 23)) * np.ldexp(1.0, expo))
+    x = np.zeros((n, cols), np.float32)
+    x[np.arange(n), ks] = v
+    y = m.matvec_batch(x)
+    for i in range(n):
+        k = ks[i]
+        g, b, j = k // 128, (k % 128) // 8, k % 8
+        bit = (blk[:, g, 2 + b] >> j) & 1
+        want = np.where(bit == 1, v[i], -v[i]).astype(np.float32)
+        assert np.array_equal(y[i], want), (n, i)
 
 
 def test_wide_dynamic_range(dz, oracle):

@@ -463,7 +463,7 @@ def main():
             % (g["avg_launch_us"], g["achieved_gbs"], cp["bytes"], cp["us"], cp["gbs"]))
         return 0
 
-    max_ctx = max(args.prefill + args.warmup + args.steps + 8, VERIFY_CTX + 4 * VERIFY_K * 4)
+    max_ctx = max(args.prefill + 2 * (args.warmup + args.steps) + 8, VERIFY_CTX + 4 * VERIFY_K * 4)
     cfg = dz.Config.bonsai27b(max_ctx=max_ctx)
     if args.only == "verify":
         model = dz.Model.synthetic(cfg, SEED)
@@ -507,7 +507,7 @@ def main():
     ms = ev.elapsed_ms(0, 1)
     ev.destroy()
     tps = args.steps / (ms / 1e3)
-    decode_ctx_end = ctx.pos  # before the config-5 verify continues on this context
+    decode_ctx_end = ctx.pos  # before the sampled run and the config-5 verify continue on this context
 
     log("decode %d tokens: %.2f tok/s" % (args.steps, tps))
     pos_timed = args.prefill + args.warmup
@@ -524,6 +524,23 @@ def main():
         model.close()
         H.hipDeviceSynchronize()
         return 0
+    # the same loop with the reference's default sampling (T 0.7, top-k 20, top-p 0.95) drawn on the
+    # device between launches (dz_decode_sample): the rate a non-greedy caller gets
+    smp = dz.SamplingParams(0.7, 20, 0.95)
+    srng = dz.LcgRng(SEED & 0xFFFFFFFF)
+    ev = Events(H, 2)
+    stoks = ctx.decode_sample(int(toks[-1]), max(1, args.warmup), smp, srng)
+    H.hipDeviceSynchronize()
+    H.hipEventRecord(ev.ev[0], stream)
+    ctx.decode_sample(int(stoks[-1]), args.steps, smp, srng)
+    H.hipEventRecord(ev.ev[1], stream)
+    H.hipEventSynchronize(ev.ev[1])
+    sms = ev.elapsed_ms(0, 1)
+    ev.destroy()
+    sampled = {"tok_s": round(args.steps / (sms / 1e3), 2), "ms_per_token": round(sms / args.steps, 4),
+               "tokens": args.steps, "temperature": 0.7, "top_k": 20, "top_p": 0.95,
+               "context_at_end": ctx.pos}
+    log("sampled decode %d tokens: %.2f tok/s" % (args.steps, sampled["tok_s"]))
     g = bench_gemv(dz, H)
     cp = bench_copy(H, g["algo_bytes"])
     log("gemv: %.2f us per launch; copy ceiling %.1f GB/s" % (g["avg_launch_us"], cp["gbs"]))
@@ -586,6 +603,7 @@ def main():
             "launches_timed": g["launches"],
             "algo_bytes_per_launch": g["algo_bytes"],
         },
+        "sampled_decode": sampled,
         "config5": v,
         "layer_steps": layers,
         "cpu_baseline": None,

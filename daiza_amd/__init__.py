@@ -162,6 +162,7 @@ _MODEL_PROTOS = {
     "dz_verify_forward": ([_vp, _u32p, ctypes.c_int, _f32p], ctypes.c_int),
     "dz_verify_commit": ([_vp, ctypes.c_int], ctypes.c_int),
     "dz_lcg_next": ([ctypes.POINTER(ctypes.c_uint64)], ctypes.c_float),
+    "dz_decode_sample": ([_vp, ctypes.c_uint32, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_uint64), _u32p], ctypes.c_int),
     "dz_sample": ([_f32p, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_uint64), _u32p], ctypes.c_int),
     "dz_leviathan_check": ([_f32p, _f32p, ctypes.c_int, ctypes.c_uint32, _vp, ctypes.POINTER(ctypes.c_uint64),
                             ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
@@ -516,6 +517,15 @@ class Context:
         """n greedy forwards on the device; the pick after each (engine.rs:850-871 without the EOS stop)."""
         out = np.empty(n, np.uint32)
         _check(lib().dz_decode_greedy(self._h, int(first_token), int(n), out.ctypes.data_as(_u32p)))
+        return out
+
+    def decode_sample(self, first_token, n, params, rng):
+        """n sampled forwards (engine.rs:850-862 without the EOS stop): each next input is
+        sample_top_k_top_p_into of the previous logits with params and rng (LcgRng, advanced once per
+        token); on the token kernel the top-k and the draw run on the device."""
+        out = np.empty(n, np.uint32)
+        _check(lib().dz_decode_sample(self._h, int(first_token), int(n), ctypes.byref(params),
+                                      ctypes.byref(rng.state), out.ctypes.data_as(_u32p)))
         return out
 
     def decode_greedy_eos(self, first_token, n, eos_id):

@@ -838,8 +838,8 @@ static bool ptk_fits(const PtkShape& s, const PtkShape& b) {
 static const void* ptk_pick(const PtkShape& s) {
   if (ptk_fits(s, PtkShape{10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32}))
     return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32>);
-  if (ptk_fits(s, PtkShape{1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8}))
-    return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 1, 4, 1, 1, 8>);
+  if (ptk_fits(s, PtkShape{1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8}))
+    return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8>);
   return nullptr;
 }
 
@@ -1035,6 +1035,33 @@ static int ptk_prepare(dz_ctx* x) {
   return DZ_OK;
 }
 
+// One launch of the token kernel on the context's stream.  A plain launch of G workgroups, one per
+// CU (the occupancy query at plan time found room for one per CU, and more than 80 KiB of LDS keeps a
+// second one off each CU): every workgroup is resident once the device is otherwise idle, which the
+// hand-overs need; should one not start, the others' bounded waits end the launch with an error.
+// DAIZA_PTK_COOP=1 asks for a cooperative launch instead, whose residency guarantee comes from the
+// runtime (profilers on this stack fault at process exit after a cooperative launch).
+static int ptk_launch(dz_ctx* x, PtkRun& r) {
+  void* args[] = {&r};
+  const PtkPlan& P = x->ptk.plan;
+  const char* coop = getenv("DAIZA_PTK_COOP");
+  if (coop && coop[0] == '1')
+    DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  else
+    DZ_HIP_CHECK(hipLaunchKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  return DZ_OK;
+}
+
+// The wait bound of a launch: DAIZA_PTK_SPIN=<n> lowers it (a wait that gives up ends the launch with
+// DZ_ERR_DEVICE); for tests of the failure path, which must stay on the host's side.
+static int ptk_spin_limit() {
+  if (const char* sl = getenv("DAIZA_PTK_SPIN")) {
+    const long v = strtol(sl, nullptr, 10);
+    if (v > 0 && v < (1 << 21)) return (int)v;
+  }
+  return 1 << 21;
+}
+
 // Runs n tokens at positions pos_host.. in one launch: tokens [0, n_feed) take the fed
 // ids (already in x->feed), the rest the greedy pick.  toklog[pos + i] receives token i and
 // toklog[pos + n] the greedy pick after the last one; logits of the last token land in x->logits,
@@ -1063,13 +1090,7 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0,
   r.want_logits = 1;
   r.eos = eos;
   r.err.flag = x->ptk.err;
-  // DAIZA_PTK_SPIN=<n> lowers the bound of every wait in the launch (a wait that gives up ends the
-  // launch with DZ_ERR_DEVICE); for tests of the failure path, which must stay on the host's side.
-  r.err.spin_limit = 1 << 21;
-  if (const char* sl = getenv("DAIZA_PTK_SPIN")) {
-    const long v = strtol(sl, nullptr, 10);
-    if (v > 0 && v < (1 << 21)) r.err.spin_limit = (int)v;
-  }
+  r.err.spin_limit = ptk_spin_limit();
   // DAIZA_PTK_TRACE=<file>: append per-phase times of every workgroup to <file> (binary: int32
   // n_tok, ppt, G, slots, then n_tok*ppt*G*slots uint64 s_memrealtime ticks of 10 ns)
   const char* trace_path = getenv("DAIZA_PTK_TRACE");
@@ -1081,18 +1102,7 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0,
     DZ_HIP_CHECK(hipMemset(trace, 0, trace_n * sizeof(u64)));
     r.trace = trace;
   }
-  void* args[] = {&r};
-  // A plain launch of G workgroups, one per CU (the occupancy query at plan time found room for one
-  // per CU, and more than 80 KiB of LDS keeps a second one off each CU): every workgroup is
-  // resident once the device is otherwise idle, which the hand-overs need; should one not start,
-  // the others' bounded waits end the launch with an error.  DAIZA_PTK_COOP=1 asks for a
-  // cooperative launch instead, whose residency guarantee comes from the runtime (profilers on
-  // this stack fault at process exit after a cooperative launch).
-  const char* coop = getenv("DAIZA_PTK_COOP");
-  if (coop && coop[0] == '1')
-    DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
-  else
-    DZ_HIP_CHECK(hipLaunchKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+  if (int rc = ptk_launch(x, r)) return rc;
   int err[4];
   DZ_HIP_CHECK(hipMemcpyAsync(err, x->ptk.err, 16, hipMemcpyDeviceToHost, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
@@ -1136,6 +1146,70 @@ static int ptk_feed(dz_ctx* x, const uint32_t* ids, int n) {
     if (ids[i] >= (uint32_t)x->m->cfg.vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", ids[i], x->m->cfg.vocab);
   DZ_HIP_CHECK(hipMemcpyAsync(x->feed, ids, (size_t)n * 4, hipMemcpyHostToDevice, x->s));
   DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  return DZ_OK;
+}
+
+// ---- sampled decode on the token kernel (dz_decode_sample, spec.hip): forward i takes feed[i]
+// and leaves its logits in x->logits; the caller's kernels after each launch write feed[i + 1].
+// The launches are enqueued without a host wait; ctx_sample_end synchronises and checks them.
+
+int ctx_sample_begin(dz_ctx* x, uint32_t first, int n, uint32_t** feed, const float** logits, hipStream_t* s,
+                     Scratch** scratch) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (int rc0 = ctx_usable(x)) return rc0;
+  if (!x->ptk.on) return DZ_ERR_UNSUPPORTED;  // the caller samples on the host instead
+  if (n < 1 || x->pos_host + n > x->m->cfg.max_ctx || n + 1 > x->feed_cap)
+    return set_error(DZ_ERR_TENSOR, "sampled decode: %d tokens from position %d (max_ctx %d)", n, x->pos_host,
+                     x->m->cfg.max_ctx);
+  x->bt.pending = 0;
+  if (int rc = ptk_feed(x, &first, 1)) return rc;
+  const PtkPlan& P = x->ptk.plan;
+  if ((x->ptk.gti + (uint64_t)n + 2) * (uint64_t)P.ppt + 1 >= (1ull << 31)) {
+    const size_t ll_words = (size_t)2 * (P.n_layers + 1) * (size_t)P.off.words;
+    DZ_HIP_CHECK(hipMemsetAsync(P.ll, 0, ll_words * sizeof(u64), x->s));
+    x->ptk.gti = 0;
+  }
+  *feed = reinterpret_cast<uint32_t*>(x->feed);
+  *logits = x->logits;
+  *s = x->s;
+  *scratch = &x->bt.spec;
+  return DZ_OK;
+}
+
+int ctx_sample_launch(dz_ctx* x, int i) {
+  const PtkPlan& P = x->ptk.plan;
+  PtkRun r;
+  r.plan = P;
+  r.plan.logits_all = nullptr;
+  r.feed = x->feed + i;
+  r.n_feed = 1;
+  r.n_tok = 1;
+  r.pos0 = x->pos_host + i;
+  r.tag0 = (unsigned)(1 + x->ptk.gti * (uint64_t)P.ppt);
+  r.want_logits = 1;
+  r.eos = -1;
+  r.err.flag = x->ptk.err;
+  r.err.spin_limit = ptk_spin_limit();
+  r.trace = nullptr;
+  if (int rc = ptk_launch(x, r)) return rc;
+  x->ptk.gti += 1;
+  return DZ_OK;
+}
+
+int ctx_sample_end(dz_ctx* x, int n) {
+  int err[4];
+  DZ_HIP_CHECK(hipMemcpyAsync(err, x->ptk.err, 16, hipMemcpyDeviceToHost, x->s));
+  DZ_HIP_CHECK(hipStreamSynchronize(x->s));
+  if (err[0] || err[3] != 1) {
+    DZ_HIP_CHECK(hipMemset(x->ptk.err, 0, 16));
+    x->poisoned = true;
+    return set_error(DZ_ERR_DEVICE, "token kernel: wait timed out (code %d, phase tag %u, workgroup %d)", err[0],
+                     (unsigned)err[1], err[2]);
+  }
+  x->pos_host += n;
+  int pp[2] = {x->pos_host - 1, x->pos_host};
+  DZ_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos), &pp[0], 4, hipMemcpyHostToDevice));
+  DZ_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(x->st) + offsetof(TokState, pos_next), &pp[1], 4, hipMemcpyHostToDevice));
   return DZ_OK;
 }
 
@@ -1537,7 +1611,7 @@ int dz_ctx_create(dz_model* m, dz_ctx** out) {
   const int64_t qkvd = 2 * (int64_t)c.ssm_k_heads * hd + inner;
   const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
   auto& A = x->allocs;
-  x->feed_cap = c.max_ctx;
+  x->feed_cap = c.max_ctx + 1;  // a sampled run writes the draw after its last token too
   x->n_am = (int)m->lm_head.nrb;
   if ((rc = alloc_t(A, &x->st, 1)) || (rc = alloc_t(A, &x->feed, (size_t)x->feed_cap)) ||
       (rc = alloc_t(A, &x->toklog, (size_t)c.max_ctx + 1)) || (rc = alloc_t(A, &x->emb_row, (size_t)c.hidden)) ||

@@ -109,4 +109,13 @@ namespace dz {
 int ctx_verify_enqueue(dz_ctx* x, const uint32_t* draft, int k);
 // The device rows of a context's pending verify forward (see dz_verify_forward), for the sampler.
 int ctx_verify_view(dz_ctx* x, const float** row0, const float** rows, hipStream_t* s, Scratch** scratch);
+// Sampled decode on the token kernel: ctx_sample_begin feeds `first` and hands out the device feed
+// array, the logits buffer, the stream and a scratch buffer (DZ_ERR_UNSUPPORTED, no error set, when
+// the context runs the graph path); ctx_sample_launch(i) enqueues forward i of feed[i] at position
+// pos + i, logits into the buffer; ctx_sample_end(n) waits, checks every launch and moves the
+// position by n.
+int ctx_sample_begin(dz_ctx* x, uint32_t first, int n, uint32_t** feed, const float** logits, hipStream_t* s,
+                     Scratch** scratch);
+int ctx_sample_launch(dz_ctx* x, int i);
+int ctx_sample_end(dz_ctx* x, int n);
 }  // namespace dz

@@ -26,6 +26,53 @@ static float lcg_next(uint64_t* st) {
   return (float)(uint32_t)((*st >> 40) & 0xFFFFFFu) / (float)0x1000000;
 }
 
+// The draw of sample_top_k_top_p_into (sampling.rs:144-247) on the device, over the row's K best
+// logits in order (spec_topk_merge_kernel: descending, lowest index first among equal values):
+// temperature, softmax over the K, the top-p cut at the first cumulative probability >= top_p,
+// renormalisation, one LcgRng draw r (sampling.rs:14-18, the generator state in device memory) and
+// the first candidate whose cumulative probability reaches r; the chosen id goes to *next.  The
+// operations and their order are the host sampler's (Sampler::top_k_top_p); one thread.
+__global__ __launch_bounds__(64) void sample_draw_kernel(const SpecCand* __restrict__ top, int K, float inv_t,
+                                                          float top_p, uint64_t* __restrict__ rng,
+                                                          uint32_t* __restrict__ next) {
+  if (threadIdx.x != 0) return;
+  float pr[kSpecMaxK];
+  float mx = -INFINITY;
+  for (int j = 0; j < K; ++j) mx = fmaxf(mx, top[j].v * inv_t);
+  for (int j = 0; j < K; ++j) pr[j] = expf(top[j].v * inv_t - mx);
+  float sum = 0.f;
+  for (int j = 0; j < K; ++j) sum += pr[j];
+  const float inv_sum = 1.0f / sum;
+  for (int j = 0; j < K; ++j) pr[j] *= inv_sum;
+  float cum = 0.f;
+  int cutoff = K;
+  for (int j = 0; j < K; ++j) {
+    cum += pr[j];
+    if (cum >= top_p) {
+      cutoff = j + 1;
+      break;
+    }
+  }
+  float new_sum = 0.f;
+  for (int j = 0; j < cutoff; ++j) new_sum += pr[j];
+  const float new_inv = 1.0f / new_sum;
+  for (int j = 0; j < cutoff; ++j) pr[j] *= new_inv;
+  uint64_t st = *rng;
+  st = st * 6364136223846793005ull + 1442695040888963407ull;
+  const float r = (float)(uint32_t)((st >> 40) & 0xFFFFFFu) / (float)0x1000000;
+  *rng = st;
+  float acc = 0.f;
+  int chosen = top[0].i;
+  for (int j = 0; j < cutoff; ++j) {
+    acc += pr[j];
+    if (r <= acc) {
+      chosen = top[j].i;
+      break;
+    }
+  }
+  *next = (uint32_t)chosen;
+}
+
 // argmax_avx2 (simd_exp.rs:551-598): strict >, so the lowest index wins ties.
 static size_t argmax_of(const float* x, size_t n) {
   size_t best = 0;
@@ -217,6 +264,73 @@ using namespace dz;
 extern "C" {
 
 float dz_lcg_next(uint64_t* state) { return state ? lcg_next(state) : 0.f; }
+
+int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* sp, uint64_t* rng_state,
+                     uint32_t* out_tokens) {
+  if (!c || !rng_state || !out_tokens) return set_error(DZ_ERR_MODEL, "null argument");
+  int rc = check_sampling(sp);
+  if (rc) return rc;
+  if (n < 1) return DZ_OK;
+  // temperature <= 0 is the argmax with no draw (sample_top_k_top_p_into's greedy branch)
+  if (sp->temperature <= 0.f) return dz_decode_greedy(c, first_token, n, out_tokens);
+  const int vocab = ctx_config(c)->vocab;
+  if (first_token >= (uint32_t)vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", first_token, vocab);
+  const int K = std::min(sp->top_k, vocab);
+  uint32_t* feed = nullptr;
+  const float* logits = nullptr;
+  hipStream_t st = nullptr;
+  Scratch* scr = nullptr;
+  rc = K <= kSpecMaxK ? ctx_sample_begin(c, first_token, n, &feed, &logits, &st, &scr) : DZ_ERR_UNSUPPORTED;
+  if (rc == DZ_ERR_UNSUPPORTED) {
+    // the graph path, or a top_k beyond the device top-k: each forward's logits to the host and the
+    // reference's sampler there
+    std::vector<float> lg((size_t)vocab);
+    Sampler smp;
+    uint32_t tok = first_token;
+    for (int i = 0; i < n; ++i) {
+      if ((rc = dz_forward_token(c, tok, lg.data(), nullptr))) return rc;
+      tok = smp.top_k_top_p(lg.data(), (size_t)vocab, *sp, rng_state);
+      out_tokens[i] = tok;
+    }
+    return DZ_OK;
+  }
+  if (rc) return rc;
+  // scratch: slice candidates | masses | top-k | total | statistics (unused by mode 0) | generator state
+  const int nsl = spec_slices(vocab);
+  const size_t off_mass = (size_t)nsl * kSpecMaxK * sizeof(SpecCand);
+  const size_t off_top = off_mass + 256 * ((nsl * 4 + 255) / 256);
+  const size_t off_tot = off_top + kSpecMaxK * sizeof(SpecCand);
+  const size_t off_st = off_tot + 256;
+  const size_t off_rng = off_st + 256 * ((sizeof(SpecRowStats) + 255) / 256);
+  if ((rc = scr->reserve(off_rng + 256))) return rc;
+  char* base = static_cast<char*>(scr->ptr);
+  SpecCand* cand_dev = reinterpret_cast<SpecCand*>(base);
+  float* mass_dev = reinterpret_cast<float*>(base + off_mass);
+  SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
+  float* tot_dev = reinterpret_cast<float*>(base + off_tot);
+  SpecRowStats* st_dev = reinterpret_cast<SpecRowStats*>(base + off_st);
+  uint64_t* rng_dev = reinterpret_cast<uint64_t*>(base + off_rng);
+  DZ_HIP_CHECK(hipMemsetAsync(st_dev, 0, sizeof(SpecRowStats), st));
+  DZ_HIP_CHECK(hipMemcpyAsync(rng_dev, rng_state, 8, hipMemcpyHostToDevice, st));
+  const float inv_t = 1.0f / sp->temperature;
+  for (int i = 0; i < n; ++i) {
+    if ((rc = ctx_sample_launch(c, i))) return rc;
+    hipLaunchKernelGGL(spec_topk_slice_kernel, dim3((unsigned)nsl), dim3(256), 0, st, logits, (const float*)nullptr,
+                       vocab, 0, (const SpecRowStats*)st_dev, K, cand_dev, mass_dev);
+    DZ_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), 0, st, (const SpecCand*)cand_dev, nsl, K,
+                       (const float*)mass_dev, top_dev, tot_dev);
+    DZ_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(sample_draw_kernel, dim3(1), dim3(64), 0, st, (const SpecCand*)top_dev, K, inv_t, sp->top_p,
+                       rng_dev, feed + i + 1);
+    DZ_HIP_CHECK(hipGetLastError());
+  }
+  if ((rc = ctx_sample_end(c, n))) return rc;
+  DZ_HIP_CHECK(hipMemcpyAsync(out_tokens, feed + 1, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+  DZ_HIP_CHECK(hipMemcpyAsync(rng_state, rng_dev, 8, hipMemcpyDeviceToHost, st));
+  DZ_HIP_CHECK(hipStreamSynchronize(st));
+  return DZ_OK;
+}
 
 int dz_sample(const float* logits, int n, const dz_sampling* sp, uint64_t* rng_state, uint32_t* out) {
   if (!logits || !rng_state || !out || n < 1) return set_error(DZ_ERR_TENSOR, "sample: bad arguments");

@@ -255,6 +255,19 @@ typedef struct dz_sampling {
 
 /* LcgRng::next_f32 (sampling.rs:14-18); *state is the generator state (seeded e.g. 0xC0FFEE). */
 float dz_lcg_next(uint64_t* state);
+/*
+ * Sampled decode of n tokens: the first forward consumes first_token, each next input is
+ * sample_top_k_top_p_into (sampling.rs:144-247) of the previous logits with *sp and the generator
+ * *rng_state (advanced by one draw per token, as LcgRng::next_f32); out_tokens[i] = the sample
+ * after forward i.  Mirrors the decode loop of Engine::generate_inner (engine.rs:850-862) without
+ * its EOS stop and with penalties off.  On the token kernel the top-k, the softmax over it, the
+ * top-p cut and the draw run on the device between launches, with no host round trip per token
+ * (top_k <= 64; a larger top_k, or the graph path, samples on the host from each forward's logits).
+ * Candidates are ranked by logit, the lowest index first among equal values.  temperature <= 0 is
+ * dz_decode_greedy (no draw).
+ */
+int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* sp, uint64_t* rng_state,
+                     uint32_t* out_tokens);
 /* sample_top_k_top_p_into (sampling.rs:144-247) over logits[n]. */
 int dz_sample(const float* logits, int n, const dz_sampling* params, uint64_t* rng_state, uint32_t* out);
 /* leviathan_check (engine.rs:1791-1819): greedy = argmax(target) == token; else accept iff

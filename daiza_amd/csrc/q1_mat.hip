@@ -423,13 +423,17 @@ static int matvec_impl(dz_mat* const* mats, int n, const float* x_dev, float* co
 
 // The tagged partials of the one-launch product (gemv_fused_kernel).  The buffer starts zeroed and
 // tags grow by one per call; it is cleared again before a tag would wrap.  One buffer serves every
-// stream: each launch waits for the previous one (g_fused_done) when it goes to another stream, so
-// calls run one after another on the device in the order the host made them.
+// stream, and a launch needs its whole grid resident, so calls run one after another on the device
+// in the order the host made them: while every call has come on one stream, the stream orders them
+// and nothing else is enqueued (an event record between launches costs about 1-3 us of device time
+// per call); the first call on another stream waits on the host for the device to drain, and from
+// then on each launch records g_fused_done and a launch on another stream waits for it.
 static Scratch g_tpart;
 static unsigned g_tag = 0;
 static int g_fused_cap = -1;  // workgroups of gemv_fused_kernel resident at once on the device
 static hipEvent_t g_fused_done = nullptr;
 static hipStream_t g_fused_last = nullptr;
+static bool g_fused_multi = false;  // a second stream has been seen: launches record g_fused_done
 static int* g_fused_err = nullptr;  // device word: 1 once a launch's wait gave up (until read)
 
 // Wait bound of the summing threads: DAIZA_GEMV_SPIN=<n> lowers it (0 gives up at once), so that
@@ -501,10 +505,18 @@ static int matvec_fused(dz_mat* const* mats, int n, const float* x_dev, float* c
     a.seg[i].vrow_begin = p.g.seg[i].rb_begin * kRowBlock;
     a.seg[i].rows = mats[i]->d.rows;
   }
-  if (g_fused_last && g_fused_last != s) DZ_HIP_CHECK(hipStreamWaitEvent(s, g_fused_done, 0));
+  if (g_fused_last && g_fused_last != s) {
+    if (g_fused_multi) {
+      DZ_HIP_CHECK(hipStreamWaitEvent(s, g_fused_done, 0));
+    } else {
+      // the earlier launches' stream may since have been destroyed: no event on it, a device drain
+      DZ_HIP_CHECK(hipDeviceSynchronize());
+      g_fused_multi = true;
+    }
+  }
   hipLaunchKernelGGL(gemv_fused_kernel<kGemvWaves>, dim3(p.nwg), dim3(kGemvWaves * 64), shmem, s, a);
   DZ_HIP_CHECK(hipGetLastError());
-  DZ_HIP_CHECK(hipEventRecord(g_fused_done, s));
+  if (g_fused_multi) DZ_HIP_CHECK(hipEventRecord(g_fused_done, s));
   g_fused_last = s;
   return DZ_OK;
 }
@@ -585,9 +597,13 @@ int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumula
 int dz_q1_0_matvec_dev_status(void* stream) {
   int rc = ensure_device();
   if (rc) return rc;
-  DZ_HIP_CHECK(hipStreamSynchronize(stream ? (hipStream_t)stream : lib_stream()));
+  const hipStream_t s = stream ? (hipStream_t)stream : lib_stream();
+  DZ_HIP_CHECK(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> lk(g_mu);
-  if (g_fused_last) DZ_HIP_CHECK(hipEventSynchronize(g_fused_done));
+  if (g_fused_multi)
+    DZ_HIP_CHECK(hipEventSynchronize(g_fused_done));
+  else if (g_fused_last && g_fused_last != s)
+    DZ_HIP_CHECK(hipDeviceSynchronize());
   return fused_check();
 }
 

@@ -97,7 +97,9 @@ int dz_q1_0_matvec_batch(dz_mat* m, const float* x, int n, float* y, int accumul
 /* Same as dz_q1_0_matvec on device pointers, enqueued on `stream` (a hipStream_t, NULL = default),
  * without a host synchronisation.  The token loop uses the fused kernels instead.
  * Calls on different streams run one after another on the device, in the order they were made
- * (the one-launch product shares one buffer of split-K partials).  A launch whose bounded wait for
+ * (the one-launch product shares one buffer of split-K partials and needs its whole grid resident);
+ * the first call that comes on a second stream waits on the host for the device to drain, later
+ * stream changes wait on the device.  A launch whose bounded wait for
  * those partials gives up leaves NaN in the rows it could not form and is reported as
  * DZ_ERR_DEVICE by dz_q1_0_matvec_dev_status (or by the next synchronous dz_q1_0_matvec*). */
 int dz_q1_0_matvec_dev(dz_mat* m, const float* x_dev, float* y_dev, int accumulate, void* stream);

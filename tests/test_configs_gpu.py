@@ -162,6 +162,40 @@ def test_config5_spec_verify_full_vocab_ctx8192(dz, oracle, case):
         assert normwise_rel(lg, olg) < 1e-3 and am == oam
 
 
+@pytest.mark.parametrize("case", ["reject_at_3", "greedy"])
+def test_config5_spec_verify_64_layers(dz, oracle, case):
+    """BASELINE config 5 at the model's own depth: the full 64-layer 27B model (48 Gated DeltaNet +
+    16 attention layers, vocabulary 248320), an N(0,1) cache of 8192 positions on every attention
+    layer and seeded state and conv rings on every DeltaNet layer; k = 8 drafts in one verify forward
+    (the forward bench.py times), Leviathan at T = 0.7 with a rejection, and greedy.  Accept count,
+    bonus token, generator state and every layer's state against the reference's sequential loop
+    (engine.rs:1255-1470, 1791-1866) over the oracle."""
+    cfg = dz.Config.bonsai27b(max_ctx=8192 + 32)
+    L = 8192
+    rng = np.random.default_rng(64)
+    attn = [i for i in range(cfg.n_layers) if (i + 1) % cfg.full_attn_interval == 0]
+    assert len(attn) == 16
+    kv = {i: (rng.standard_normal((cfg.n_head_kv, L, cfg.head_dim), dtype=np.float32),
+              rng.standard_normal((cfg.n_head_kv, L, cfg.head_dim), dtype=np.float32)) for i in attn}
+    dn = {}
+    for i in range(cfg.n_layers):
+        if i not in kv:
+            st = (rng.standard_normal((cfg.ssm_v_heads, cfg.ssm_state, cfg.ssm_state)) * 0.02).astype(np.float32)
+            conv = (rng.standard_normal((4, cfg.qkv_dim)) * 0.1).astype(np.float32)
+            dn[i] = (st, conv, i % 4)
+    assert len(dn) == 48
+
+    def setup(ctx, om, probe):
+        for o in (ctx, om, probe):
+            o.set_pos(L)
+            for i, (k, v) in kv.items():
+                o.set_kv(i, k, v)
+            for i, (st, conv, head) in dn.items():
+                o.set_ssm_state(i, st, conv, head)
+
+    _spec_case(dz, oracle, cfg, SEED + 5, [3, 99], case, setup=setup)
+
+
 def _tie_model(dz, oracle, cfg, seed, prompt):
     """The synthetic model with lm_head row b made a byte copy of the target maximum's row a after
     the prompt, b in another 4096-logit slice than a: an exact tie of the maximum across slices."""

@@ -26,53 +26,6 @@ static float lcg_next(uint64_t* st) {
   return (float)(uint32_t)((*st >> 40) & 0xFFFFFFu) / (float)0x1000000;
 }
 
-// The draw of sample_top_k_top_p_into (sampling.rs:144-247) on the device, over the row's K best
-// logits in order (spec_topk_merge_kernel: descending, lowest index first among equal values):
-// temperature, softmax over the K, the top-p cut at the first cumulative probability >= top_p,
-// renormalisation, one LcgRng draw r (sampling.rs:14-18, the generator state in device memory) and
-// the first candidate whose cumulative probability reaches r; the chosen id goes to *next.  The
-// operations and their order are the host sampler's (Sampler::top_k_top_p); one thread.
-__global__ __launch_bounds__(64) void sample_draw_kernel(const SpecCand* __restrict__ top, int K, float inv_t,
-                                                          float top_p, uint64_t* __restrict__ rng,
-                                                          uint32_t* __restrict__ next) {
-  if (threadIdx.x != 0) return;
-  float pr[kSpecMaxK];
-  float mx = -INFINITY;
-  for (int j = 0; j < K; ++j) mx = fmaxf(mx, top[j].v * inv_t);
-  for (int j = 0; j < K; ++j) pr[j] = expf(top[j].v * inv_t - mx);
-  float sum = 0.f;
-  for (int j = 0; j < K; ++j) sum += pr[j];
-  const float inv_sum = 1.0f / sum;
-  for (int j = 0; j < K; ++j) pr[j] *= inv_sum;
-  float cum = 0.f;
-  int cutoff = K;
-  for (int j = 0; j < K; ++j) {
-    cum += pr[j];
-    if (cum >= top_p) {
-      cutoff = j + 1;
-      break;
-    }
-  }
-  float new_sum = 0.f;
-  for (int j = 0; j < cutoff; ++j) new_sum += pr[j];
-  const float new_inv = 1.0f / new_sum;
-  for (int j = 0; j < cutoff; ++j) pr[j] *= new_inv;
-  uint64_t st = *rng;
-  st = st * 6364136223846793005ull + 1442695040888963407ull;
-  const float r = (float)(uint32_t)((st >> 40) & 0xFFFFFFu) / (float)0x1000000;
-  *rng = st;
-  float acc = 0.f;
-  int chosen = top[0].i;
-  for (int j = 0; j < cutoff; ++j) {
-    acc += pr[j];
-    if (r <= acc) {
-      chosen = top[j].i;
-      break;
-    }
-  }
-  *next = (uint32_t)chosen;
-}
-
 // argmax_avx2 (simd_exp.rs:551-598): strict >, so the lowest index wins ties.
 static size_t argmax_of(const float* x, size_t n) {
   size_t best = 0;
@@ -280,7 +233,9 @@ int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* 
   const float* logits = nullptr;
   hipStream_t st = nullptr;
   Scratch* scr = nullptr;
-  rc = K <= kSpecMaxK ? ctx_sample_begin(c, first_token, n, &feed, &logits, &st, &scr) : DZ_ERR_UNSUPPORTED;
+  const size_t merge_lds = spec_merge_shmem(spec_slices(vocab), K);
+  rc = K <= kSpecMaxK && merge_lds ? ctx_sample_begin(c, first_token, n, &feed, &logits, &st, &scr)
+                                   : DZ_ERR_UNSUPPORTED;
   if (rc == DZ_ERR_UNSUPPORTED) {
     // the graph path, or a top_k beyond the device top-k: each forward's logits to the host and the
     // reference's sampler there
@@ -297,14 +252,14 @@ int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* 
   if (rc) return rc;
   // scratch: slice candidates | masses | top-k | total | statistics (unused by mode 0) | generator state
   const int nsl = spec_slices(vocab);
-  const size_t off_mass = (size_t)nsl * kSpecMaxK * sizeof(SpecCand);
+  const size_t off_mass = (size_t)nsl * kSpecMaxK * sizeof(uint64_t);
   const size_t off_top = off_mass + 256 * ((nsl * 4 + 255) / 256);
   const size_t off_tot = off_top + kSpecMaxK * sizeof(SpecCand);
   const size_t off_st = off_tot + 256;
   const size_t off_rng = off_st + 256 * ((sizeof(SpecRowStats) + 255) / 256);
   if ((rc = scr->reserve(off_rng + 256))) return rc;
   char* base = static_cast<char*>(scr->ptr);
-  SpecCand* cand_dev = reinterpret_cast<SpecCand*>(base);
+  uint64_t* cand_dev = reinterpret_cast<uint64_t*>(base);
   float* mass_dev = reinterpret_cast<float*>(base + off_mass);
   SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
   float* tot_dev = reinterpret_cast<float*>(base + off_tot);
@@ -318,11 +273,8 @@ int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* 
     hipLaunchKernelGGL(spec_topk_slice_kernel, dim3((unsigned)nsl), dim3(256), 0, st, logits, (const float*)nullptr,
                        vocab, 0, (const SpecRowStats*)st_dev, K, cand_dev, mass_dev);
     DZ_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), 0, st, (const SpecCand*)cand_dev, nsl, K,
-                       (const float*)mass_dev, top_dev, tot_dev);
-    DZ_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(sample_draw_kernel, dim3(1), dim3(64), 0, st, (const SpecCand*)top_dev, K, inv_t, sp->top_p,
-                       rng_dev, feed + i + 1);
+    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), merge_lds, st, (const uint64_t*)cand_dev, nsl, K,
+                       (const float*)mass_dev, top_dev, tot_dev, SpecDraw{inv_t, sp->top_p, rng_dev, feed + i + 1});
     DZ_HIP_CHECK(hipGetLastError());
   }
   if ((rc = ctx_sample_end(c, n))) return rc;
@@ -379,8 +331,9 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   if ((rc = dz_ctx_vocab(c, &vocab))) return rc;
   const size_t V = (size_t)vocab;
   const int K = greedy ? 1 : std::min(sp->top_k, vocab);
-  if (K > kSpecMaxK) {
-    // a top-k beyond what the device pass keeps: every row to the host, the sampler of dz_sample
+  if (K > kSpecMaxK || !spec_merge_shmem(spec_slices(vocab), K)) {
+    // a top-k beyond what the device pass keeps (or a vocabulary beyond its merge): every row to the
+    // host, the sampler of dz_sample
     std::vector<float> rows((size_t)(k + 1) * V);
     if ((rc = dz_ctx_logits(c, rows.data()))) return rc;
     if ((rc = dz_verify_forward(c, draft, k, rows.data() + V))) return rc;
@@ -420,7 +373,7 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   const int nsl = spec_slices(vocab);
   const size_t off_tok = greedy ? 0 : (size_t)k * V * 4, off_st = off_tok + 256 * ((k * 4 + 255) / 256);
   const size_t off_cand = off_st + 256 * (((size_t)(k + 1) * sizeof(SpecRowStats) + 255) / 256);
-  const size_t off_mass = off_cand + (size_t)nsl * kSpecMaxK * sizeof(SpecCand);
+  const size_t off_mass = off_cand + (size_t)nsl * kSpecMaxK * sizeof(uint64_t);
   const size_t off_top = off_mass + 256 * ((nsl * 4 + 255) / 256);
   const size_t off_tot = off_top + kSpecMaxK * sizeof(SpecCand);
   const size_t off_part = off_tot + 256;
@@ -429,7 +382,7 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
   float* dl_dev = greedy ? nullptr : reinterpret_cast<float*>(base);
   uint32_t* tok_dev = reinterpret_cast<uint32_t*>(base + off_tok);
   SpecRowStats* st_dev = reinterpret_cast<SpecRowStats*>(base + off_st);
-  SpecCand* cand_dev = reinterpret_cast<SpecCand*>(base + off_cand);
+  uint64_t* cand_dev = reinterpret_cast<uint64_t*>(base + off_cand);
   float* mass_dev = reinterpret_cast<float*>(base + off_mass);
   SpecCand* top_dev = reinterpret_cast<SpecCand*>(base + off_top);
   float* tot_dev = reinterpret_cast<float*>(base + off_tot);
@@ -460,8 +413,9 @@ int dz_spec_verify(dz_ctx* c, const uint32_t* draft, int k, const float* draft_l
                        (const float*)(dl_dev ? dl_dev + (size_t)r * V : nullptr), vocab, mode,
                        (const SpecRowStats*)(st_dev + r), K, cand_dev, mass_dev);
     DZ_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), 0, st, (const SpecCand*)cand_dev, nsl, K,
-                       (const float*)mass_dev, top_dev, tot_dev);
+    hipLaunchKernelGGL(spec_topk_merge_kernel, dim3(1), dim3(256), spec_merge_shmem(nsl, K), st,
+                       (const uint64_t*)cand_dev, nsl, K, (const float*)mass_dev, top_dev, tot_dev,
+                       SpecDraw{0.f, 0.f, nullptr, nullptr});
     DZ_HIP_CHECK(hipGetLastError());
     out.resize((size_t)K);
     DZ_HIP_CHECK(hipMemcpyAsync(out.data(), top_dev, (size_t)K * sizeof(SpecCand), hipMemcpyDeviceToHost, st));

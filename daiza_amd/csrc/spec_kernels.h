@@ -186,77 +186,235 @@ __device__ __forceinline__ float spec_value(const float* t, const float* d, int 
   return fmaxf(p - q, 0.0f);
 }
 
+// Candidates as 64-bit keys whose unsigned order is cand_ahead's: the value's bits mapped to an
+// order-preserving unsigned word (a zero of either sign as +0, which compares equal to -0) in the
+// high half, the complement of the index in the low half (lower index first among equal values).
+// A NaN value gets key 0, below every other key, so it is never taken, as cand_ahead never ranks a
+// NaN ahead; "none" (-inf, 0x7FFFFFFF) is the key below every real candidate.
+__device__ __forceinline__ uint64_t cand_key(float v, int i) {
+  if (v != v) return 0ull;
+  const unsigned u = __float_as_uint(v == 0.f ? 0.f : v);
+  const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(~(unsigned)i);
+}
+constexpr uint64_t kCandNone = ((uint64_t)0x007FFFFFu << 32) | 0x80000000u;  // cand_key(-inf, 0x7FFFFFFF)
+__device__ __forceinline__ SpecCand cand_of(uint64_t k) {
+  const unsigned o = (unsigned)(k >> 32);
+  const unsigned u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+  return SpecCand{__uint_as_float(u), (int)~(unsigned)k};
+}
+
+// The largest key of the wave, in every lane: the 16 lanes of each DPP row (xor 1, xor 2, half-row
+// mirror, row mirror), then the four rows' lanes 0, 16, 32, 48.
+template <int CTRL>
+__device__ __forceinline__ uint64_t key_max_dpp(uint64_t k) {
+  const unsigned lo = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)k, CTRL, 0xF, 0xF, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)(k >> 32), CTRL, 0xF, 0xF, false);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > k ? o : k;
+}
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+  k = key_max_dpp<0xB1>(k);
+  k = key_max_dpp<0x4E>(k);
+  k = key_max_dpp<0x141>(k);
+  k = key_max_dpp<0x140>(k);
+  uint64_t m = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t o = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(unsigned)(k >> 32), 16 * r) << 32) |
+                       (unsigned)__builtin_amdgcn_readlane((int)(unsigned)k, 16 * r);
+    m = o > m ? o : m;
+  }
+  return m;
+}
+
 // Stage 1: grid spec_slices(V), 256 threads.  Slice s of the row (kSpecSlice elements, in LDS) keeps
-// its K best (value, index) in order and, in mode 1, its residual mass.
+// its K best candidates in order (as keys, cand_key) and, in mode 1, its residual mass.  Each wave
+// ranks its quarter of the slice in registers (16 keys per lane): K rounds of a lane's largest key
+// below the previous pick and a wave maximum, with no workgroup barrier; the first wave then merges
+// the four ordered lists by their heads.  Past the row's end the keys are kCandNone, and a list runs
+// out with kCandNone entries.
 __global__ __launch_bounds__(256) void spec_topk_slice_kernel(const float* __restrict__ t, const float* __restrict__ d,
                                                               int V, int mode, const SpecRowStats* __restrict__ st,
-                                                              int K, SpecCand* __restrict__ cand,
+                                                              int K, uint64_t* __restrict__ cand,
                                                               float* __restrict__ mass) {
-  constexpr int NT = 256;
-  __shared__ float sv[NT / 64];
-  __shared__ int si[NT / 64];
+  constexpr int NT = 256, NW = NT / 64, PER = kSpecSlice / NT;
+  __shared__ float sv[NW];
   __shared__ float vals[kSpecSlice];
+  __shared__ uint64_t lst[NW][kSpecMaxK];
   const SpecRowStats s = *st;
   const int i0 = blockIdx.x * kSpecSlice, n = min(V - i0, kSpecSlice);
+  // the thread's PER values requested together (a loop with a run-time bound waits one memory round
+  // trip per value), then added in index order
+  float x[PER];
+  if (mode == 0) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int j = (int)threadIdx.x + NT * q;
+      x[q] = j < n ? t[i0 + j] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int j = (int)threadIdx.x + NT * q;
+      x[q] = j < n ? spec_value(t, d, i0 + j, 1, s) : 0.f;
+    }
+  }
   float m = 0.f;
-  for (int j = threadIdx.x; j < n; j += NT) {
-    const float v = spec_value(t, d, i0 + j, mode, s);
-    vals[j] = v;
-    m += v;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int j = (int)threadIdx.x + NT * q;
+    if (j < n) {
+      vals[j] = x[q];
+      m += x[q];
+    }
   }
   m = block_total<NT>(m, sv);  // (its barriers also publish vals)
   if (threadIdx.x == 0) mass[blockIdx.x] = mode == 1 ? m : 0.f;
-  float pv = INFINITY;
-  int pi = -1;  // the previous pick: candidates must come after it in the order
+  const int lane = (int)(threadIdx.x & 63u), w = (int)(threadIdx.x >> 6);
+  uint64_t key[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int j = w * (kSpecSlice / NW) + 64 * q + lane;
+    key[q] = j < n ? cand_key(vals[j], i0 + j) : kCandNone;
+  }
+  uint64_t prev = ~0ull;  // the previous pick: candidates must come after it
   for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int j = threadIdx.x; j < n; j += NT) {
-      const float v = vals[j];
-      const int i = i0 + j;
-      if (cand_ahead(pv, pi, v, i) && cand_ahead(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    block_best<NT>(bv, bi, sv, si);
-    if (threadIdx.x == 0) cand[(size_t)blockIdx.x * K + k] = SpecCand{bv, bi};
-    pv = bv;
-    pi = bi;
+    uint64_t best = kCandNone;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) best = key[q] < prev && key[q] > best ? key[q] : best;
+    best = wave_max_key(best);
+    if (lane == 0) lst[w][k] = best;
+    prev = best;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  int h = 0;  // lane l < NW: the head of wave l's list
+  for (int k = 0; k < K; ++k) {
+    const uint64_t c = lane < NW && h < K ? lst[lane][h] : kCandNone;
+    const uint64_t best = wave_max_key(c);
+    if (best != kCandNone && c == best) ++h;  // keys are unique within a row (the index is part of it)
+    if (lane == 0) cand[(size_t)blockIdx.x * K + k] = best;
   }
 }
 
+// The draw of sample_top_k_top_p_into (sampling.rs:144-247) after a merge, for the device decode
+// loop: rng null = no draw.
+struct SpecDraw {
+  float inv_t, top_p;
+  uint64_t* rng;  // LcgRng state (sampling.rs:14-18)
+  uint32_t* next; // the chosen id
+};
+
 // Stage 2: one workgroup of 256 threads merges the slices' candidates into the row's K best, in
-// order, and adds the slices' masses in slice order.
-__global__ __launch_bounds__(256) void spec_topk_merge_kernel(const SpecCand* __restrict__ cand, int slices, int K,
+// order (as (value, index) pairs), and adds the slices' masses in slice order.  The keys are staged
+// in LDS (dynamic: slices * K entries); the first wave follows every slice's ordered list by its
+// head (lane l: slices l, l + 64, ...; up to 4 per lane) and takes K rounds of the largest head.
+// With dr.rng set it then draws the next id from the K best logits: temperature, softmax over the
+// K, the top-p cut at the first cumulative probability >= top_p, renormalisation, one LcgRng draw r
+// and the first candidate whose cumulative probability reaches r; the operations and their order
+// are the host sampler's (Sampler::top_k_top_p), each sum taken in candidate order.
+__global__ __launch_bounds__(256) void spec_topk_merge_kernel(const uint64_t* __restrict__ cand, int slices, int K,
                                                               const float* __restrict__ mass, SpecCand* __restrict__ out,
-                                                              float* __restrict__ total) {
-  constexpr int NT = 256;
-  __shared__ float sv[NT / 64];
-  __shared__ int si[NT / 64];
-  const int n = slices * K;
-  float pv = INFINITY;
-  int pi = -1;
+                                                              float* __restrict__ total, const SpecDraw dr) {
+  constexpr int NT = 256, MAXL = 4, U = 8;
+  extern __shared__ uint64_t lc[];
+  const int nc = slices * K;
+  for (int c0 = 0; c0 < nc; c0 += NT * U) {  // U keys per thread in flight at once
+    uint64_t r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + (int)threadIdx.x + NT * u;
+      r[u] = c < nc ? cand[c] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + (int)threadIdx.x + NT * u;
+      if (c < nc) lc[c] = r[u];
+    }
+  }
+  __syncthreads();
+  const int lane = (int)(threadIdx.x & 63u), w = (int)(threadIdx.x >> 6);
+  auto at = [](float x, int j) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j)); };
+  if (w == 1) {  // the masses in slice order, 64 loaded at a time
+    float m = 0.f;
+    for (int s0 = 0; s0 < slices; s0 += 64) {
+      const float x = s0 + lane < slices ? mass[s0 + lane] : 0.f;
+      const int cnt = min(64, slices - s0);
+      for (int j = 0; j < cnt; ++j) m += at(x, j);
+    }
+    if (lane == 0) *total = m;
+  }
+  if (w != 0) return;
+  int h[MAXL] = {0, 0, 0, 0};
+  uint64_t mine = kCandNone;  // lane j < K: candidate j of the result
   for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int c = threadIdx.x; c < n; c += NT) {
-      const SpecCand x = cand[c];
-      if (x.i != 0x7FFFFFFF && cand_ahead(pv, pi, x.v, x.i) && cand_ahead(x.v, x.i, bv, bi)) {
-        bv = x.v;
-        bi = x.i;
+    uint64_t best = kCandNone;
+    int bm = -1;
+#pragma unroll
+    for (int m = 0; m < MAXL; ++m) {
+      const int sl = lane + 64 * m;
+      if (sl < slices && h[m] < K) {
+        const uint64_t c = lc[sl * K + h[m]];
+        if (c > best) {
+          best = c;
+          bm = m;
+        }
       }
     }
-    block_best<NT>(bv, bi, sv, si);
-    if (threadIdx.x == 0) out[k] = SpecCand{bv, bi};
-    pv = bv;
-    pi = bi;
+    const uint64_t top = wave_max_key(best);
+#pragma unroll
+    for (int m = 0; m < MAXL; ++m)
+      if (m == bm && top != kCandNone && best == top) ++h[m];
+    if (lane == 0) out[k] = cand_of(top);
+    if (lane == k) mine = top;
   }
-  if (threadIdx.x == 0) {
-    float m = 0.f;
-    for (int s = 0; s < slices; ++s) m += mass[s];
-    *total = m;
+  if (dr.rng == nullptr) return;
+  const SpecCand c = cand_of(mine);
+  const float sc = lane < K ? c.v * dr.inv_t : -INFINITY;
+  float mx = sc;
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float pr = lane < K ? expf(sc - mx) : 0.f;
+  float sum = 0.f;
+  for (int j = 0; j < K; ++j) sum += at(pr, j);
+  const float inv_sum = 1.0f / sum;
+  pr *= inv_sum;
+  float cum = 0.f;
+  int cutoff = K;
+  for (int j = 0; j < K; ++j) {
+    cum += at(pr, j);
+    if (cum >= dr.top_p) {
+      cutoff = j + 1;
+      break;
+    }
   }
+  float ns = 0.f;
+  for (int j = 0; j < cutoff; ++j) ns += at(pr, j);
+  const float ninv = 1.0f / ns;
+  pr *= ninv;
+  uint64_t rs = *dr.rng;
+  rs = rs * 6364136223846793005ull + 1442695040888963407ull;
+  const float r = (float)(uint32_t)((rs >> 40) & 0xFFFFFFu) / (float)0x1000000;
+  float acc = 0.f;
+  int chosen = __builtin_amdgcn_readlane(c.i, 0);
+  for (int j = 0; j < cutoff; ++j) {
+    acc += at(pr, j);
+    if (r <= acc) {
+      chosen = __builtin_amdgcn_readlane(c.i, j);
+      break;
+    }
+  }
+  if (lane == 0) {
+    *dr.rng = rs;
+    *dr.next = (uint32_t)chosen;
+  }
+}
+
+// LDS bytes of spec_topk_merge_kernel for `slices` slices of K candidates (0 when they do not fit:
+// more than 256 slices, or above 64 KiB).
+__host__ __device__ inline size_t spec_merge_shmem(int slices, int K) {
+  const size_t b = (size_t)slices * (size_t)K * sizeof(uint64_t);
+  return slices > 256 || b > 65536 ? 0 : b;
 }
 
 }  // namespace dz

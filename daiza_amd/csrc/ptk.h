@@ -11,6 +11,14 @@
 // workgroup does all polling; waves 1..7 hold the GEMV weights, requested as soon as the previous
 // GEMV's weights are consumed, so the weight stream overlaps the hand-overs (ptk_kernel.h).
 //
+// Data outside LL words.  The conv ring rows and the KV appends of a token are written by sync waves
+// with agent-scope write-through stores (co_st) and read by other workgroups one token or more later
+// (co_ld).  Each sync wave waits for its stores to complete (s_waitcnt vmcnt(0)) at the start of the
+// next token, before its first publish of that token, and every workgroup's layer-0 input depends on
+// every workgroup's embedding columns: any read of those rows in a later token happens after the
+// stores are visible at the device's coherence point.  The DeltaNet state rows are read and written
+// by the same threads of the same workgroup every token (program order on one CU).
+//
 // Per DeltaNet layer: A in-proj GEMV -> R0 (in-proj partial sums) -> B DeltaNet -> C out-proj GEMV
 // -> R1 (h_mid = h + sum of out-proj partials) -> D gate/up GEMV -> R2 (SwiGLU of the gate/up
 // partials) -> E down GEMV -> R3 (h = h_mid + sum of down partials).  An attention layer replaces

@@ -4,12 +4,15 @@
 // small per-column phases (residual sums, SwiGLU, q/k/v sums, attention chunk merge, token
 // selection), the per-head prologues of the DeltaNet and attention phases, and it stages every GEMV
 // input into LDS.  Waves 1..7 are compute waves: they hold GEMV weights in registers, build the
-// lookup table together with the sync wave, run the table lookups and publish the split-K partials;
-// they never poll.  A wave's vector memory operations complete in issue order (gfx9 counts loads
-// and stores on one vmcnt), so a poll issued behind a weight load waits for that load.  With the
-// roles split, a compute wave requests the next GEMV's weights as soon as the current ones are
-// consumed, and the weight stream overlaps every hand-over, while the sync wave's polls cost one
-// round trip.
+// lookup table together with the sync wave and publish the split-K partials; they never poll.  In
+// the layer GEMV phases the sync wave also runs a share of the table lookups once its input is
+// staged (eight lookup waves, two per SIMD); in the lm_head it stages the next tile instead.  A
+// wave's vector memory operations complete in issue order (gfx9 counts loads and stores on one
+// vmcnt), so a poll issued behind a weight load waits for that load, and the CU returns results in
+// issue order across its waves.  With the roles split, a compute wave requests the next GEMV's
+// weights as soon as the current ones are consumed, and the weight stream overlaps every hand-over;
+// the sync wave issues its next polls only after its workgroup's partial stores (an LDS count it
+// waits on), so that those stores do not queue behind a poll round.
 #pragma once
 #include "ptk.h"
 

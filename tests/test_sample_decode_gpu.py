@@ -85,3 +85,31 @@ def test_decode_sample_graph_path(dz, oracle, monkeypatch):
     got = ctx.decode_sample(11, 16, dz.SamplingParams(0.8, 20, 0.9), rng)
     want, state, _ = _oracle_loop(oracle, om, 11, 16, 0.8, 20, 0.9, 77)
     assert [int(x) for x in got] == want and rng.state.value == state
+
+
+def test_decode_sample_exact_ties(dz, oracle):
+    """An lm_head whose rows 8192..12287 are byte copies of rows 0..4095 (vocabulary 12289, four
+    device slices): every logit of the first slice has an exact twin in the third, so the device
+    top-k must order equal values by lower index, as the oracle's sampler does, for the draws (and
+    the chosen ids) to agree."""
+    from named_tensors import named_tensors
+    cfg = dz.Config.small(n_layers=4, max_ctx=64, vocab=12289)
+    seed = SEED + 7
+    om = oracle.Model(cfg, seed)
+    t = named_tensors(oracle, om, cfg, seed)
+    row = (cfg.hidden // 128) * 18
+    w = t["output.weight"][1].copy()
+    w[8192 * row:12288 * row] = w[0:4096 * row]
+    t["output.weight"] = (dz.GGUF_Q1_0, w)
+    m = dz.Model.from_tensors(cfg, t)
+    ctx = dz.Context(m)
+    assert ctx.token_kernel
+    for k, temp in ((20, 0.7), (64, 1.5)):
+        ctx.reset()
+        o2 = oracle.Model(cfg, seed)
+        o2.q1(3, -1)[0][:] = w  # the oracle's own lm_head buffer, written in place
+        rng = dz.LcgRng(99 + k)
+        got = ctx.decode_sample(3, 24, dz.SamplingParams(temp, k, 0.95), rng)
+        want, state, _ = _oracle_loop(oracle, o2, 3, 24, temp, k, 0.95, 99 + k)
+        assert [int(x) for x in got] == want, k
+        assert rng.state.value == state

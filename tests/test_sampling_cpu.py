@@ -139,3 +139,20 @@ def test_library_sampler_matches_oracle(oracle, dzl, temperature, top_k, top_p):
         if temperature > 0:
             assert dzl.sample_bonus(t, d, params, rl) == oracle.sample_bonus(t, d, temperature, top_k, top_p, ro)
         assert rl.state.value == ro.state.value, trial
+
+
+@pytest.mark.parametrize("top_k", [3, 20, 64])
+def test_library_sampler_exact_ties(oracle, dzl, top_k):
+    """Logits with many exactly equal values straddling the top-k boundary: the library's sampler
+    keeps the k best by value and, among equal values, by lower index, as the oracle and the device
+    top-k do, so the draws and the generator state agree."""
+    rng = np.random.default_rng(5)
+    params = dzl.SamplingParams(0.8, top_k, 0.97)
+    for trial in range(30):
+        n = int(rng.integers(top_k + 1, 3000))
+        t = rng.integers(-3, 4, n).astype(np.float32) * 0.5  # seven distinct values
+        seed = int(rng.integers(0, 2**63))
+        ro, rl = oracle.Rng(seed), dzl.LcgRng(seed)
+        for _ in range(4):
+            assert dzl.sample_top_k_top_p(t, params, rl) == oracle.sample_top_k_top_p(t, 0.8, top_k, 0.97, ro), trial
+        assert rl.state.value == ro.state.value

@@ -8,7 +8,8 @@
 // The vocabulary-wide work (softmax statistics, the draft token's probabilities, top-k candidates of
 // the row or of the residual distribution) runs on the device (spec_kernels.h); the acceptance
 // draws and the final temperature / top-p draw over the k candidates run on the host, in the
-// reference's order.
+// reference's order.  The sampled decode loop (dz_decode_sample) runs on the device: one token-kernel
+// launch per token, then the top-k and the draw, which feeds the next launch.
 #include "runtime.h"
 #include "spec_kernels.h"
 

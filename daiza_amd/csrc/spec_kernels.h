@@ -3,8 +3,9 @@
 // token's probabilities (softmax_pair_single_avx2, Daiza-engine/src/math/simd_exp.rs:656-767) and the
 // target's argmax (argmax_avx2, simd_exp.rs:551-598), and the top-k candidates of a row or of the
 // residual distribution max(0, p - q) with its mass (sample_bonus, Daiza-runtime/src/engine.rs:
-// 1833-1866; residual_max_zero_sum_avx2, simd_exp.rs:605-642).  The host finishes the reference's
-// temperature / top-k / top-p draw (sampling.rs:144-247) on those candidates.
+// 1833-1866; residual_max_zero_sum_avx2, simd_exp.rs:605-642).  For a verify step the host finishes
+// the reference's temperature / top-k / top-p draw (sampling.rs:144-247) on those candidates; the
+// device decode loop (dz_decode_sample) draws on the device, in the merge kernel.
 #pragma once
 #include "common.h"
 

@@ -87,8 +87,8 @@ struct Sampler {
     idx.resize(n);
     std::iota(idx.begin(), idx.end(), 0u);
     // larger value first, the lower index first among equal values: a strict total order, so the k
-    // kept and their order are fixed (the device top-k and the oracle rank the same way; the
-    // reference's select_nth_unstable_by leaves the order of exact ties to its partition steps)
+    // kept and their order are fixed (the device top-k ranks the same way; the reference's
+    // select_nth_unstable_by leaves the order of exact ties to its partition steps)
     auto desc = [&](uint32_t a, uint32_t b) { return scaled[a] > scaled[b] || (scaled[a] == scaled[b] && a < b); };
     std::nth_element(idx.begin(), idx.begin() + (k - 1), idx.end(), desc);
     std::sort(idx.begin(), idx.begin() + k, desc);

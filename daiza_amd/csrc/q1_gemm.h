@@ -16,9 +16,9 @@
 //
 // Layout.  The weights stay in the GEMV layout (common.h): unit (row-block rb, tile t) holds 64
 // rows × 512 columns, each row's 64 sign bytes as four 16-byte chunks, chunk c of row L holding
-// group (L >> 4) ^ c with its bytes permuted by position ^ L.  A workgroup owns row-blocks
-// 4·blockIdx.x .. +3 (one wave each, or two waves each taking two 16-row blocks: gemm_waves) and
-// walks the tiles; in a 16-row block sb of a unit, lane (r, q)
+// group (L >> 4) ^ c with its bytes permuted by position ^ L.  A workgroup owns RB row-blocks
+// RB·blockIdx.x .. +RB-1 (RB = 4: two waves each, taking two 16-row blocks; RB = 8, the wide form
+// only: one wave each, taking all four) and walks the tiles; in a 16-row block sb of a unit, lane (r, q)
 // (r = lane & 15, q = lane >> 4) takes the chunk of row 16·sb + r that holds group q, restores the
 // byte order in registers, and feeds the 32 sign bits of dword j of that group as the A operands
 // of steps 4j .. 4j+3 of v_mfma_f32_16x16x32_f16 (columns 128q + 32j .. +31).  The B operand, token
@@ -307,7 +307,7 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
   s2x = ((sc_bits & 0xFFFFu) * 0x00010001u) ^ 0x80008000u;
 }
 
-// Grid (ceil(nrb / 4), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB, HL) bytes of
+// Grid (ceil(nrb / RB), Np / (16·NB), splits), 64·gemm_waves(NB) threads, gemm_shmem(NB, HL) bytes of
 // LDS.  Workgroup z of a split product takes K tiles [z·tps, min(ntiles, (z+1)·tps)) and writes its
 // partial to y + z·zstride; an unsplit product (gridDim.z = 1) writes
 // y[n][row] = (accumulate ? y : 0) + sig[n] · Σ_k W[row][k] (xh + xm + xl)[n][k] for n < n_tok,
@@ -323,15 +323,16 @@ __device__ __forceinline__ void restore_chunk(const u32x4 v, unsigned sc_bits, u
 // 0..7, so each (step, block) takes two matrix instructions instead of three; lanes r and r + 8 of
 // the first D layout hold the hi and mid sums of token r & 7, lane r of the second its lo sum (all
 // scaled by that token's sig(n, t)), added once after the last tile.
-template <int NB, bool RAW = false, bool HL = false>
-__global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
+template <int NB, bool RAW = false, bool HL = false, int RB = 4>
+__global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : (RB == 4 ? 2 : 1)) void q1_gemm_kernel(const uint8_t* __restrict__ W, int64_t rows, int64_t nrb,
                                                          int ntiles, int tps, const GemmX x, int n_tok,
                                                          float* __restrict__ y, int64_t ldy, int64_t zstride,
                                                          int accumulate) {
   static_assert(!HL || (NB == 1 && RAW), "the paired form is a raw form of one token block");
   constexpr int TOK = 16 * NB;
   constexpr int NT = 64 * gemm_waves(NB);  // threads
-  constexpr int HALVES = gemm_waves(NB) / 4;  // waves per row-block
+  static_assert(RB == 4 || (RB == 8 && NB > 1), "row-blocks per workgroup: 4, or 8 for the wide form");
+  constexpr int HALVES = gemm_waves(NB) / RB;  // waves per row-block
   constexpr int SBW = 4 / HALVES;             // 16-row blocks per wave
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int WV = gemm_waves(NB);
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64 * gemm_waves(NB), NB == 1 ? 4 : 2) void q1_gemm_
 #pragma unroll                         // this workgroup's tiles (the same value in every lane)
   for (int jt = 0; jt < TPW; ++jt) ss_acc[jt] = 0.f;
   const unsigned tid = threadIdx.x, lane = tid & 63u;
-  const int64_t rb = (int64_t)blockIdx.x * 4 + (tid >> 6) / HALVES;
+  const int64_t rb = (int64_t)blockIdx.x * RB + (tid >> 6) / HALVES;
   const int sb0 = (int)((tid >> 6) % HALVES) * SBW;  // first 16-row block of this wave
   const bool live = rb < nrb;
   const int tok0 = (int)blockIdx.y * TOK;

@@ -525,7 +525,7 @@ def main():
         H.hipDeviceSynchronize()
         return 0
     # the same loop with the reference's default sampling (T 0.7, top-k 20, top-p 0.95) drawn on the
-    # device between launches (dz_decode_sample): the rate a non-greedy caller gets
+    # device inside the token kernel (dz_decode_sample): the rate a non-greedy caller gets
     smp = dz.SamplingParams(0.7, 20, 0.95)
     srng = dz.LcgRng(SEED & 0xFFFFFFFF)
     ev = Events(H, 2)

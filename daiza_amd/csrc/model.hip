@@ -84,10 +84,12 @@ struct dz_ctx {
     dz::PtkPlan plan{};
     dz::PtkLayer* layers_d = nullptr;
     int* err = nullptr;           // [4]
+    uint64_t* rng = nullptr;      // the sampled selection's generator state
     float* logits_all = nullptr;  // [chunk][vocab]
     int chunk = 32;
     uint64_t gti = 0;             // index of the next token for tags and parity
-    const void* kfn = nullptr;
+    const void* kfn = nullptr;    // the greedy instance
+    const void* kfn_s = nullptr;  // the sampled instance (null: sampled decode takes the per-token launches)
   } ptk;
   // n-token forward (prefill, speculative verify): activations [cap][width], grown on demand
   struct {
@@ -824,22 +826,9 @@ static int ctx_set_pos_dev(dz_ctx* x, int pos) {
 
 // ---------------------------------------------------------------- persistent token kernel (host)
 
-// Kernel instantiation for a model shape (the template bounds of ptk_kernel): K tiles of hidden (exact), GQA
-// group, row-block slots per compute wave of each GEMV kind, terms per thread of the reducers'
-// residual sums, gate/up items per thread of their SwiGLU sums, rows per thread of their in-projection
-// sums and outputs per workgroup of the attention merge.  Other shapes run on the graph path.
-struct PtkShape {
-  int th, grp, u_in, u_out, u_gu, u_dn, u_lm, qr, mf, mr, mo;
-};
-static bool ptk_fits(const PtkShape& s, const PtkShape& b) {
-  return s.th == b.th && s.grp == b.grp && s.u_in <= b.u_in && s.u_out <= b.u_out && s.u_gu <= b.u_gu &&
-         s.u_dn <= b.u_dn && s.u_lm <= b.u_lm && s.qr <= b.qr && s.mf <= b.mf && s.mr <= b.mr && s.mo <= b.mo;
-}
 static const void* ptk_pick(const PtkShape& s) {
-  if (ptk_fits(s, PtkShape{10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32}))
-    return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32>);
-  if (ptk_fits(s, PtkShape{1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8}))
-    return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8>);
+  if (ptk_fits(s, kPtkShape27b)) return reinterpret_cast<const void*>(ptk_kernel<10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32>);
+  if (ptk_fits(s, kPtkShapeSmall)) return reinterpret_cast<const void*>(ptk_kernel<1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8>);
   return nullptr;
 }
 
@@ -958,7 +947,7 @@ static int ptk_prepare(dz_ctx* x) {
   P.off.qkv = take(std::max<int64_t>(attn_rows, max_rows_in));
   P.off.rec = take((int64_t)c.n_head * gmax * (2 + c.head_dim));
   P.off.ao = take(qdim);
-  P.off.words = std::max<int64_t>(o, al(ld_h + 2 * (int64_t)G));
+  P.off.words = std::max<int64_t>(o, al(ptk_samp_off(ld_h, G) + ptk_samp_words(G)));
   // phases: S, then 9 per DeltaNet layer / 10 per attention layer, then L
   std::vector<PtkLayer> Ls((size_t)c.n_layers);
   const size_t kvsz = (size_t)c.n_head_kv * c.max_ctx * c.head_dim;
@@ -1022,7 +1011,7 @@ static int ptk_prepare(dz_ctx* x) {
   int rc;
   const size_t ll_words = (size_t)2 * (c.n_layers + 1) * (size_t)P.off.words;
   if ((rc = alloc_t(A, &P.ll, ll_words)) || (rc = alloc_t(A, &x->ptk.layers_d, Ls.size())) ||
-      (rc = alloc_t(A, &x->ptk.err, 4)) ||
+      (rc = alloc_t(A, &x->ptk.err, 4)) || (rc = alloc_t(A, &x->ptk.rng, 1)) ||
       (rc = alloc_t(A, &x->ptk.logits_all, (size_t)x->ptk.chunk * c.vocab)))
     return rc;
   DZ_HIP_CHECK(hipMemset(P.ll, 0, ll_words * sizeof(u64)));
@@ -1030,6 +1019,12 @@ static int ptk_prepare(dz_ctx* x) {
   DZ_HIP_CHECK(hipMemcpy(x->ptk.layers_d, Ls.data(), Ls.size() * sizeof(PtkLayer), hipMemcpyHostToDevice));
   P.L = x->ptk.layers_d;
   x->ptk.kfn = kfn;
+  // the sampled instance, where it fits one workgroup per CU as the greedy one does
+  const void* kfn_s = ptk_pick_samp(sh);
+  int occ_s = 0;
+  DZ_HIP_CHECK(hipFuncSetAttribute(kfn_s, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
+  DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_s, kfn_s, kPtkThreads, kPtkLds));
+  x->ptk.kfn_s = occ_s >= 1 ? kfn_s : nullptr;
   x->ptk.gti = 0;
   x->ptk.on = true;
   return DZ_OK;
@@ -1044,11 +1039,13 @@ static int ptk_prepare(dz_ctx* x) {
 static int ptk_launch(dz_ctx* x, PtkRun& r) {
   void* args[] = {&r};
   const PtkPlan& P = x->ptk.plan;
+  const void* kfn = r.samp.k > 0 ? x->ptk.kfn_s : x->ptk.kfn;
+  if (!kfn) return set_error(DZ_ERR_UNSUPPORTED, "token kernel: no sampled instance");
   const char* coop = getenv("DAIZA_PTK_COOP");
   if (coop && coop[0] == '1')
-    DZ_HIP_CHECK(hipLaunchCooperativeKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+    DZ_HIP_CHECK(hipLaunchCooperativeKernel(kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
   else
-    DZ_HIP_CHECK(hipLaunchKernel(x->ptk.kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
+    DZ_HIP_CHECK(hipLaunchKernel(kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));
   return DZ_OK;
 }
 
@@ -1068,7 +1065,10 @@ static int ptk_spin_limit() {
 // and with per_pos every token's logits in ptk.logits_all[i] (n <= ptk.chunk).
 // With eos >= 0 a greedy pick equal to eos ends the launch before that token is forwarded; *n_done
 // (if given) receives the number of tokens forwarded and the position advances by that many.
-static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0, int eos = -1, int* n_done = nullptr) {
+// With smp.k > 0 the tokens past the fed ones (and the pick after the last) are drawn on the device
+// from the previous logits' smp.k best instead of the greedy pick.
+static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0, int eos = -1, int* n_done = nullptr,
+                   const PtkSamp& smp = PtkSamp{}) {
   const PtkPlan& P = x->ptk.plan;
   if (x->pos_host + n > x->m->cfg.max_ctx)
     return set_error(DZ_ERR_TENSOR, "context full: pos %d + %d > max_ctx %d", x->pos_host, n, x->m->cfg.max_ctx);
@@ -1089,6 +1089,7 @@ static int ptk_run(dz_ctx* x, int n, int n_feed, bool per_pos, int feed_off = 0,
   r.tag0 = (unsigned)(1 + x->ptk.gti * (uint64_t)P.ppt);
   r.want_logits = 1;
   r.eos = eos;
+  r.samp = smp;
   r.err.flag = x->ptk.err;
   r.err.spin_limit = ptk_spin_limit();
   // DAIZA_PTK_TRACE=<file>: append per-phase times of every workgroup to <file> (binary: int32
@@ -1188,11 +1189,34 @@ int ctx_sample_launch(dz_ctx* x, int i) {
   r.tag0 = (unsigned)(1 + x->ptk.gti * (uint64_t)P.ppt);
   r.want_logits = 1;
   r.eos = -1;
+  r.samp = PtkSamp{};
   r.err.flag = x->ptk.err;
   r.err.spin_limit = ptk_spin_limit();
   r.trace = nullptr;
   if (int rc = ptk_launch(x, r)) return rc;
   x->ptk.gti += 1;
+  return DZ_OK;
+}
+
+int ctx_sample_decode(dz_ctx* x, uint32_t first, int n, int k, float inv_t, float top_p, uint64_t* rng,
+                      uint32_t* out) {
+  if (!x) return set_error(DZ_ERR_MODEL, "null context");
+  if (int rc0 = ctx_usable(x)) return rc0;
+  if (!x->ptk.on || !x->ptk.kfn_s || x->ptk.plan.G > kPtkFan * kPtkFan || k < 1 || k > kPtkSampMax)
+    return DZ_ERR_UNSUPPORTED;
+  x->bt.pending = 0;
+  const int p0 = x->pos_host;
+  int rc = ptk_feed(x, &first, 1);
+  if (rc) return rc;
+  DZ_HIP_CHECK(hipMemcpyAsync(x->ptk.rng, rng, 8, hipMemcpyHostToDevice, x->s));
+  PtkSamp smp;
+  smp.k = k;
+  smp.inv_t = inv_t;
+  smp.top_p = top_p;
+  smp.rng = x->ptk.rng;
+  if ((rc = ptk_run(x, n, 1, false, 0, -1, nullptr, smp))) return rc;
+  DZ_HIP_CHECK(hipMemcpy(out, x->toklog + p0 + 1, (size_t)n * 4, hipMemcpyDeviceToHost));
+  DZ_HIP_CHECK(hipMemcpy(rng, x->ptk.rng, 8, hipMemcpyDeviceToHost));
   return DZ_OK;
 }
 

@@ -390,6 +390,9 @@ __device__ __forceinline__ float ref_f16_to_f32_dev(unsigned bits) {
   return __builtin_bit_cast(float, out);
 }
 
+// (Not in the translation unit of the sampled token kernel, which includes this header for its
+// device helpers only: the kernel is defined once, with the graph path that launches it.)
+#ifndef DZ_PTK_SAMP_TU
 // One workgroup: pick the next token (host feed first, else argmax of the last logits),
 // bump the position and write its embedding row (forward.rs:212-213).
 __global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) {
@@ -449,6 +452,7 @@ __global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) 
     }
   }
 }
+#endif
 
 // ---------------------------------------------------------------- Gated DeltaNet step
 

@@ -171,7 +171,8 @@ struct PtkPlan {
   const float* rope;           // [max_ctx][rope_dim]
   const PtkLayer* L;
   // LL memory: [2 parities][n_layers + 1 regions][off.words]; region n_layers holds the token-level
-  // words: hemb (nrb_h*64), candv (G), candi (G)
+  // words: hemb (nrb_h*64), candv (G), candi (G), then (from ptk_samp_off) the sampled selection's
+  // lists: G lists of 2K words, kPtkFan merged lists of 2K words, the drawn id (one word)
   u64* ll;
   // state / outputs
   TokState* st;
@@ -181,11 +182,46 @@ struct PtkPlan {
 };
 
 constexpr int kPtkMaxLayers = 128;
+// Sampled selection inside the token kernel: top_k up to kPtkSampMax, merged kPtkFan lists at a time
+// in two levels (so G <= kPtkFan^2 workgroups).
+constexpr int kPtkSampMax = 32;
+constexpr int kPtkFan = 16;
+// Word offsets of the sampled selection's lists within the token region (G workgroups; sizes fixed
+// at kPtkSampMax so that the layout does not depend on the run's top_k).
+__host__ __device__ inline int64_t ptk_samp_off(int64_t ld_h, int G) { return (ld_h + 2 * (int64_t)G + 63) / 64 * 64; }
+__host__ __device__ inline int64_t ptk_samp_words(int G) {
+  return 2 * (int64_t)kPtkSampMax * (G + kPtkFan) + 64;
+}
 // Trace stamps per (token, phase, workgroup): 0 = phase done; in a GEMV phase 1 = first compute
 // wave at the staging barrier, 2 = table built (lookups start), 3 = sync wave done staging; in a
 // DeltaNet phase 2 = inputs polled, 4 = conv inputs in LDS, 5 = conv and SiLU done, 3 = prologue
 // done, 1 = delta-rule waves at the barrier, 6 = delta rule computed, 7 = its stores issued.
 constexpr int kPtkTraceSlots = 8;
+
+// Kernel instantiation for a model shape (the template bounds of ptk_kernel): K tiles of hidden
+// (exact), GQA group, row-block slots per compute wave of each GEMV kind, terms per thread of the
+// reducers' residual sums, gate/up items per thread of their SwiGLU sums, rows per thread of their
+// in-projection sums and outputs per workgroup of the attention merge.  Other shapes run on the
+// graph path.
+struct PtkShape {
+  int th, grp, u_in, u_out, u_gu, u_dn, u_lm, qr, mf, mr, mo;
+};
+constexpr PtkShape kPtkShape27b{10, 6, 2, 1, 4, 2, 3, 12, 3, 2, 32};
+constexpr PtkShape kPtkShapeSmall{1, 2, 1, 1, 1, 1, 3, 4, 1, 1, 8};
+inline bool ptk_fits(const PtkShape& s, const PtkShape& b) {
+  return s.th == b.th && s.grp == b.grp && s.u_in <= b.u_in && s.u_out <= b.u_out && s.u_gu <= b.u_gu &&
+         s.u_dn <= b.u_dn && s.u_lm <= b.u_lm && s.qr <= b.qr && s.mf <= b.mf && s.mr <= b.mr && s.mo <= b.mo;
+}
+// The sampled instance for a shape (ptk_samp.hip), or null.
+const void* ptk_pick_samp(const PtkShape& s);
+
+// Sampled selection: tokens past the fed ones are drawn from the previous logits' k best
+// (temperature 1/inv_t, top_p) with the LcgRng state *rng (device memory); k = 0: the greedy pick.
+struct PtkSamp {
+  int k = 0;
+  float inv_t = 1.f, top_p = 1.f;
+  uint64_t* rng = nullptr;
+};
 
 struct PtkRun {
   PtkPlan plan;                // by value: kernel arguments are read with scalar loads
@@ -198,6 +234,7 @@ struct PtkRun {
   int eos;                     // >= 0: a greedy pick equal to eos ends the launch unforwarded
   PtkErr err;                  // err.flag[3] receives the number of tokens forwarded
   u64* trace;                  // optional [n_tok][ppt][G][kPtkTraceSlots] times (s_memrealtime), else null
+  PtkSamp samp;                // tokens past the fed ones: drawn (samp.k > 0) or the greedy pick
 };
 
 static_assert(sizeof(PtkRun) <= 4096, "kernel arguments are limited to 4 KiB");

@@ -15,6 +15,7 @@
 // waits on), so that those stores do not queue behind a poll round.
 #pragma once
 #include "ptk.h"
+#include "topk.h"
 
 namespace dz {
 
@@ -44,6 +45,7 @@ constexpr int kLdsXs = kLutBytes;                                // staged LUT i
 constexpr int kLdsRed = kLdsXs + kMaxTilesH * kTileCols * 4;     // 64 floats: reductions
 constexpr int kLdsFlag = kLdsRed + 64 * 4;                       // abort flag, trace, hand-off, arrival counts
 constexpr int kLdsAsg = kLdsFlag + 16;                           // 8 x {t, rb0, rb1, lead}: GEMV assignments
+constexpr int kLdsRng = kLdsAsg + 6 * 16;                        // u64: the sampled selection's generator state
 constexpr int kLdsRing = kLdsAsg + 8 * 16;                       // kPtkMaxLayers ints: conv ring bases
 constexpr int kLdsScratch = kLdsRing + kPtkMaxLayers * 4;        // phase scratch
 constexpr int kLdsScratchBytes = 16 * 1024;
@@ -422,12 +424,64 @@ __device__ __forceinline__ int s_pick(const PtkPlan& P, unsigned lane, const u64
   return tok;
 }
 
-__device__ __forceinline__ bool s_select(const PtkPlan& P, const PtkRun& r, int i, int w, unsigned lane, u64* hemb,
-                                         const u64* cand_v, const u64* cand_i, unsigned tag_prev, unsigned tag,
-                                         int pos, int& tok) {
+// Sampled selection (sample_top_k_top_p_into, sampling.rs:144-247, over the previous lm_head's
+// logits): each workgroup's lm_head phase published its samp.k best as an ordered list of keys
+// (cand_key, two LL words each: high half, low half) at `sl`; workgroups [0, nm) merge kPtkFan lists
+// each into the lists behind them, and every workgroup merges those and draws (spec_draw) with its
+// own copy of the generator state (in LDS, kLdsRng), so that all of them draw the same id with no
+// further hand-over.  With `fin` (the pick after a launch's last token) only workgroup 0 draws.
+
+// Polls nl <= kPtkFan ordered lists of K <= kPtkSampMax keys (2K LL words each, contiguous from src)
+// and selects their K best: lane 4j + r holds list j's keys r, r + 4, ... (descending) as its queue.
+__device__ __forceinline__ uint64_t s_lists(const u64* src, int nl, int K, unsigned tag, unsigned lane,
+                                            const PtkErr& e, bool& ok) {
+  constexpr int Q = kPtkSampMax / 4;
+  const int j = (int)(lane >> 2), r0 = (int)(lane & 3u);
+  u64 x[2 * Q];
+  auto addr = [&](int s, unsigned) { return src + (size_t)j * 2 * K + 2 * (r0 + 4 * (s >> 1)) + (s & 1); };
+  auto valid = [&](int s) { return j < nl && r0 + 4 * (s >> 1) < K; };
+  ok = poll<2 * Q>(addr, valid, TagC{tag}, x, e);
+  uint64_t q[Q];
+#pragma unroll
+  for (int i = 0; i < Q; ++i)
+    q[i] = valid(2 * i) ? ((uint64_t)(unsigned)x[2 * i] << 32) | (unsigned)x[2 * i + 1] : kCandNone;
+  return queue_select<Q>(q, K);
+}
+
+__device__ __forceinline__ int s_sample(unsigned char* smem, const PtkPlan& P, const PtkRun& r, int w, unsigned lane,
+                                        u64* sl, unsigned tag, bool fin, bool& ok) {
+  const int K = r.samp.k, G = P.G, nm = (G + kPtkFan - 1) / kPtkFan;
+  u64* merged = sl + 2 * kPtkSampMax * G;
+  ok = true;
+  if (w < nm) {
+    const int l0 = w * kPtkFan;
+    const uint64_t key = s_lists(sl + (size_t)l0 * 2 * K, min(kPtkFan, G - l0), K, tag, lane, r.err, ok);
+    if ((int)lane < K) {
+      ll_st(merged + (size_t)w * 2 * K + 2 * lane, __uint_as_float((unsigned)(key >> 32)), tag);
+      ll_st(merged + (size_t)w * 2 * K + 2 * lane + 1, __uint_as_float((unsigned)key), tag);
+    }
+  }
+  if (fin && w != 0) return 0;
+  bool ok2 = true;
+  const uint64_t key = s_lists(merged, nm, K, tag, lane, r.err, ok2);
+  ok = ok && ok2;
+  uint64_t* rsp = lds_ptr<uint64_t>(smem, kLdsRng);
+  uint64_t rs = *rsp;
+  int tok = spec_draw(key, K, r.samp.inv_t, r.samp.top_p, rs);
+  if (lane == 0) *rsp = rs;
+  if (tok < 0 || tok >= P.vocab) tok = 0;  // a failed wait: token 0
+  return tok;
+}
+
+template <bool SAMP>
+__device__ __forceinline__ bool s_select(unsigned char* smem, const PtkPlan& P, const PtkRun& r, int i, int w,
+                                         unsigned lane, u64* hemb, const u64* cand_v, const u64* cand_i, u64* sl,
+                                         unsigned tag_prev, unsigned tag, int pos, int& tok) {
   bool ok = true;
   if (i < r.n_feed) {
     tok = __builtin_amdgcn_readfirstlane(glb(r.feed)[i]);
+  } else if constexpr (SAMP) {
+    tok = s_sample(smem, P, r, w, lane, sl, tag_prev, false, ok);
   } else {
     tok = s_pick(P, lane, cand_v, cand_i, tag_prev, r.err, ok);
   }
@@ -1092,10 +1146,10 @@ __device__ __forceinline__ bool phase_attn(unsigned char* smem, bool prior, cons
 // weights requested one tile ahead; logits = inv_rms(h) * W (h * output_norm) (forward.rs:332-341).
 // The tile loop is unrolled (NTH bounds the tile count), so that no loaded value is carried around a
 // loop (a phi, resolved with register copies that wait for the loads).
-template <bool SYNC, int NTH, int U_LM, int U>
+template <bool SYNC, bool SAMP, int NTH, int U_LM, int U>
 __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const PtkPlan& P, const PtkRun& r, int i, int w,
                                          unsigned tid, const u64* h_fin, unsigned tag_h, WRegs<U>& cur, u64* cand_v,
-                                         u64* cand_i, unsigned tag) {
+                                         u64* cand_i, u64* sl, unsigned tag) {
   const PtkErr& e = r.err;
   const unsigned lane = tid & 63u, wave = tid >> 6, cw = wave - 1;
   int rb0, rb1;
@@ -1167,6 +1221,28 @@ __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const 
       sv[cw] = bv;
       si[cw] = bi;
     }
+    // sampled selection: the wave's samp.k best logits as an ordered list of keys (LDS, in the
+    // table's space), from each lane's U_LM keys in descending order
+    if constexpr (SAMP) {
+      uint64_t q[U_LM];
+#pragma unroll
+      for (int m = 0; m < U_LM; ++m) {
+        const int rb = rb0 + (int)cw + kCW * m;
+        const int row = rb * kRowBlock + (int)lane;
+        q[m] = rb < rb1 && row < P.vocab ? cand_key(acc[m] * inv, row) : kCandNone;
+      }
+#pragma unroll
+      for (int a = 0; a < U_LM; ++a)
+#pragma unroll
+        for (int b = U_LM - 1; b > a; --b)
+          if (q[b] > q[b - 1]) {
+            const uint64_t t = q[b];
+            q[b] = q[b - 1];
+            q[b - 1] = t;
+          }
+      const uint64_t mine = queue_select<U_LM>(q, r.samp.k);
+      if ((int)lane < r.samp.k) lds_ptr<uint64_t>(smem, 0)[cw * kPtkSampMax + lane] = mine;
+    }
   }
   lds_barrier();
   if (SYNC && tid == 0) {
@@ -1179,6 +1255,22 @@ __device__ __forceinline__ bool phase_lm(unsigned char* smem, bool prior, const 
       }
     ll_st(cand_v + w, bv, tag);
     ll_st(cand_i + w, __int_as_float(bi), tag);
+  }
+  if constexpr (SYNC && SAMP) {
+    // the compute waves' lists merged into the workgroup's list at sl[w]: lane 8j + r holds list j's
+    // keys r, r + 8, ... as its queue
+    constexpr int Q = kPtkSampMax / 8;
+    const int K = r.samp.k, j = (int)(lane >> 3), r0 = (int)(lane & 7u);
+    const uint64_t* lst = lds_ptr<uint64_t>(smem, 0);
+    uint64_t q[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) q[i] = j < kCW && r0 + 8 * i < K ? lst[j * kPtkSampMax + r0 + 8 * i] : kCandNone;
+    const uint64_t mine = queue_select<Q>(q, K);
+    if ((int)lane < K) {
+      u64* d = sl + (size_t)w * 2 * K + 2 * lane;
+      ll_st(d, __uint_as_float((unsigned)(mine >> 32)), tag);
+      ll_st(d + 1, __uint_as_float((unsigned)mine), tag);
+    }
   }
   return true;
 }
@@ -1204,11 +1296,13 @@ __device__ __forceinline__ bool asg_lead(unsigned char* smem, int k) { return ld
 // per workgroup of the chunk merge (all checked on the host).
 #define DZ_PTK_TPARAMS int NTH, int GRP, int U_IN, int U_OUT, int U_GU, int U_DN, int U_LM, int QR, int MF, int MR, int MO
 
-// The token loop of one role: SYNC for wave 0, else for a compute wave.  Both roles walk the same
+// The token loop of one role: SYNC for wave 0, else for a compute wave; SAMP draws the tokens past
+// the fed ones (PtkRun::samp) instead of the greedy pick (a kernel instance of its own, so that the
+// greedy instance carries none of the sampling code).  Both roles walk the same
 // phases and meet at the same barriers (each phase function holds both roles' barriers); a role's
 // registers (the sync wave's poll words, a compute wave's weights) exist only in its own copy.  In a
 // reducer workgroup both roles run the same reducer code.
-template <bool SYNC, DZ_PTK_TPARAMS>
+template <bool SYNC, bool SAMP, DZ_PTK_TPARAMS>
 __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   const PtkPlan P0 = plan_view(r.plan);
   const PtkErr& e = r.err;
@@ -1216,7 +1310,8 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   const bool reducer = w0 >= P0.Gp;
   const PtkOffsets& O = P0.off;
   const int64_t ld_in_h = (int64_t)P0.nrb_h * kRowBlock;
-  const int64_t cand_off = ld_in_h;  // token region: h_emb [ld_in_h], cand_v [G], cand_i [G]
+  const int64_t cand_off = ld_in_h;  // token region: h_emb [ld_in_h], cand_v [G], cand_i [G], sampling lists
+  const int64_t samp_off = ptk_samp_off(ld_in_h, G);
   // a compute wave's weight registers: each GEMV phase's weights from the phase that requested them
   // to the phase that uses them
   constexpr int UW = U_IN > U_OUT ? (U_IN > U_GU ? (U_IN > U_DN ? U_IN : U_DN) : (U_GU > U_DN ? U_GU : U_DN))
@@ -1236,11 +1331,11 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
     const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);
     const int pos = r.pos0 + i;
     u64* tokreg = ll_region(P0, par, P0.n_layers);
-    const u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
+    u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
     int tok = 0;
     if constexpr (SYNC) {
-      ok = s_select(P0, r, i, w0, threadIdx.x, tokreg, prev_tok + cand_off, prev_tok + cand_off + G,
-                    tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos, tok);
+      ok = s_select<SAMP>(smem, P0, r, i, w0, threadIdx.x, tokreg, prev_tok + cand_off, prev_tok + cand_off + G,
+                    prev_tok + samp_off, tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, tb, pos, tok);
       ptk_mark(r, P0, i, 0, w0, threadIdx.x, 0);
     }
     // EOS stop (engine.rs:850-871: a sampled eos_token_id ends the loop before it is forwarded).  Every
@@ -1390,8 +1485,8 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
       tag_h = t0 + k + 4;
     }
     // L: lm_head + argmax candidates (all workgroups)
-    if (!phase_lm<SYNC, NTH, U_LM>(smem, ok, P0, r, i, w0, threadIdx.x, h_in, tag_h, wn, tokreg + cand_off,
-                                   tokreg + cand_off + G, tb + (unsigned)P0.ph_l))
+    if (!phase_lm<SYNC, SAMP, NTH, U_LM>(smem, ok, P0, r, i, w0, threadIdx.x, h_in, tag_h, wn, tokreg + cand_off,
+                                   tokreg + cand_off + G, tokreg + samp_off, tb + (unsigned)P0.ph_l))
       return;
     if constexpr (SYNC) ptk_mark(r, P0, i, P0.ph_l, w0, threadIdx.x, 0);
   }
@@ -1399,8 +1494,23 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   if constexpr (SYNC) {
     if (w0 == 0 && threadIdx.x == 0) __hip_atomic_store(glb(e.flag) + 3, n_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // greedy pick after the last token, published as toklog[pos0 + n_tok] (workgroup 0)
-  if constexpr (SYNC) {
+  // the pick after the last token, published as toklog[pos0 + n_tok]: the greedy pick by workgroup
+  // 0, or the draw, with the merging workgroups, and the generator state after it
+  if constexpr (SYNC && SAMP) {
+    if (!stopped && w0 < (G + kPtkFan - 1) / kPtkFan) {
+      const int i = r.n_tok;
+      const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
+      const int par = (int)((r.tag0 / (unsigned)P0.ppt + (unsigned)i) & 1u);
+      u64* prev_tok = ll_region(P0, par ^ 1, P0.n_layers);
+      bool pk = true;
+      const int tok = s_sample(smem, P0, r, w0, threadIdx.x, prev_tok + samp_off,
+                               tb - (unsigned)P0.ppt + (unsigned)P0.ph_l, true, pk);
+      if (w0 == 0 && threadIdx.x == 0 && pk) {
+        P0.toklog[r.pos0 + r.n_tok] = tok;
+        *glb(r.samp.rng) = *lds_ptr<uint64_t>(smem, kLdsRng);
+      }
+    }
+  } else if constexpr (SYNC) {
     if (w0 == 0 && !stopped) {
       const int i = r.n_tok;
       const unsigned tb = r.tag0 + (unsigned)i * (unsigned)P0.ppt;
@@ -1414,13 +1524,14 @@ __device__ __forceinline__ void ptk_role(const PtkRun& r, unsigned char* smem) {
   }
 }
 
-template <DZ_PTK_TPARAMS>
-__global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
+template <bool SAMP, DZ_PTK_TPARAMS>
+__device__ __forceinline__ void ptk_body(const PtkRun& r) {
   extern __shared__ __align__(16) unsigned char smem[];
   const PtkPlan P = plan_view(r.plan);
   const unsigned tid = threadIdx.x;
   const int w = (int)blockIdx.x, G = P.G;
   if (tid < 4) lds_ptr<int>(smem, kLdsFlag)[tid] = 0;
+  if (SAMP && tid == 0) *lds_ptr<uint64_t>(smem, kLdsRng) = *glb(r.samp.rng);
   if (tid < 2) lds_ptr<int>(smem, kLdsRed)[60 + tid] = 0;
   // this workgroup's GEMV assignments per matrix kind (0/1: in-proj of a DeltaNet/attention layer,
   // 2/3: out-proj, 4: gate/up, 5: down) and the conv ring bases, fixed for the launch
@@ -1444,9 +1555,21 @@ __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
   lds_barrier();
   // one wave-uniform branch into the two roles
   if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0)
-    ptk_role<true, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
+    ptk_role<true, SAMP, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
   else
-    ptk_role<false, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
+    ptk_role<false, SAMP, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r, smem);
+}
+
+// The greedy kernel (instantiated in model.hip) and the sampled one (ptk_samp.hip, a code object of
+// its own: the greedy kernel's place in model.hip's code object, by which the instruction cache maps
+// its hot loops, does not move with it).
+template <DZ_PTK_TPARAMS>
+__global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
+  ptk_body<false, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
+}
+template <DZ_PTK_TPARAMS>
+__global__ __launch_bounds__(kPtkThreads) void ptk_kernel_samp(const PtkRun r) {
+  ptk_body<true, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
 }
 #undef DZ_PTK_TPARAMS
 

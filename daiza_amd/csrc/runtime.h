@@ -118,4 +118,10 @@ int ctx_sample_begin(dz_ctx* x, uint32_t first, int n, uint32_t** feed, const fl
                      Scratch** scratch);
 int ctx_sample_launch(dz_ctx* x, int i);
 int ctx_sample_end(dz_ctx* x, int n);
+// Sampled decode of n tokens in one token-kernel launch: forward 0 takes `first`; the draws (top_k k
+// <= kPtkSampMax, temperature 1/inv_t, top_p) run inside the kernel; out[i] = the draw after forward
+// i, *rng the generator state after the last draw.  DZ_ERR_UNSUPPORTED (no error set) on the graph
+// path, for a k beyond kPtkSampMax, or for a plan of more than kPtkFan^2 workgroups.
+int ctx_sample_decode(dz_ctx* x, uint32_t first, int n, int k, float inv_t, float top_p, uint64_t* rng,
+                      uint32_t* out);
 }  // namespace dz

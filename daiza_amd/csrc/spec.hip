@@ -14,6 +14,7 @@
 #include "spec_kernels.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -233,6 +234,13 @@ int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* 
   const int vocab = ctx_config(c)->vocab;
   if (first_token >= (uint32_t)vocab) return set_error(DZ_ERR_TENSOR, "token id %u >= vocab %d", first_token, vocab);
   const int K = std::min(sp->top_k, vocab);
+  // one token-kernel launch that draws inside the kernel (DAIZA_PTK_SAMPLE=0: a launch per token
+  // with the top-k and the draw in kernels of their own between the launches)
+  const char* ev = getenv("DAIZA_PTK_SAMPLE");
+  if (!(ev && ev[0] == '0')) {
+    rc = ctx_sample_decode(c, first_token, n, K, 1.0f / sp->temperature, sp->top_p, rng_state, out_tokens);
+    if (rc != DZ_ERR_UNSUPPORTED) return rc;
+  }
   uint32_t* feed = nullptr;
   const float* logits = nullptr;
   hipStream_t st = nullptr;

@@ -7,7 +7,7 @@
 // the reference's temperature / top-k / top-p draw (sampling.rs:144-247) on those candidates; the
 // device decode loop (dz_decode_sample) draws on the device, in the merge kernel.
 #pragma once
-#include "common.h"
+#include "topk.h"
 
 namespace dz {
 
@@ -16,11 +16,6 @@ struct SpecRowStats {
   float p, q;                    // softmax(target)[token], softmax(draft)[token]
   int argmax;                    // first maximum of the target
   int pad;
-};
-
-struct SpecCand {
-  float v;
-  int i;
 };
 
 // (v, i) is ahead of (w, j) in the order "larger value first, then lower index".
@@ -187,48 +182,6 @@ __device__ __forceinline__ float spec_value(const float* t, const float* d, int 
   return fmaxf(p - q, 0.0f);
 }
 
-// Candidates as 64-bit keys whose unsigned order is cand_ahead's: the value's bits mapped to an
-// order-preserving unsigned word (a zero of either sign as +0, which compares equal to -0) in the
-// high half, the complement of the index in the low half (lower index first among equal values).
-// A NaN value gets key 0, below every other key, so it is never taken, as cand_ahead never ranks a
-// NaN ahead; "none" (-inf, 0x7FFFFFFF) is the key below every real candidate.
-__device__ __forceinline__ uint64_t cand_key(float v, int i) {
-  if (v != v) return 0ull;
-  const unsigned u = __float_as_uint(v == 0.f ? 0.f : v);
-  const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)o << 32) | (uint64_t)(~(unsigned)i);
-}
-constexpr uint64_t kCandNone = ((uint64_t)0x007FFFFFu << 32) | 0x80000000u;  // cand_key(-inf, 0x7FFFFFFF)
-__device__ __forceinline__ SpecCand cand_of(uint64_t k) {
-  const unsigned o = (unsigned)(k >> 32);
-  const unsigned u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
-  return SpecCand{__uint_as_float(u), (int)~(unsigned)k};
-}
-
-// The largest key of the wave, in every lane: the 16 lanes of each DPP row (xor 1, xor 2, half-row
-// mirror, row mirror), then the four rows' lanes 0, 16, 32, 48.
-template <int CTRL>
-__device__ __forceinline__ uint64_t key_max_dpp(uint64_t k) {
-  const unsigned lo = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)k, CTRL, 0xF, 0xF, false);
-  const unsigned hi = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)(k >> 32), CTRL, 0xF, 0xF, false);
-  const uint64_t o = ((uint64_t)hi << 32) | lo;
-  return o > k ? o : k;
-}
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-  k = key_max_dpp<0xB1>(k);
-  k = key_max_dpp<0x4E>(k);
-  k = key_max_dpp<0x141>(k);
-  k = key_max_dpp<0x140>(k);
-  uint64_t m = 0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const uint64_t o = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(unsigned)(k >> 32), 16 * r) << 32) |
-                       (unsigned)__builtin_amdgcn_readlane((int)(unsigned)k, 16 * r);
-    m = o > m ? o : m;
-  }
-  return m;
-}
-
 // Stage 1: grid spec_slices(V), 256 threads.  Slice s of the row (kSpecSlice elements, in LDS) keeps
 // its K best candidates in order (as keys, cand_key) and, in mode 1, its residual mass.  Each wave
 // ranks its quarter of the slice in registers (16 keys per lane): K rounds of a lane's largest key
@@ -311,10 +264,8 @@ struct SpecDraw {
 // order (as (value, index) pairs), and adds the slices' masses in slice order.  The keys are staged
 // in LDS (dynamic: slices * K entries); the first wave follows every slice's ordered list by its
 // head (lane l: slices l, l + 64, ...; up to 4 per lane) and takes K rounds of the largest head.
-// With dr.rng set it then draws the next id from the K best logits: temperature, softmax over the
-// K, the top-p cut at the first cumulative probability >= top_p, renormalisation, one LcgRng draw r
-// and the first candidate whose cumulative probability reaches r; the operations and their order
-// are the host sampler's (Sampler::top_k_top_p), each sum taken in candidate order.
+// With dr.rng set it then draws the next id from the K best logits (spec_draw: temperature, softmax
+// over the K, top-p cut, one LcgRng draw).
 __global__ __launch_bounds__(256) void spec_topk_merge_kernel(const uint64_t* __restrict__ cand, int slices, int K,
                                                               const float* __restrict__ mass, SpecCand* __restrict__ out,
                                                               float* __restrict__ total, const SpecDraw dr) {
@@ -371,40 +322,8 @@ __global__ __launch_bounds__(256) void spec_topk_merge_kernel(const uint64_t* __
     if (lane == k) mine = top;
   }
   if (dr.rng == nullptr) return;
-  const SpecCand c = cand_of(mine);
-  const float sc = lane < K ? c.v * dr.inv_t : -INFINITY;
-  float mx = sc;
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  float pr = lane < K ? expf(sc - mx) : 0.f;
-  float sum = 0.f;
-  for (int j = 0; j < K; ++j) sum += at(pr, j);
-  const float inv_sum = 1.0f / sum;
-  pr *= inv_sum;
-  float cum = 0.f;
-  int cutoff = K;
-  for (int j = 0; j < K; ++j) {
-    cum += at(pr, j);
-    if (cum >= dr.top_p) {
-      cutoff = j + 1;
-      break;
-    }
-  }
-  float ns = 0.f;
-  for (int j = 0; j < cutoff; ++j) ns += at(pr, j);
-  const float ninv = 1.0f / ns;
-  pr *= ninv;
   uint64_t rs = *dr.rng;
-  rs = rs * 6364136223846793005ull + 1442695040888963407ull;
-  const float r = (float)(uint32_t)((rs >> 40) & 0xFFFFFFu) / (float)0x1000000;
-  float acc = 0.f;
-  int chosen = __builtin_amdgcn_readlane(c.i, 0);
-  for (int j = 0; j < cutoff; ++j) {
-    acc += at(pr, j);
-    if (r <= acc) {
-      chosen = __builtin_amdgcn_readlane(c.i, j);
-      break;
-    }
-  }
+  const int chosen = spec_draw(mine, K, dr.inv_t, dr.top_p, rs);
   if (lane == 0) {
     *dr.rng = rs;
     *dr.next = (uint32_t)chosen;

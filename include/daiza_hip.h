@@ -263,10 +263,11 @@ float dz_lcg_next(uint64_t* state);
  * *rng_state (advanced by one draw per token, as LcgRng::next_f32); out_tokens[i] = the sample
  * after forward i.  Mirrors the decode loop of Engine::generate_inner (engine.rs:850-862) without
  * its EOS stop and with penalties off.  On the token kernel the top-k, the softmax over it, the
- * top-p cut and the draw run on the device between launches, with no host round trip per token
- * (top_k <= 64; a larger top_k, or the graph path, samples on the host from each forward's logits).
- * Candidates are ranked by logit, the lowest index first among equal values.  temperature <= 0 is
- * dz_decode_greedy (no draw).
+ * top-p cut and the draw run on the device with no host round trip per token: for top_k <= 32
+ * inside the one token-kernel launch of the call, for top_k <= 64 in kernels between per-token
+ * launches (also with DAIZA_PTK_SAMPLE=0); a larger top_k, or the graph path, samples on the host
+ * from each forward's logits.  Candidates are ranked by logit, the lowest index first among equal
+ * values.  temperature <= 0 is dz_decode_greedy (no draw).
  */
 int dz_decode_sample(dz_ctx* c, uint32_t first_token, int n, const dz_sampling* sp, uint64_t* rng_state,
                      uint32_t* out_tokens);

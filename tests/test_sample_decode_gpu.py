@@ -3,10 +3,12 @@ sample_top_k_top_p_into (Daiza-engine/src/math/sampling.rs:144-247) and its LcgR
 (sampling.rs:9-19), on the GPU against the same loop over the oracle (oracle forward, oracle
 sampler): the same tokens draw for draw and the same generator state at the end.
 
-The token kernel runs the top-k over the vocabulary, the softmax over the k, the top-p cut and the
-draw on the device between launches (vocabulary 248320: 61 slices of the device top-k); a top_k
-above 64 and the graph path sample on the host from each forward's logits.  Bar: identical tokens
-and generator state; the logits after the loop within 1e-3 normwise.
+For a top_k up to 32 the draws run inside the one token-kernel launch of the loop (per-workgroup
+top-k lists from the lm_head phase, merged in two levels at the next token's start); a top_k up to 64
+(or DAIZA_PTK_SAMPLE=0) takes a launch per token with the top-k over the vocabulary (vocabulary
+248320: 61 slices), the softmax over the k, the top-p cut and the draw in kernels between the
+launches; a top_k above 64 and the graph path sample on the host from each forward's logits.  Bar:
+identical tokens and generator state; the logits after the loop within 1e-3 normwise.
 """
 import os
 
@@ -36,8 +38,8 @@ def big_vocab(dz):
     return cfg, dz.Model.synthetic(cfg, SEED)
 
 
-@pytest.mark.parametrize("t,k,p,n", [(0.7, 20, 0.95, 64), (1.3, 64, 0.9, 24), (0.5, 1, 0.95, 8),
-                                     (0.9, 100, 0.8, 12)])
+@pytest.mark.parametrize("t,k,p,n", [(0.7, 20, 0.95, 64), (0.8, 32, 0.9, 16), (1.3, 64, 0.9, 24),
+                                     (0.5, 1, 0.95, 8), (0.9, 100, 0.8, 12)])
 def test_decode_sample_matches_oracle_loop(dz, oracle, big_vocab, t, k, p, n):
     cfg, m = big_vocab
     ctx = dz.Context(m)
@@ -51,6 +53,32 @@ def test_decode_sample_matches_oracle_loop(dz, oracle, big_vocab, t, k, p, n):
     assert rng.state.value == state
     assert ctx.pos == n
     assert normwise_rel(ctx.logits(), lg) < 1e-3
+
+
+def test_decode_sample_in_kernel_matches_launch_per_token(dz, big_vocab, monkeypatch):
+    """The in-kernel draws against the launch-per-token path (DAIZA_PTK_SAMPLE=0) on two contexts of
+    one model: the same tokens and generator states over a sampled call, a greedy call and a second
+    sampled call with other parameters, which continue each other's positions and generator."""
+    cfg, m = big_vocab
+    a, b = dz.Context(m), dz.Context(m)
+    ra, rb = dz.LcgRng(1234), dz.LcgRng(1234)
+
+    def both(fn):
+        x = fn(a, ra)
+        monkeypatch.setenv("DAIZA_PTK_SAMPLE", "0")
+        try:
+            y = fn(b, rb)
+        finally:
+            monkeypatch.delenv("DAIZA_PTK_SAMPLE")
+        assert [int(v) for v in x] == [int(v) for v in y]
+        assert ra.state.value == rb.state.value
+        return x
+
+    t1 = both(lambda c, r: c.decode_sample(5, 12, dz.SamplingParams(0.9, 32, 0.9), r))
+    t2 = both(lambda c, r: c.decode_greedy(int(t1[-1]), 3))
+    both(lambda c, r: c.decode_sample(int(t2[-1]), 9, dz.SamplingParams(1.1, 7, 0.8), r))
+    assert a.pos == b.pos == 24
+    assert normwise_rel(a.logits(), b.logits()) < 1e-6
 
 
 def test_decode_sample_greedy_temperature_and_errors(dz, big_vocab):

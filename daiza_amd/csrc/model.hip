@@ -90,6 +90,7 @@ struct dz_ctx {
     uint64_t gti = 0;             // index of the next token for tags and parity
     const void* kfn = nullptr;    // the greedy instance
     const void* kfn_s = nullptr;  // the sampled instance (null: sampled decode takes the per-token launches)
+    const void* kfn_t[2] = {nullptr, nullptr};  // the traced greedy / sampled instances (DAIZA_PTK_TRACE)
   } ptk;
   // n-token forward (prefill, speculative verify): activations [cap][width], grown on demand
   struct {
@@ -1025,6 +1026,10 @@ static int ptk_prepare(dz_ctx* x) {
   DZ_HIP_CHECK(hipFuncSetAttribute(kfn_s, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
   DZ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_s, kfn_s, kPtkThreads, kPtkLds));
   x->ptk.kfn_s = occ_s >= 1 ? kfn_s : nullptr;
+  for (int t = 0; t < 2; ++t) {
+    x->ptk.kfn_t[t] = ptk_pick_trace(sh, t == 1);
+    DZ_HIP_CHECK(hipFuncSetAttribute(x->ptk.kfn_t[t], hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPtkLds));
+  }
   x->ptk.gti = 0;
   x->ptk.on = true;
   return DZ_OK;
@@ -1039,8 +1044,8 @@ static int ptk_prepare(dz_ctx* x) {
 static int ptk_launch(dz_ctx* x, PtkRun& r) {
   void* args[] = {&r};
   const PtkPlan& P = x->ptk.plan;
-  const void* kfn = r.samp.k > 0 ? x->ptk.kfn_s : x->ptk.kfn;
-  if (!kfn) return set_error(DZ_ERR_UNSUPPORTED, "token kernel: no sampled instance");
+  const void* kfn = r.trace ? x->ptk.kfn_t[r.samp.k > 0] : r.samp.k > 0 ? x->ptk.kfn_s : x->ptk.kfn;
+  if (!kfn) return set_error(DZ_ERR_UNSUPPORTED, "token kernel: no instance for this run");
   const char* coop = getenv("DAIZA_PTK_COOP");
   if (coop && coop[0] == '1')
     DZ_HIP_CHECK(hipLaunchCooperativeKernel(kfn, dim3((unsigned)P.G), dim3(kPtkThreads), args, kPtkLds, x->s));

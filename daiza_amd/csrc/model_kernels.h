@@ -390,9 +390,9 @@ __device__ __forceinline__ float ref_f16_to_f32_dev(unsigned bits) {
   return __builtin_bit_cast(float, out);
 }
 
-// (Not in the translation unit of the sampled token kernel, which includes this header for its
-// device helpers only: the kernel is defined once, with the graph path that launches it.)
-#ifndef DZ_PTK_SAMP_TU
+// (Not in the translation units that hold only token-kernel instances and include this header for
+// its device helpers: the kernel is defined once, with the graph path that launches it.)
+#ifndef DZ_PTK_ONLY_TU
 // One workgroup: pick the next token (host feed first, else argmax of the last logits),
 // bump the position and write its embedding row (forward.rs:212-213).
 __global__ __launch_bounds__(1024) void select_token_kernel(const SelectArgs a) {

@@ -214,6 +214,8 @@ inline bool ptk_fits(const PtkShape& s, const PtkShape& b) {
 }
 // The sampled instance for a shape (ptk_samp.hip), or null.
 const void* ptk_pick_samp(const PtkShape& s);
+// The traced instance, greedy or sampled, for a shape (ptk_trace.hip), or null.
+const void* ptk_pick_trace(const PtkShape& s, bool samp);
 
 // Sampled selection: tokens past the fed ones are drawn from the previous logits' k best
 // (temperature 1/inv_t, top_p) with the LcgRng state *rng (device memory); k = 0: the greedy pick.

@@ -19,6 +19,17 @@
 
 namespace dz {
 
+// The trace stamps (DAIZA_PTK_TRACE) exist only in the kernels of a translation unit that defines
+// DZ_PTK_TRACE before it includes this header (ptk_trace.hip: ptk_kernel_trace, ptk_kernel_samp_trace).
+// The production kernels carry none of their code.  The kernel's code is several times the size of
+// the instruction cache, and the stamps' branches, skipped but interleaved with the hot code, cost 1%
+// of a token.
+#ifdef DZ_PTK_TRACE
+constexpr bool kPtkTraced = true;
+#else
+constexpr bool kPtkTraced = false;
+#endif
+
 constexpr int kCW = kPtkWaves - 1;  // compute waves per workgroup
 constexpr int kLW = kPtkWaves;      // lookup waves of a layer GEMV phase (the sync wave included)
 
@@ -283,8 +294,10 @@ struct SrcGatedYLL {
 // Trace stamp `slot` of phase `ph` of token i, written by thread `by` (tracing runs only).
 __device__ __forceinline__ void ptk_mark(const PtkRun& r, const PtkPlan& P, int i, int ph, int w, unsigned tid,
                                          unsigned by, int slot = 0) {
-  if (r.trace && tid == by)
-    glb(r.trace)[(((size_t)i * P.ppt + ph) * P.G + w) * kPtkTraceSlots + slot] = __builtin_amdgcn_s_memrealtime();
+  if constexpr (kPtkTraced) {
+    if (r.trace && tid == by)
+      glb(r.trace)[(((size_t)i * P.ppt + ph) * P.G + w) * kPtkTraceSlots + slot] = __builtin_amdgcn_s_memrealtime();
+  }
 }
 struct TraceAt;
 __device__ __forceinline__ bool r_trace_wait(const TraceAt& tr);
@@ -297,7 +310,7 @@ struct TraceAt {  // where a GEMV phase stamps its sub-points
   }
   // slot 0 from the last compute wave to finish its stores (an LDS arrival count, tracing runs only)
   __device__ __forceinline__ void last_wave(unsigned char* smem, unsigned tid) const {
-    if (!r->trace) return;
+    if (!kPtkTraced || !r->trace) return;
     if ((tid & 63u) == 0) {
       int* cnt = reinterpret_cast<int*>(smem + kLdsFlag + 4);
       const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -305,7 +318,7 @@ struct TraceAt {  // where a GEMV phase stamps its sub-points
     }
   }
 };
-__device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return tr.r->trace != nullptr; }
+__device__ __forceinline__ bool r_trace_wait(const TraceAt& tr) { return kPtkTraced && tr.r->trace != nullptr; }
 
 // One split-K GEMV phase, run by both roles (SYNC: the sync wave, else a compute wave) with the same
 // barriers (prior: this thread's previous phases succeeded).  The sync wave stages the tile's inputs and the
@@ -1562,7 +1575,17 @@ __device__ __forceinline__ void ptk_body(const PtkRun& r) {
 
 // The greedy kernel (instantiated in model.hip) and the sampled one (ptk_samp.hip, a code object of
 // its own: the greedy kernel's place in model.hip's code object, by which the instruction cache maps
-// its hot loops, does not move with it).
+// its hot loops, does not move with it); with DZ_PTK_TRACE, the same two with the trace stamps.
+#ifdef DZ_PTK_TRACE
+template <DZ_PTK_TPARAMS>
+__global__ __launch_bounds__(kPtkThreads) void ptk_kernel_trace(const PtkRun r) {
+  ptk_body<false, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
+}
+template <DZ_PTK_TPARAMS>
+__global__ __launch_bounds__(kPtkThreads) void ptk_kernel_samp_trace(const PtkRun r) {
+  ptk_body<true, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
+}
+#else
 template <DZ_PTK_TPARAMS>
 __global__ __launch_bounds__(kPtkThreads) void ptk_kernel(const PtkRun r) {
   ptk_body<false, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
@@ -1571,6 +1594,7 @@ template <DZ_PTK_TPARAMS>
 __global__ __launch_bounds__(kPtkThreads) void ptk_kernel_samp(const PtkRun r) {
   ptk_body<true, NTH, GRP, U_IN, U_OUT, U_GU, U_DN, U_LM, QR, MF, MR, MO>(r);
 }
+#endif
 #undef DZ_PTK_TPARAMS
 
 }  // namespace dz

@@ -1,6 +1,6 @@
 // ptk_samp.hip — the sampled instances of the persistent token kernel (ptk_kernel_samp: the token
 // kernel with the draws of dz_decode_sample inside it), in a code object of their own.
-#define DZ_PTK_SAMP_TU
+#define DZ_PTK_ONLY_TU
 #include "ptk_kernel.h"
 
 namespace dz {

@@ -211,3 +211,44 @@ def test_token_kernel_and_graph_agree(dz, monkeypatch):
     for i in range(len(ids)):
         assert normwise_rel(out["1"][i], out["0"][i]) < 1e-5, i
     assert list(out["1g"]) == list(out["0g"])
+
+
+def test_traced_token_kernel_matches(dz, tmp_path, monkeypatch):
+    """DAIZA_PTK_TRACE runs the traced instances (ptk_trace.hip), a kernel of their own beside the
+    production one: the same greedy and sampled tokens and generator state, the same logits, and a
+    trace file of n_tok x phases x workgroups x slots stamps: every workgroup stamps each token's
+    selection (phase 0) and lm_head (the last phase), in that order, token after token."""
+    cfg = dz.Config.small(n_layers=8, max_ctx=96)
+    m = dz.Model.synthetic(cfg, SEED + 11)
+    a, b = dz.Context(m), dz.Context(m)
+    assert a.token_kernel and b.token_kernel
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 12).astype(np.uint32)
+    first = int(np.argmax(a.forward_batch(prompt)))
+    b.forward_batch(prompt)
+    path = tmp_path / "trace.bin"
+    ra, rb = dz.LcgRng(31), dz.LcgRng(31)
+    sp = dz.SamplingParams(0.9, 20, 0.9)
+    ga = a.decode_greedy(first, 6)
+    sa = a.decode_sample(int(ga[-1]), 5, sp, ra)
+    monkeypatch.setenv("DAIZA_PTK_TRACE", str(path))
+    try:
+        gb = b.decode_greedy(first, 6)
+        sb = b.decode_sample(int(gb[-1]), 5, sp, rb)
+    finally:
+        monkeypatch.delenv("DAIZA_PTK_TRACE")
+    assert list(ga) == list(gb) and list(sa) == list(sb)
+    assert ra.state.value == rb.state.value
+    assert normwise_rel(a.logits(), b.logits()) < 1e-6
+    data = path.read_bytes()
+    off = 0
+    for n_expect in (6, 5):
+        n, ppt, G, S = np.frombuffer(data[off:off + 16], np.int32)
+        assert n == n_expect and S == 8
+        off += 16
+        t = np.frombuffer(data[off:off + 8 * n * ppt * G * S], np.uint64).reshape(n, ppt, G, S)
+        off += 8 * n * ppt * G * S
+        ends = np.stack([t[:, 0, :, 0], t[:, ppt - 1, :, 0]], axis=1).astype(np.int64)  # [token][S, LM][wg]
+        assert (ends > 0).all()
+        seq = ends.transpose(2, 0, 1).reshape(G, 2 * n)  # per workgroup: S0, LM0, S1, LM1, ...
+        assert (np.diff(seq, axis=1) > 0).all()
+    assert off == len(data)

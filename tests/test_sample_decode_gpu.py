@@ -39,7 +39,8 @@ def big_vocab(dz):
 
 
 @pytest.mark.parametrize("t,k,p,n", [(0.7, 20, 0.95, 64), (0.8, 32, 0.9, 16), (1.3, 64, 0.9, 24),
-                                     (0.5, 1, 0.95, 8), (0.9, 100, 0.8, 12)])
+                                     (0.5, 1, 0.95, 8), (0.9, 100, 0.8, 12), (0.7, 20, 0.95, 1),
+                                     (2.0, 32, 1.0, 12), (0.05, 7, 0.5, 10)])
 def test_decode_sample_matches_oracle_loop(dz, oracle, big_vocab, t, k, p, n):
     cfg, m = big_vocab
     ctx = dz.Context(m)

@@ -215,9 +215,11 @@ struct GatedYSrc {
 };
 
 // Positions per chunk of the graph path's attention at context ctx with at most gmax chunks per kv
-// head: at least 64, four waves of one 16-position tile each.
+// head: whole 16-position tiles (so that no chunk ends in a tile of one position), at least 64 (four
+// waves of one tile each).
 __device__ __forceinline__ int attn_chunk(int ctx, int gmax) {
-  const int c = (ctx + gmax - 1) / gmax;
+  int c = (ctx + gmax - 1) / gmax;
+  c = (c + 15) / 16 * 16;
   return c < 64 ? 64 : c;
 }
 
